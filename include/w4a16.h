@@ -1,0 +1,154 @@
+/*
+ * libw4a16 -- C ABI of the MI355X (gfx950) W4A16 fused dequant-GEMM.
+ *
+ * Plain C types only: device pointers as `void*` / `int32_t*`, sizes as int64_t,
+ * the HIP stream as `void*` (a hipStream_t; NULL = the legacy default stream).
+ * All device pointers belong to the calling thread's current HIP device and are
+ * owned by the caller; the library allocates nothing and keeps no global mutable
+ * state apart from a per-device cache of the CU count.  Launches are
+ * asynchronous on `stream`.
+ *
+ * Return value: 0 (W4A16_OK) on success, a negative w4a16_status for an invalid
+ * argument (detected on the host, before anything is launched), or a positive
+ * hipError_t from the launch.
+ *
+ * Tensor formats (reference: w4a16-kernel/src/w4a16/quant.py:1-30,
+ * W4A16_SPEC.md:109-171), all row-major and contiguous:
+ *   x       fp16  [M, K]        activations
+ *   qweight int32 [K/8, N]      word (i, n) holds rows 8i..8i+7, row 8i+j in
+ *                               bits [4j, 4j+4), unsigned codes 0..15
+ *   scales  fp16  [K/G, N]
+ *   zeros   fp16  [K/G, N]      integer zero-points (the fused GEMM kernels
+ *                               require integers in [-63, 63]; quantize_weight
+ *                               produces 0..15)
+ *   y       fp16  [M, N]        Y = fp16(fp32-accumulated X @ dequant(W))
+ */
+#ifndef W4A16_H_
+#define W4A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_ABI_VERSION 1
+
+enum w4a16_status {
+  W4A16_OK = 0,
+  W4A16_ERR_NULL_POINTER = -1, /* a required pointer is NULL                     */
+  W4A16_ERR_BAD_SHAPE = -2,    /* negative size, K % 8 != 0, or size > INT32_MAX  */
+  W4A16_ERR_BAD_GROUP = -3,    /* group_size <= 0 or K % group_size != 0          */
+  W4A16_ERR_WORKSPACE = -4,    /* workspace NULL or smaller than the plan needs    */
+  W4A16_ERR_BAD_PLAN = -5,     /* plan does not fit the shape / pointers           */
+  W4A16_ERR_NO_DEVICE = -6     /* no HIP device could be queried                   */
+};
+
+/* Kernel families a plan can name. */
+enum w4a16_kernel {
+  W4A16_KERNEL_AUTO = 0,
+  W4A16_KERNEL_GEMV = 1, /* decode: VALU dot2, no MFMA, M <= 8, optional split-K    */
+  W4A16_KERNEL_MFMA = 2, /* prefill: v_mfma_f32_32x32x16_f16, LDS-staged activations */
+  W4A16_KERNEL_SIMT = 3  /* sequential-k, one thread per output, any shape           */
+};
+
+/* The launch a GEMM call will make.  Filled by w4a16_gemm_plan(). */
+typedef struct w4a16_plan {
+  int32_t kernel;          /* enum w4a16_kernel (never AUTO once planned)       */
+  int32_t split_k;         /* GEMV: k-splits across workgroups (1 = none)       */
+  int32_t tile_cfg;        /* MFMA: tile configuration index                   */
+  int32_t tile_m, tile_n;  /* MFMA: workgroup tile; GEMV: 0 x 256               */
+  int64_t grid_x, grid_y;  /* workgroups launched                              */
+  int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */
+} w4a16_plan;
+
+/* Version of this ABI (W4A16_ABI_VERSION). */
+int w4a16_abi_version(void);
+
+/* Static English text for a status code (never NULL). */
+const char* w4a16_status_string(int status);
+
+/*
+ * Choose the kernel for a GEMM shape on the current device.  `kernel` and
+ * `split_k` force a family / k-split when non-zero (tests, benchmarks); 0 lets
+ * the library choose.  No reference counterpart: the reference's Triton
+ * autotuner picks configs at run time (triton_kernel.py:41-62).
+ */
+int w4a16_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t group_size, int32_t kernel,
+                    int32_t split_k, w4a16_plan* plan);
+
+/* Workspace bytes the automatic plan for this shape needs (0 = none). */
+size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size);
+
+/*
+ * Fused W4A16 GEMM, y = x @ dequant(qweight, scales, zeros).
+ * Replaces the reference's fused entry point w4a16_matmul
+ * (w4a16-kernel/src/w4a16/triton_kernel.py:131-200) and its native launcher
+ * w4a16_gemm_cuda (w4a16-kernel/src/w4a16/cuda/w4a16_gemm.cu:76-115).
+ * `workspace` must hold w4a16_gemm_workspace_bytes() bytes, zero-filled before
+ * its first use; every call leaves it zero-filled again.  Calls that share one
+ * workspace must be ordered (same stream).
+ */
+int w4a16_gemm_f16(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
+                   void* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * W4A16Linear.forward's arithmetic (w4a16-kernel/src/w4a16/linear.py:82-92):
+ * y = fp16(x @ dequant(W)) + bias, the bias added in fp16 after the GEMM's own
+ * rounding, fused into the GEMM epilogue.  `bias` may be NULL.
+ */
+int w4a16_linear_f16(const void* x, const int32_t* qweight, const void* scales,
+                     const void* zeros, const void* bias, void* y, int64_t M, int64_t N,
+                     int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Run a GEMM (with optional bias) with an explicit plan from w4a16_gemm_plan(). */
+int w4a16_gemm_f16_planned(const w4a16_plan* plan, const void* x, const int32_t* qweight,
+                           const void* scales, const void* zeros, const void* bias, void* y,
+                           int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * Group-wise asymmetric uint4 quantisation of fp16 W [K, N] with int4 packing,
+ * bit-exact with the reference's quantize_weight evaluated by torch on the CPU
+ * (w4a16-kernel/src/w4a16/quant.py:101-144).  `flag` is a device int32 the
+ * caller zero-fills; the kernel sets it to 1 if W holds a non-finite value (the
+ * reference's pack_int4 range assertion fires for such input, quant.py:62-63).
+ */
+int w4a16_quantize_pack_f16(const void* W, int32_t* qweight, void* scales, void* zeros,
+                            int64_t K, int64_t N, int64_t group_size, int32_t* flag,
+                            void* stream);
+
+/*
+ * As w4a16_quantize_pack_f16 for fp32 W [K, N]: the reference quantises fp32
+ * weights in fp32 without rounding them to fp16 first (quant.py:105,124).
+ */
+int w4a16_quantize_pack_f32(const void* W, int32_t* qweight, void* scales, void* zeros,
+                            int64_t K, int64_t N, int64_t group_size, int32_t* flag,
+                            void* stream);
+
+/*
+ * pack_int4 (w4a16-kernel/src/w4a16/quant.py:45-70): int32 codes [K, N] ->
+ * int32 [K/8, N].  `flag` (caller zero-filled) is set to 1 if a code lies
+ * outside [0, 15] (the reference asserts, quant.py:62-63).
+ */
+int w4a16_pack_int4(const int32_t* q, int32_t* qweight, int64_t K, int64_t N, int32_t* flag,
+                    void* stream);
+
+/* unpack_int4 (w4a16-kernel/src/w4a16/quant.py:73-95): int32 [K/8, N] -> int32 [K, N]. */
+int w4a16_unpack_int4(const int32_t* qweight, int32_t* q, int64_t K, int64_t N, void* stream);
+
+/*
+ * dequantize_weight (w4a16-kernel/src/w4a16/quant.py:147-178):
+ * w = fp16((fp16(q) - z) * s), fp16 [K, N]; exact fp16 arithmetic for any zeros.
+ */
+int w4a16_dequantize_f16(const int32_t* qweight, const void* scales, const void* zeros, void* w,
+                         int64_t K, int64_t N, int64_t group_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H_ */

@@ -1,0 +1,261 @@
+"""CPU tests of the C ABI library and of the Python host logic (no GPU compute).
+
+* libw4a16.so loads and exports every function include/w4a16.h declares;
+* the ABI rejects invalid arguments with its negative status codes before it
+  touches a device (null pointers, bad shapes / group sizes, missing workspace);
+* the planner picks the kernel family by shape;
+* the Python wrappers raise the reference's exception types for bad input
+  (AssertionError / ValueError, reference quant.py:114-119, triton_kernel.py:153-187,
+  linear.py:38-41) before any device work.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "w4a16.h")
+
+
+def _declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(w4a16_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_api():
+    names = _declared_functions()
+    for required in ("w4a16_gemm_f16", "w4a16_quantize_pack_f16", "w4a16_pack_int4",
+                     "w4a16_unpack_int4", "w4a16_dequantize_f16", "w4a16_linear_f16",
+                     "w4a16_gemm_plan", "w4a16_abi_version", "w4a16_status_string"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from w4a16 import _lib
+
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"libw4a16.so does not export {name}"
+        assert name in _lib.SIGNATURES, f"ctypes binding lacks {name}"
+    assert set(_lib.SIGNATURES) == set(_declared_functions())
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.w4a16_abi_version() == 1
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        s = lib.w4a16_status_string(code)
+        assert s and isinstance(s, bytes)
+    assert lib.w4a16_status_string(-99) == b"unknown status"
+
+
+NULL = None
+
+
+@pytest.mark.parametrize("M,N,K,G,expect", [
+    (-1, 16, 64, 32, -2),     # negative M
+    (1, 16, 60, 32, -2),      # K % 8 != 0
+    (1, 16, 64, 0, -3),       # G <= 0
+    (1, 16, 64, 48, -3),      # K % G != 0
+    (1, 2**31, 64, 32, -2),   # N > INT32_MAX
+])
+def test_gemm_rejects_bad_shapes(lib, M, N, K, G, expect):
+    dummy = ctypes.c_void_p(256)
+    code = lib.w4a16_gemm_f16(dummy, dummy, dummy, dummy, dummy, M, N, K, G, NULL, 0, NULL)
+    assert code == expect
+
+
+def test_gemm_rejects_null_pointers(lib):
+    dummy = ctypes.c_void_p(256)
+    assert lib.w4a16_gemm_f16(NULL, dummy, dummy, dummy, dummy, 1, 16, 64, 32, NULL, 0, NULL) == -1
+    assert lib.w4a16_gemm_f16(dummy, NULL, dummy, dummy, dummy, 1, 16, 64, 32, NULL, 0, NULL) == -1
+    assert lib.w4a16_gemm_f16(dummy, dummy, dummy, dummy, NULL, 1, 16, 64, 32, NULL, 0, NULL) == -1
+    # empty problems are valid and launch nothing
+    assert lib.w4a16_gemm_f16(NULL, NULL, NULL, NULL, NULL, 0, 16, 64, 32, NULL, 0, NULL) == 0
+    assert lib.w4a16_gemm_f16(NULL, NULL, NULL, NULL, NULL, 4, 0, 64, 32, NULL, 0, NULL) == 0
+
+
+def test_split_k_gemv_requires_workspace(lib):
+    from w4a16 import _lib
+
+    p = _lib.plan(1, 4096, 4096, 128)
+    assert p.kernel == _lib.KERNEL_GEMV and p.split_k > 1 and p.workspace_bytes > 0
+    a = ctypes.c_void_p(1 << 12)   # aligned fake pointers: never dereferenced
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 4096, 4096, 128,
+                                      NULL, 0, NULL)
+    assert code == -4
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 4096, 4096, 128,
+                                      a, 16, NULL)
+    assert code == -4
+
+
+def test_planned_rejects_mismatched_plan(lib):
+    from w4a16 import _lib
+
+    p = _lib.plan(1, 4096, 4096, 128, _lib.KERNEL_GEMV, 1)
+    a = ctypes.c_void_p(1 << 12)
+    # GEMV plan used for M = 64 (GEMV takes M <= 8)
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 64, 4096, 4096, 128,
+                                      NULL, 0, NULL)
+    assert code == -5
+    # misaligned activation pointer for a vector kernel
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), ctypes.c_void_p((1 << 12) + 2), a, a, a,
+                                      NULL, a, 1, 4096, 4096, 128, NULL, 0, NULL)
+    assert code == -5
+
+
+def test_quant_entry_points_reject_bad_args(lib):
+    a = ctypes.c_void_p(1 << 12)
+    assert lib.w4a16_quantize_pack_f16(a, a, a, a, 100, 16, 64, a, NULL) == -2
+    assert lib.w4a16_quantize_pack_f16(a, a, a, a, 96, 16, 64, a, NULL) == -3
+    assert lib.w4a16_quantize_pack_f16(a, a, a, a, 128, 16, 64, NULL, NULL) == -1
+    assert lib.w4a16_quantize_pack_f32(NULL, a, a, a, 128, 16, 64, a, NULL) == -1
+    assert lib.w4a16_pack_int4(a, a, 12, 4, a, NULL) == -2
+    assert lib.w4a16_pack_int4(NULL, a, 16, 4, a, NULL) == -1
+    assert lib.w4a16_unpack_int4(a, NULL, 16, 4, NULL) == -1
+    assert lib.w4a16_dequantize_f16(a, a, a, NULL, 128, 4, 64, NULL) == -1
+    assert lib.w4a16_dequantize_f16(a, a, a, a, 128, 4, 0, NULL) == -3
+    # empty inputs launch nothing
+    assert lib.w4a16_quantize_pack_f16(NULL, NULL, NULL, NULL, 0, 16, 64, NULL, NULL) == 0
+    assert lib.w4a16_unpack_int4(NULL, NULL, 16, 0, NULL) == 0
+
+
+@pytest.mark.parametrize("M,N,K,G,kernel", [
+    (1, 4096, 4096, 128, "gemv"),
+    (8, 28672, 4096, 128, "gemv"),
+    (9, 4096, 4096, 128, "mfma"),
+    (4096, 14336, 4096, 128, "mfma"),
+    (16, 4096, 4096, 32, "mfma"),
+    (1, 4098, 4096, 128, "simt"),     # N % 4 != 0
+    (64, 4096, 4096, 16, "simt"),     # G % 32 != 0 beyond the GEMV's M range
+    (1, 8, 8, 4, "simt"),             # G = 4: words straddle groups
+])
+def test_planner_kernel_choice(M, N, K, G, kernel):
+    from w4a16 import _lib
+
+    p = _lib.plan(M, N, K, G)
+    assert _lib.KERNEL_NAMES[p.kernel] == kernel
+    assert p.grid_x >= 1 and p.grid_y >= 1
+
+
+def test_planner_gemv_split_fills_device():
+    from w4a16 import _lib
+
+    p = _lib.plan(1, 4096, 4096, 128)
+    assert p.grid_x * p.grid_y >= 256          # at least one workgroup per CU
+    rows = -(-512 // p.split_k)
+    assert (p.split_k - 1) * rows < 512        # every split owns at least one row
+    p1 = _lib.plan(1, 4096, 4096, 128, _lib.KERNEL_GEMV, 1)
+    assert p1.split_k == 1 and p1.workspace_bytes == 0
+
+
+def test_planner_forced_kernel_must_fit():
+    from w4a16 import _lib
+
+    with pytest.raises(RuntimeError):
+        _lib.plan(16, 4096, 4096, 128, _lib.KERNEL_GEMV, 0)   # GEMV takes M <= 8
+    with pytest.raises(RuntimeError):
+        _lib.plan(64, 4098, 4096, 128, _lib.KERNEL_MFMA, 0)   # MFMA needs N % 4 == 0
+
+
+# --------------------------------------------------------------------------- #
+# Python wrappers: precondition errors before any device work                  #
+# --------------------------------------------------------------------------- #
+def test_quantize_weight_divisibility_errors():
+    """Reference test_quant.py:103-109 (raised before staging to a device)."""
+    from w4a16 import quantize_weight
+
+    with pytest.raises(ValueError):
+        quantize_weight(torch.randn(100, 16, dtype=torch.float16), group_size=64)
+    with pytest.raises(ValueError):
+        quantize_weight(torch.randn(96, 16, dtype=torch.float16), group_size=64)
+    with pytest.raises(AssertionError):
+        quantize_weight(torch.randn(8, 8, 8, dtype=torch.float16), group_size=8)
+
+
+def test_pack_requires_k_div_8():
+    """Reference test_quant.py:50-52."""
+    from w4a16 import pack_int4
+
+    with pytest.raises(AssertionError):
+        pack_int4(torch.zeros((7, 4), dtype=torch.int32))
+
+
+def test_w4a16_matmul_requires_device_tensors():
+    from w4a16 import w4a16_matmul
+
+    x = torch.zeros(1, 64, dtype=torch.float16)
+    qw = torch.zeros(8, 16, dtype=torch.int32)
+    s = torch.zeros(2, 16, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        w4a16_matmul(x, qw, s, s, 32)
+
+
+def test_linear_constructor_errors():
+    """Reference linear.py:38-41."""
+    from w4a16 import W4A16Linear
+
+    with pytest.raises(ValueError):
+        W4A16Linear(100, 16)
+    with pytest.raises(ValueError):
+        W4A16Linear(192, 16, group_size=128)
+    m = W4A16Linear(256, 48, group_size=128, bias=True)
+    sd = m.state_dict()
+    assert list(sd) == ["qweight", "scales", "zeros", "bias"]
+    assert sd["qweight"].shape == (32, 48) and sd["qweight"].dtype == torch.int32
+    assert sd["scales"].shape == (2, 48) and sd["scales"].dtype == torch.float16
+    assert sd["zeros"].shape == (2, 48) and sd["bias"].shape == (48,)
+    assert "group_size=128" in repr(m)
+    assert W4A16Linear(256, 48, bias=False).bias is None
+
+
+def test_no_cpu_fallback_without_device(monkeypatch):
+    """With no HIP device visible, compute entry points raise instead of running
+    anything on the CPU."""
+    from w4a16 import quantize_weight, unpack_int4
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError):
+        quantize_weight(torch.zeros(64, 8, dtype=torch.float16), 32)
+    with pytest.raises(RuntimeError):
+        unpack_int4(torch.zeros(8, 8, dtype=torch.int32))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from w4a16 import _lib
+
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libw4a16.so"))
+    with pytest.raises(ImportError):
+        _lib.load()
+
+
+def test_package_exports_reference_names():
+    """Reference __init__.py:21-36 names, plus HAS_TRITON (False here)."""
+    import w4a16
+
+    for name in ("quantize_weight", "dequantize_weight", "pack_int4", "unpack_int4",
+                 "reference_w4a16", "dequant_then_matmul", "fp16_matmul", "w4a16_matmul",
+                 "W4A16Linear"):
+        assert name in w4a16.__all__ and hasattr(w4a16, name)
+    assert w4a16.HAS_TRITON is False and w4a16.HAS_HIP is True
+    from w4a16.triton_kernel import w4a16_matmul as alias
+
+    assert alias is w4a16.w4a16_matmul
+    from w4a16 import cuda_kernel
+
+    assert set(cuda_kernel.__all__) == {"w4a16_matmul_cuda", "load_cuda_module", "is_available"}
+
+
+def test_workload_bytes_formula():
+    """bench_gemm.py:61-67 bytes and :86 flops at the headline configs."""
+    from w4a16 import workloads as wl
+
+    c2 = wl.CONFIGS["C2"][0]
+    assert c2.bytes() == 8_929_280
+    c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
+    assert c4.flops() == 2 * 4096 * 14336 * 4096
+    assert c4.bytes() == 182_190_080

@@ -1,0 +1,298 @@
+// extern "C" entry points of libw4a16.so (declared in include/w4a16.h).
+//
+// Host-side argument checks mirror the reference's preconditions
+// (w4a16-kernel/src/w4a16/triton_kernel.py:153-182, cuda/w4a16_gemm.cu:80-96,
+// quant.py:114-119) but report status codes instead of raising; the Python
+// package maps them to the reference's exception types.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+
+#include "../../include/w4a16.h"
+#include "w4a16_launch.h"
+
+using namespace w4a16;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kDefaultCUs = 256;  // MI355X; used only if the device cannot be queried
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return kDefaultCUs;
+  }
+  int c = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = kDefaultCUs;
+  }
+  g_cu_count[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+bool fits_i32(int64_t v) { return v >= 0 && v <= INT32_MAX; }
+
+int check_gemm_shape(int64_t M, int64_t N, int64_t K, int64_t G) {
+  if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K)) return W4A16_ERR_BAD_SHAPE;
+  if (K % 8 != 0) return W4A16_ERR_BAD_SHAPE;
+  if (G <= 0 || G > INT32_MAX || K % G != 0) return W4A16_ERR_BAD_GROUP;
+  // element counts must stay addressable with size_t and kernel int math on rows
+  if ((uint64_t)M * (uint64_t)K > (1ull << 46) || (uint64_t)M * (uint64_t)N > (1ull << 46) ||
+      (uint64_t)K * (uint64_t)N > (1ull << 48))
+    return W4A16_ERR_BAD_SHAPE;
+  return W4A16_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+bool gemv_applicable(int64_t M, int64_t N, int64_t G) {
+  return M >= 1 && M <= kGemvMaxM && N % 4 == 0 && G % 8 == 0;
+}
+bool mfma_applicable(int64_t N, int64_t G) { return N % 4 == 0 && G % 32 == 0; }
+
+int gemv_split_auto(int64_t N, int64_t K, int cus) {
+  const int64_t nblk = (N + kGemvCols - 1) / kGemvCols;
+  const int64_t KP = K / 8;
+  if (nblk <= 0 || KP <= 0) return 1;
+  const int64_t target = 2 * (int64_t)cus;
+  int64_t S = (target + nblk - 1) / nblk;
+  const int64_t smax = KP / 4 > 1 ? KP / 4 : 1;
+  if (S > smax) S = smax;
+  if (S < 1) S = 1;
+  if (S > 1) {
+    const int64_t rows = (KP + S - 1) / S;
+    S = (KP + rows - 1) / rows;
+  }
+  return (int)S;
+}
+
+int mfma_cfg_auto(int64_t M, int64_t N, int cus) {
+  if (M <= 64) return 2;
+  const int64_t t0 = ((N + 511) / 512) * ((M + 127) / 128);
+  if (t0 >= cus) return 0;
+  return 1;
+}
+
+int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_t split,
+              w4a16_plan* p) {
+  const int cus = device_cu_count();
+  *p = w4a16_plan{};
+  if (kernel == W4A16_KERNEL_AUTO && (M == 0 || N == 0 || K == 0)) kernel = W4A16_KERNEL_SIMT;
+  if (kernel == W4A16_KERNEL_AUTO) {
+    if (gemv_applicable(M, N, G))
+      kernel = W4A16_KERNEL_GEMV;
+    else if (M > kGemvMaxM && mfma_applicable(N, G))
+      kernel = W4A16_KERNEL_MFMA;
+    else
+      kernel = W4A16_KERNEL_SIMT;
+  }
+  p->kernel = kernel;
+  p->split_k = 1;
+  switch (kernel) {
+    case W4A16_KERNEL_GEMV: {
+      if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
+      int S = split > 0 ? split : gemv_split_auto(N, K, cus);
+      const int64_t KP = K / 8;
+      if (KP == 0) S = 1;
+      if (S > 1) {
+        if (S > KP) S = (int)KP;
+        const int64_t rows = (KP + S - 1) / S;
+        S = (int)((KP + rows - 1) / rows);
+      }
+      p->split_k = S;
+      p->tile_m = 0;
+      p->tile_n = kGemvCols;
+      p->grid_x = (N + kGemvCols - 1) / kGemvCols;
+      p->grid_y = S;
+      p->workspace_bytes = (int64_t)gemv_workspace_bytes((int)M, (int)N, (int)K, S);
+      return W4A16_OK;
+    }
+    case W4A16_KERNEL_MFMA: {
+      if (!mfma_applicable(N, G)) return W4A16_ERR_BAD_PLAN;
+      const int cfg = mfma_cfg_auto(M, N, cus);
+      const MfmaTile t = mfma_tile(cfg);
+      p->tile_cfg = cfg;
+      p->tile_m = t.bm;
+      p->tile_n = t.bn;
+      p->grid_x = (N + t.bn - 1) / t.bn;
+      p->grid_y = (M + t.bm - 1) / t.bm;
+      return W4A16_OK;
+    }
+    case W4A16_KERNEL_SIMT:
+      p->tile_m = 4;
+      p->tile_n = 64;
+      p->grid_x = (N + 63) / 64;
+      p->grid_y = (M + 3) / 4;
+      return W4A16_OK;
+    default:
+      return W4A16_ERR_BAD_PLAN;
+  }
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : (int)e; }
+
+int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const void* sc,
+                const void* zr, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                int64_t G, void* ws, size_t ws_bytes, void* stream) {
+  if (!p) return W4A16_ERR_NULL_POINTER;
+  if (int st = check_gemm_shape(M, N, K, G)) return st;
+  if (M == 0 || N == 0) return W4A16_OK;
+  if (!x || !y || (K > 0 && (!qw || !sc || !zr))) return W4A16_ERR_NULL_POINTER;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K == 0) return to_status(hipMemsetAsync(y, 0, (size_t)M * (size_t)N * 2, s));
+  GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G};
+  switch (p->kernel) {
+    case W4A16_KERNEL_GEMV: {
+      if (!gemv_applicable(M, N, G) || p->split_k < 1 || p->split_k > K / 8)
+        return W4A16_ERR_BAD_PLAN;
+      if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8))
+        return W4A16_ERR_BAD_PLAN;
+      const size_t need = gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
+      if (need > 0 && (!ws || ws_bytes < need || !aligned(ws, 256))) return W4A16_ERR_WORKSPACE;
+      return to_status(launch_gemv(a, p->split_k, ws, s));
+    }
+    case W4A16_KERNEL_MFMA: {
+      if (!mfma_applicable(N, G) || p->tile_cfg < 0 || p->tile_cfg >= kMfmaConfigs)
+        return W4A16_ERR_BAD_PLAN;
+      if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
+          !aligned(y, 8) || (bias && !aligned(bias, 8)))
+        return W4A16_ERR_BAD_PLAN;
+      return to_status(launch_mfma(a, p->tile_cfg, s));
+    }
+    case W4A16_KERNEL_SIMT:
+      return to_status(launch_simt(a, s));
+    default:
+      return W4A16_ERR_BAD_PLAN;
+  }
+}
+
+// Automatic plan, falling back to the SIMT kernel when the pointers do not meet
+// the vector kernels' alignment.
+int run_auto(const void* x, const int32_t* qw, const void* sc, const void* zr, const void* bias,
+             void* y, int64_t M, int64_t N, int64_t K, int64_t G, void* ws, size_t ws_bytes,
+             void* stream) {
+  if (int st = check_gemm_shape(M, N, K, G)) return st;
+  w4a16_plan p;
+  if (int st = make_plan(M, N, K, G, W4A16_KERNEL_AUTO, 0, &p)) return st;
+  const bool vec_aligned = aligned(x, 16) && aligned(qw, 16) && aligned(sc, 8) &&
+                           aligned(zr, 8) && aligned(y, 8) && (!bias || aligned(bias, 8));
+  if (p.kernel != W4A16_KERNEL_SIMT && !vec_aligned) {
+    if (int st = make_plan(M, N, K, G, W4A16_KERNEL_SIMT, 0, &p)) return st;
+  }
+  return run_planned(&p, x, qw, sc, zr, bias, y, M, N, K, G, ws, ws_bytes, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
+const char* w4a16_status_string(int status) {
+  switch (status) {
+    case W4A16_OK: return "ok";
+    case W4A16_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case W4A16_ERR_BAD_SHAPE: return "invalid shape (negative size, K % 8 != 0, or too large)";
+    case W4A16_ERR_BAD_GROUP: return "invalid group_size (must be > 0 and divide K)";
+    case W4A16_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
+    case W4A16_ERR_BAD_PLAN: return "plan does not fit this shape, group size or pointers";
+    case W4A16_ERR_NO_DEVICE: return "no HIP device";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+int w4a16_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t group_size, int32_t kernel,
+                    int32_t split_k, w4a16_plan* plan) {
+  if (!plan) return W4A16_ERR_NULL_POINTER;
+  if (int st = check_gemm_shape(M, N, K, group_size)) return st;
+  if (kernel < 0 || kernel > W4A16_KERNEL_SIMT || split_k < 0) return W4A16_ERR_BAD_PLAN;
+  return make_plan(M, N, K, group_size, kernel, split_k, plan);
+}
+
+size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+  w4a16_plan p;
+  if (check_gemm_shape(M, N, K, group_size) != W4A16_OK) return 0;
+  if (make_plan(M, N, K, group_size, W4A16_KERNEL_AUTO, 0, &p) != W4A16_OK) return 0;
+  return (size_t)p.workspace_bytes;
+}
+
+int w4a16_gemm_f16(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
+                   void* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  return run_auto(x, qweight, scales, zeros, nullptr, y, M, N, K, group_size, workspace,
+                  workspace_bytes, stream);
+}
+
+int w4a16_linear_f16(const void* x, const int32_t* qweight, const void* scales,
+                     const void* zeros, const void* bias, void* y, int64_t M, int64_t N,
+                     int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  return run_auto(x, qweight, scales, zeros, bias, y, M, N, K, group_size, workspace,
+                  workspace_bytes, stream);
+}
+
+int w4a16_gemm_f16_planned(const w4a16_plan* plan, const void* x, const int32_t* qweight,
+                           const void* scales, const void* zeros, const void* bias, void* y,
+                           int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return run_planned(plan, x, qweight, scales, zeros, bias, y, M, N, K, group_size, workspace,
+                     workspace_bytes, stream);
+}
+
+static int quantize_common(const void* W, bool f32, int32_t* qweight, void* scales, void* zeros,
+                           int64_t K, int64_t N, int64_t group_size, int32_t* flag, void* stream) {
+  if (int st = check_gemm_shape(0, N, K, group_size)) return st;
+  if (K == 0 || N == 0) return W4A16_OK;
+  if (!W || !qweight || !scales || !zeros || !flag) return W4A16_ERR_NULL_POINTER;
+  return to_status(launch_quantize_pack(W, f32, qweight, scales, zeros, (int)K, (int)N,
+                                        (int)group_size, flag,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int w4a16_quantize_pack_f16(const void* W, int32_t* qweight, void* scales, void* zeros,
+                            int64_t K, int64_t N, int64_t group_size, int32_t* flag,
+                            void* stream) {
+  return quantize_common(W, false, qweight, scales, zeros, K, N, group_size, flag, stream);
+}
+
+int w4a16_quantize_pack_f32(const void* W, int32_t* qweight, void* scales, void* zeros,
+                            int64_t K, int64_t N, int64_t group_size, int32_t* flag,
+                            void* stream) {
+  return quantize_common(W, true, qweight, scales, zeros, K, N, group_size, flag, stream);
+}
+
+int w4a16_pack_int4(const int32_t* q, int32_t* qweight, int64_t K, int64_t N, int32_t* flag,
+                    void* stream) {
+  if (int st = check_gemm_shape(0, N, K, 8)) return st;
+  if (K == 0 || N == 0) return W4A16_OK;
+  if (!q || !qweight || !flag) return W4A16_ERR_NULL_POINTER;
+  return to_status(launch_pack(q, qweight, (int)K, (int)N, flag, static_cast<hipStream_t>(stream)));
+}
+
+int w4a16_unpack_int4(const int32_t* qweight, int32_t* q, int64_t K, int64_t N, void* stream) {
+  if (int st = check_gemm_shape(0, N, K, 8)) return st;
+  if (K == 0 || N == 0) return W4A16_OK;
+  if (!q || !qweight) return W4A16_ERR_NULL_POINTER;
+  return to_status(launch_unpack(qweight, q, (int)K, (int)N, static_cast<hipStream_t>(stream)));
+}
+
+int w4a16_dequantize_f16(const int32_t* qweight, const void* scales, const void* zeros, void* w,
+                         int64_t K, int64_t N, int64_t group_size, void* stream) {
+  if (int st = check_gemm_shape(0, N, K, group_size)) return st;
+  if (K == 0 || N == 0) return W4A16_OK;
+  if (!qweight || !scales || !zeros || !w) return W4A16_ERR_NULL_POINTER;
+  return to_status(launch_dequant(qweight, scales, zeros, w, (int)K, (int)N, (int)group_size,
+                                  static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,307 @@
+// Quantise / pack / unpack / dequantise kernels, bit-exact with the reference's
+// PyTorch quantiser as torch evaluates it on the CPU
+// (w4a16-kernel/src/w4a16/quant.py:45-178):
+//   scale = (gmax - gmin) / 15        IEEE fp32 division (not a reciprocal multiply)
+//   scale = scale > 0 ? scale : 1
+//   zero  = clamp(rint(-gmin / scale), 0, 15)   compare-select clamp, -0.0 survives
+//   q     = clamp(rint(W / scale) + zero, 0, 15) with the fp32 scale
+//   scales, zeros -> fp16 (RNE); codes packed 8 per int32, row 8i+j in nibble j.
+// rint is round-half-to-even (v_rndne_f32).  HIP divides fp32 with the correctly
+// rounded sequence by default, and the build never enables fast-math, so the
+// compare-selects are not folded into min/max (which could drop -0.0).
+// Group minimum: when several zeros tie, the last one in k order wins
+// (v <= min ? v : min), matching torch's vectorised CPU column reduction.
+#include "w4a16_device.h"
+#include "w4a16_launch.h"
+
+namespace w4a16 {
+namespace {
+
+// Input element traits: fp16 weights arrive as raw bits, fp32 as floats.
+struct InF16 {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float val(T b) { return (float)as_h(b); }
+  static __device__ __forceinline__ bool nonfinite(T b) { return (b & 0x7C00u) == 0x7C00u; }
+  // four consecutive elements (8-byte aligned)
+  static __device__ __forceinline__ void load4(const T* p, T out[4]) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    out[0] = v.x & 0xFFFFu;
+    out[1] = v.x >> 16;
+    out[2] = v.y & 0xFFFFu;
+    out[3] = v.y >> 16;
+  }
+};
+struct InF32 {
+  typedef float T;
+  static __device__ __forceinline__ float val(T v) { return v; }
+  static __device__ __forceinline__ bool nonfinite(T v) {
+    return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) == 0x7F800000u;
+  }
+  // four consecutive elements (16-byte aligned)
+  static __device__ __forceinline__ void load4(const T* p, T out[4]) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+  }
+};
+
+__device__ __forceinline__ float clamp_q(float v) {
+  v = (v < 0.0f) ? 0.0f : v;
+  v = (v > 15.0f) ? 15.0f : v;
+  return v;
+}
+
+template <class IN, int CPT>
+__device__ __forceinline__ void load_row(const typename IN::T* p, typename IN::T b[CPT]) {
+  if constexpr (CPT == 4) {
+    IN::load4(p, b);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) b[c] = p[c];
+  }
+}
+
+// One thread quantises CPT adjacent columns of one group (G % 8 == 0).
+template <class IN, int CPT>
+__global__ __launch_bounds__(256) void quantize_kernel(const typename IN::T* __restrict__ W,
+                                                       uint32_t* __restrict__ QW,
+                                                       uint16_t* __restrict__ SC,
+                                                       uint16_t* __restrict__ ZR, int K, int N,
+                                                       int G, int32_t* __restrict__ flag) {
+  typedef typename IN::T T;
+  const int n = (blockIdx.y * 256 + threadIdx.x) * CPT;
+  const int g = blockIdx.x;
+  if (n >= N) return;
+  const T* src = W + (size_t)g * G * N + n;
+
+  float mn[CPT], mx[CPT];
+  bool bad = false;
+  {
+    T b[CPT];
+    load_row<IN, CPT>(src, b);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      bad |= IN::nonfinite(b[c]);
+      mn[c] = mx[c] = IN::val(b[c]);
+    }
+  }
+  for (int r = 1; r < G; ++r) {
+    T b[CPT];
+    load_row<IN, CPT>(src + (size_t)r * N, b);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      bad |= IN::nonfinite(b[c]);
+      const float v = IN::val(b[c]);
+      mn[c] = (v <= mn[c]) ? v : mn[c];
+      mx[c] = (v >= mx[c]) ? v : mx[c];
+    }
+  }
+  if (bad) *flag = 1;
+
+  float sc[CPT], zr[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    float s = (mx[c] - mn[c]) / 15.0f;
+    s = (s > 0.0f) ? s : 1.0f;
+    sc[c] = s;
+    zr[c] = clamp_q(__builtin_rintf(-mn[c] / s));
+  }
+
+  for (int r8 = 0; r8 < G / 8; ++r8) {
+    uint32_t word[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) word[c] = 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      T b[CPT];
+      load_row<IN, CPT>(src + (size_t)(r8 * 8 + j) * N, b);
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const float q = clamp_q(__builtin_rintf(IN::val(b[c]) / sc[c]) + zr[c]);
+        word[c] |= ((uint32_t)(int)q & 0xFu) << (4 * j);
+      }
+    }
+    uint32_t* dst = QW + (size_t)(g * (G / 8) + r8) * N + n;
+    if constexpr (CPT == 4) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(word[0], word[1], word[2], word[3]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) dst[c] = word[c];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    SC[(size_t)g * N + n + c] = as_u16((f16)sc[c]);
+    ZR[(size_t)g * N + n + c] = as_u16((f16)zr[c]);
+  }
+}
+
+// Any G dividing K (G % 8 != 0 lets a packed word straddle groups): one thread
+// per packed word; each row's group statistics are recomputed from the group's
+// G values, and the thread that owns a group's first row writes its scale/zero.
+struct GroupQ {
+  float scale, zero;
+  bool bad;
+};
+
+template <class IN>
+__device__ GroupQ group_stats(const typename IN::T* __restrict__ W, int g, int G, int N, int n) {
+  const typename IN::T* src = W + (size_t)g * G * N + n;
+  typename IN::T b = src[0];
+  bool bad = IN::nonfinite(b);
+  float mn = IN::val(b), mx = mn;
+  for (int r = 1; r < G; ++r) {
+    b = src[(size_t)r * N];
+    bad |= IN::nonfinite(b);
+    const float v = IN::val(b);
+    mn = (v <= mn) ? v : mn;
+    mx = (v >= mx) ? v : mx;
+  }
+  float s = (mx - mn) / 15.0f;
+  s = (s > 0.0f) ? s : 1.0f;
+  return GroupQ{s, clamp_q(__builtin_rintf(-mn / s)), bad};
+}
+
+template <class IN>
+__global__ __launch_bounds__(256) void quantize_general_kernel(
+    const typename IN::T* __restrict__ W, uint32_t* __restrict__ QW, uint16_t* __restrict__ SC,
+    uint16_t* __restrict__ ZR, int K, int N, int G, int32_t* __restrict__ flag) {
+  const int n = blockIdx.y * 256 + threadIdx.x;
+  const int i = blockIdx.x;
+  if (n >= N) return;
+  uint32_t word = 0u;
+  int gcur = -1;
+  GroupQ gq{1.0f, 0.0f, false};
+  bool bad = false;
+  for (int j = 0; j < 8; ++j) {
+    const int k = 8 * i + j;
+    const int g = k / G;
+    if (g != gcur) {
+      gcur = g;
+      gq = group_stats<IN>(W, g, G, N, n);
+      bad |= gq.bad;
+      if (k == g * G) {
+        SC[(size_t)g * N + n] = as_u16((f16)gq.scale);
+        ZR[(size_t)g * N + n] = as_u16((f16)gq.zero);
+      }
+    }
+    const float q = clamp_q(__builtin_rintf(IN::val(W[(size_t)k * N + n]) / gq.scale) + gq.zero);
+    word |= ((uint32_t)(int)q & 0xFu) << (4 * j);
+  }
+  if (bad) *flag = 1;
+  QW[(size_t)i * N + n] = word;
+}
+
+// pack_int4: int32 codes [K, N] -> int32 [K/8, N]; flags values outside [0, 15].
+__global__ __launch_bounds__(256) void pack_kernel(const int32_t* __restrict__ Q,
+                                                   uint32_t* __restrict__ QW, int K, int N,
+                                                   int32_t* __restrict__ flag) {
+  const int n = blockIdx.y * 256 + threadIdx.x;
+  const int i = blockIdx.x;
+  if (n >= N) return;
+  uint32_t word = 0u;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int32_t v = Q[(size_t)(8 * i + j) * N + n];
+    bad |= (v < 0) | (v > 15);
+    word |= ((uint32_t)v & 0xFu) << (4 * j);
+  }
+  if (bad) *flag = 1;
+  QW[(size_t)i * N + n] = word;
+}
+
+// unpack_int4: int32 [K/8, N] -> int32 codes [K, N].
+__global__ __launch_bounds__(256) void unpack_kernel(const uint32_t* __restrict__ QW,
+                                                     int32_t* __restrict__ Q, int K, int N) {
+  const int n = blockIdx.y * 256 + threadIdx.x;
+  const int i = blockIdx.x;
+  if (n >= N) return;
+  const uint32_t w = QW[(size_t)i * N + n];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) Q[(size_t)(8 * i + j) * N + n] = (int32_t)((w >> (4 * j)) & 0xFu);
+}
+
+// dequantize_weight: fp16 (fp16(q) - z) * s for any fp16 zero-point.
+__global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ QW,
+                                                      const f16* __restrict__ SC,
+                                                      const f16* __restrict__ ZR,
+                                                      f16* __restrict__ Wd, int K, int N, int G) {
+  const int n = blockIdx.y * 256 + threadIdx.x;
+  const int i = blockIdx.x;
+  if (n >= N) return;
+  const uint32_t w = QW[(size_t)i * N + n];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int g = (8 * i + j) / G;
+    const f16 s = SC[(size_t)g * N + n];
+    const f16 z = ZR[(size_t)g * N + n];
+    const f16 q = (f16)(float)((w >> (4 * j)) & 0xFu);
+    Wd[(size_t)(8 * i + j) * N + n] = (q - z) * s;
+  }
+}
+
+template <class IN>
+hipError_t quantize_launch(const void* W, int32_t* qw, void* sc, void* zr, int K, int N, int G,
+                           int32_t* flag, hipStream_t st) {
+  typedef typename IN::T T;
+  const T* w = static_cast<const T*>(W);
+  uint32_t* q = reinterpret_cast<uint32_t*>(qw);
+  uint16_t* s = static_cast<uint16_t*>(sc);
+  uint16_t* z = static_cast<uint16_t*>(zr);
+  if (G % 8 != 0) {
+    dim3 grid(K / 8, (N + 255) / 256);
+    hipLaunchKernelGGL(quantize_general_kernel<IN>, grid, dim3(256), 0, st, w, q, s, z, K, N, G,
+                       flag);
+    return hipGetLastError();
+  }
+  const uintptr_t wa = 4 * sizeof(T);
+  const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(W) & (wa - 1)) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(qw) & 15) == 0);
+  if (vec) {
+    dim3 grid(K / G, (N / 4 + 255) / 256);
+    hipLaunchKernelGGL((quantize_kernel<IN, 4>), grid, dim3(256), 0, st, w, q, s, z, K, N, G,
+                       flag);
+  } else {
+    dim3 grid(K / G, (N + 255) / 256);
+    hipLaunchKernelGGL((quantize_kernel<IN, 1>), grid, dim3(256), 0, st, w, q, s, z, K, N, G,
+                       flag);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quantize_pack(const void* W, bool w_is_f32, int32_t* qw, void* sc, void* zr,
+                                int K, int N, int G, int32_t* flag, hipStream_t st) {
+  return w_is_f32 ? quantize_launch<InF32>(W, qw, sc, zr, K, N, G, flag, st)
+                  : quantize_launch<InF16>(W, qw, sc, zr, K, N, G, flag, st);
+}
+
+hipError_t launch_pack(const int32_t* q, int32_t* qw, int K, int N, int32_t* flag,
+                       hipStream_t st) {
+  dim3 grid(K / 8, (N + 255) / 256);
+  hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, st, q, reinterpret_cast<uint32_t*>(qw), K,
+                     N, flag);
+  return hipGetLastError();
+}
+
+hipError_t launch_unpack(const int32_t* qw, int32_t* q, int K, int N, hipStream_t st) {
+  dim3 grid(K / 8, (N + 255) / 256);
+  hipLaunchKernelGGL(unpack_kernel, grid, dim3(256), 0, st,
+                     reinterpret_cast<const uint32_t*>(qw), q, K, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const int32_t* qw, const void* sc, const void* zr, void* w, int K,
+                          int N, int G, hipStream_t st) {
+  dim3 grid(K / 8, (N + 255) / 256);
+  hipLaunchKernelGGL(dequant_kernel, grid, dim3(256), 0, st,
+                     reinterpret_cast<const uint32_t*>(qw), static_cast<const f16*>(sc),
+                     static_cast<const f16*>(zr), static_cast<f16*>(w), K, N, G);
+  return hipGetLastError();
+}
+
+}  // namespace w4a16

@@ -1,0 +1,49 @@
+// Host-side interface between the C-ABI layer (capi.cpp) and the kernel
+// translation units.  Internal to libw4a16.so; not installed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+// One W4A16 GEMM call: Y[M,N] = X[M,K] @ dequant(qweight, scales, zeros) (+ bias).
+struct GemmArgs {
+  const void* x;        // fp16 [M, K]
+  const int32_t* qw;    // int32 [K/8, N]
+  const void* sc;       // fp16 [K/G, N]
+  const void* zr;       // fp16 [K/G, N]
+  const void* bias;     // fp16 [N] or nullptr
+  void* y;              // fp16 [M, N]
+  int M, N, K, G;
+};
+
+// Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  `split` k-splits; when split > 1
+// `ws` holds the counters + fp32 partials described by gemv_workspace_bytes().
+constexpr int kGemvMaxM = 8;
+constexpr int kGemvCols = 256;
+size_t gemv_workspace_bytes(int M, int N, int K, int split);
+int gemv_rows_per_split(int K, int split);
+hipError_t launch_gemv(const GemmArgs& a, int split, void* ws, hipStream_t st);
+
+// Prefill GEMM on MFMA (v_mfma_f32_32x32x16_f16).  `cfg` picks the tile shape.
+struct MfmaTile {
+  int bm, bn;
+};
+constexpr int kMfmaConfigs = 3;
+MfmaTile mfma_tile(int cfg);
+hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st);
+
+// Sequential-k SIMT kernel: any N, any G dividing K, no alignment needs.
+hipError_t launch_simt(const GemmArgs& a, hipStream_t st);
+
+// Quantisation / packing kernels.
+hipError_t launch_quantize_pack(const void* W, bool w_is_f32, int32_t* qw, void* sc, void* zr,
+                                int K, int N, int G, int32_t* flag, hipStream_t st);
+hipError_t launch_pack(const int32_t* q, int32_t* qw, int K, int N, int32_t* flag, hipStream_t st);
+hipError_t launch_unpack(const int32_t* qw, int32_t* q, int K, int N, hipStream_t st);
+hipError_t launch_dequant(const int32_t* qw, const void* sc, const void* zr, void* w, int K,
+                          int N, int G, hipStream_t st);
+
+}  // namespace w4a16

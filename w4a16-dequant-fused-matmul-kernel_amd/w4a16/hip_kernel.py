@@ -1,0 +1,148 @@
+"""Fused W4A16 GEMM entry point on MI355X: ``Y = X @ dequant(qweight)``.
+
+Drop-in for the reference's primary backend ``w4a16_matmul``
+(w4a16-kernel/src/w4a16/triton_kernel.py:131-200): same signature, same
+preconditions raised as ``AssertionError`` (:153-187), optional ``out``.  The
+kernel is chosen inside ``libw4a16.so`` by shape:
+
+* M <= 8: decode GEMV -- VALU v_dot2_f32_f16, no MFMA, split-K across
+  workgroups with a deterministic in-kernel reduction;
+* M > 8: prefill GEMM -- v_mfma_f32_32x32x16_f16, weights dequantised in
+  registers, activations staged through LDS;
+* shapes the vector kernels do not take (N % 4 != 0, misaligned views): the
+  sequential-k SIMT kernel.
+
+Group size: the reference's Triton path needs every autotune BLOCK_K to divide
+G (:177-182), i.e. G % 64 == 0.  These kernels need G % 32 == 0, so G = 32 works
+here as well; G = 8 still raises AssertionError like the reference.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from . import _runtime as rt
+
+__all__ = ["w4a16_matmul", "w4a16_linear", "plan_for", "GROUP_MULTIPLE"]
+
+GROUP_MULTIPLE = 32
+
+
+def _check_operands(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor, group_size: int):
+    assert x.is_cuda, "x must be on a HIP device"
+    assert qweight.is_cuda and scales.is_cuda and zeros.is_cuda, "all inputs must be on a HIP device"
+    assert x.dtype == torch.float16, f"x must be fp16, got {x.dtype}"
+    assert qweight.dtype == torch.int32, f"qweight must be int32, got {qweight.dtype}"
+    assert scales.dtype == torch.float16, f"scales must be fp16, got {scales.dtype}"
+    assert zeros.dtype == torch.float16, f"zeros must be fp16, got {zeros.dtype}"
+    assert x.dim() == 2 and qweight.dim() == 2, "x and qweight must be 2D"
+    M, K = x.shape
+    Kp, N = qweight.shape
+    assert Kp * 8 == K, f"qweight rows (K//8)={Kp} incompatible with x K={K}"
+    assert K % 8 == 0, f"K={K} must be divisible by 8"
+    assert group_size > 0 and K % group_size == 0, (
+        f"K={K} must be divisible by group_size={group_size}")
+    num_groups = K // group_size
+    assert scales.shape == (num_groups, N), f"scales shape {tuple(scales.shape)} != {(num_groups, N)}"
+    assert zeros.shape == (num_groups, N), f"zeros shape {tuple(zeros.shape)} != {(num_groups, N)}"
+    assert x.is_contiguous(), "x must be contiguous"
+    assert qweight.is_contiguous(), "qweight must be contiguous"
+    assert scales.is_contiguous(), "scales must be contiguous"
+    assert zeros.is_contiguous(), "zeros must be contiguous"
+    assert group_size % GROUP_MULTIPLE == 0, (
+        f"group_size={group_size} must be a multiple of {GROUP_MULTIPLE} for the fused kernels")
+    dev = x.device
+    assert qweight.device == dev and scales.device == dev and zeros.device == dev, (
+        "all inputs must be on the same device")
+    return M, K, N
+
+
+def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | None"):
+    dev = x.device
+    with rt.on_device(dev):
+        if plan is None:
+            ws_bytes = rt.lib().w4a16_gemm_workspace_bytes(M, N, K, G)
+        else:
+            ws_bytes = int(plan.workspace_bytes)
+        ws = rt.workspace(dev, ws_bytes)
+        stream = rt.stream_ptr(dev)
+        if plan is None:
+            code = rt.lib().w4a16_linear_f16(
+                x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
+                rt.ptr(bias), y.data_ptr(), M, N, K, G, rt.ptr(ws),
+                0 if ws is None else ws.numel(), stream)
+        else:
+            code = rt.lib().w4a16_gemm_f16_planned(
+                ctypes.byref(plan), x.data_ptr(), qweight.data_ptr(), scales.data_ptr(),
+                zeros.data_ptr(), rt.ptr(bias), y.data_ptr(), M, N, K, G, rt.ptr(ws),
+                0 if ws is None else ws.numel(), stream)
+    _lib.check(code, "w4a16 GEMM")
+    return y
+
+
+def _output(x: Tensor, M: int, N: int, out: Tensor | None) -> Tensor:
+    if out is None:
+        return torch.empty((M, N), device=x.device, dtype=torch.float16)
+    assert out.shape == (M, N) and out.dtype == torch.float16 and out.is_contiguous()
+    assert out.device == x.device, "out must be on the same device as x"
+    return out
+
+
+def w4a16_matmul(
+    x: Tensor,
+    qweight: Tensor,
+    scales: Tensor,
+    zeros: Tensor,
+    group_size: int,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Fused W4A16 GEMM: ``Y = X @ dequant(qweight)`` (triton_kernel.py:131-200).
+
+    Args:
+        x: activations [M, K] fp16, contiguous, on a HIP device.
+        qweight: int32 [K//8, N], contiguous.
+        scales, zeros: fp16 [K//G, N], contiguous.
+        group_size: G, with G | K, 8 | K and G % 32 == 0.
+        out: optional preallocated fp16 [M, N] output.
+    Returns:
+        fp16 [M, N], fp32-accumulated.
+    """
+    M, K, N = _check_operands(x, qweight, scales, zeros, group_size)
+    y = _output(x, M, N, out)
+    return _launch(x, qweight, scales, zeros, None, y, M, N, K, group_size, None)
+
+
+def w4a16_linear(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor,
+                 bias: Tensor | None, group_size: int, out: Tensor | None = None) -> Tensor:
+    """``fp16(X @ dequant(W)) + bias`` with the bias add fused into the epilogue.
+
+    Same arithmetic as W4A16Linear's kernel call followed by ``y + bias``
+    (linear.py:89-91): the GEMM result is rounded to fp16, then the fp16 bias is
+    added with one more fp16 rounding.
+    """
+    M, K, N = _check_operands(x, qweight, scales, zeros, group_size)
+    if bias is not None:
+        assert bias.shape == (N,) and bias.dtype == torch.float16 and bias.is_contiguous()
+        assert bias.device == x.device
+    y = _output(x, M, N, out)
+    return _launch(x, qweight, scales, zeros, bias, y, M, N, K, group_size, None)
+
+
+def plan_for(M: int, N: int, K: int, group_size: int, kernel: str | int = 0,
+             split_k: int = 0) -> "_lib.Plan":
+    """The launch plan for a shape; `kernel` may force "gemv", "mfma" or "simt"."""
+    if isinstance(kernel, str):
+        kernel = {"auto": 0, "gemv": 1, "mfma": 2, "simt": 3}[kernel]
+    return _lib.plan(M, N, K, group_size, kernel, split_k)
+
+
+def w4a16_matmul_planned(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor,
+                         group_size: int, plan: "_lib.Plan", bias: Tensor | None = None,
+                         out: Tensor | None = None) -> Tensor:
+    """Run the fused GEMM with an explicit plan (tests and benchmarks)."""
+    M, K, N = _check_operands(x, qweight, scales, zeros, group_size)
+    y = _output(x, M, N, out)
+    return _launch(x, qweight, scales, zeros, bias, y, M, N, K, group_size, plan)
