@@ -81,15 +81,21 @@ def test_gemm_rejects_null_pointers(lib):
 def test_split_k_gemv_requires_workspace(lib):
     from w4a16 import _lib
 
-    p = _lib.plan(1, 4096, 4096, 128)
+    # N = 1024 is too narrow to fill 256 CUs with 16-column blocks: split-K
+    p = _lib.plan(1, 1024, 4096, 128)
     assert p.kernel == _lib.KERNEL_GEMV and p.split_k > 1 and p.workspace_bytes > 0
     a = ctypes.c_void_p(1 << 12)   # aligned fake pointers: never dereferenced
-    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 4096, 4096, 128,
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       NULL, 0, NULL)
     assert code == -4
-    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 4096, 4096, 128,
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       a, 16, NULL)
     assert code == -4
+    # a column width the kernel does not have
+    p.tile_n = 48
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
+                                      a, 1 << 30, NULL)
+    assert code == -5
 
 
 def test_planned_rejects_mismatched_plan(lib):
@@ -144,11 +150,15 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
 def test_planner_gemv_split_fills_device():
     from w4a16 import _lib
 
-    p = _lib.plan(1, 4096, 4096, 128)
-    assert p.grid_x * p.grid_y >= 256          # at least one workgroup per CU
-    rows = -(-512 // p.split_k)
-    assert (p.split_k - 1) * rows < 512        # every split owns at least one row
-    p1 = _lib.plan(1, 4096, 4096, 128, _lib.KERNEL_GEMV, 1)
+    for N in (1024, 4096, 6144, 28672):
+        p = _lib.plan(1, N, 4096, 128)
+        assert p.grid_x * p.grid_y >= 256          # at least one workgroup per CU
+        assert p.tile_n in (16, 32, 64, 256)
+        rows = -(-512 // p.split_k)
+        assert (p.split_k - 1) * rows < 512        # every split owns at least one row
+    assert _lib.plan(1, 4096, 4096, 128).split_k == 1
+    assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
+    p1 = _lib.plan(1, 1024, 4096, 128, _lib.KERNEL_GEMV, 1)
     assert p1.split_k == 1 and p1.workspace_bytes == 0
 
 

@@ -58,19 +58,23 @@ bool gemv_applicable(int64_t M, int64_t N, int64_t G) {
 }
 bool mfma_applicable(int64_t N, int64_t G) { return N % 4 == 0 && G % 32 == 0; }
 
-int gemv_split_auto(int64_t N, int64_t K, int cus) {
-  const int64_t nblk = (N + kGemvCols - 1) / kGemvCols;
+// Widest column block that still gives every CU a workgroup; split K across
+// workgroups only when even 16-column blocks cannot fill the device.
+int gemv_cols_auto(int64_t N, int cus) {
+  static const int kCols[] = {256, 64, 32, 16};
+  for (int c : kCols)
+    if ((N + c - 1) / c >= cus) return c;
+  return 16;
+}
+
+int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
+  const int64_t nblk = (N + cols - 1) / cols;
   const int64_t KP = K / 8;
-  if (nblk <= 0 || KP <= 0) return 1;
-  const int64_t target = 2 * (int64_t)cus;
-  int64_t S = (target + nblk - 1) / nblk;
-  const int64_t smax = KP / 4 > 1 ? KP / 4 : 1;
+  if (nblk <= 0 || KP <= 0 || nblk >= cus) return 1;
+  int64_t S = (cus + nblk - 1) / nblk;
+  const int64_t smax = KP / 16 > 1 ? KP / 16 : 1;   // keep >= 16 rows per workgroup
   if (S > smax) S = smax;
   if (S < 1) S = 1;
-  if (S > 1) {
-    const int64_t rows = (KP + S - 1) / S;
-    S = (KP + rows - 1) / rows;
-  }
   return (int)S;
 }
 
@@ -99,7 +103,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   switch (kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
-      int S = split > 0 ? split : gemv_split_auto(N, K, cus);
+      const int cols = gemv_cols_auto(N, cus);
+      int S = split > 0 ? split : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
       if (S > 1) {
@@ -107,11 +112,12 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
         const int64_t rows = (KP + S - 1) / S;
         S = (int)((KP + rows - 1) / rows);
       }
+      if ((N + cols - 1) / cols > kGemvMaxCounterBlocks) S = 1;
       p->split_k = S;
       p->tile_m = 0;
-      p->tile_n = kGemvCols;
-      p->grid_x = (N + kGemvCols - 1) / kGemvCols;
-      p->grid_y = S;
+      p->tile_n = cols;
+      p->grid_x = ((N + cols - 1) / cols) * S;
+      p->grid_y = 1;
       p->workspace_bytes = (int64_t)gemv_workspace_bytes((int)M, (int)N, (int)K, S);
       return W4A16_OK;
     }
@@ -151,13 +157,17 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G};
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
-      if (!gemv_applicable(M, N, G) || p->split_k < 1 || p->split_k > K / 8)
+      if (!gemv_applicable(M, N, G) || p->split_k < 1 || p->split_k > K / 8 ||
+          !gemv_cols_valid(p->tile_n))
         return W4A16_ERR_BAD_PLAN;
+      const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
+      if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;
+      if (p->split_k > 1 && nblk > kGemvMaxCounterBlocks) return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8))
         return W4A16_ERR_BAD_PLAN;
       const size_t need = gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
       if (need > 0 && (!ws || ws_bytes < need || !aligned(ws, 256))) return W4A16_ERR_WORKSPACE;
-      return to_status(launch_gemv(a, p->split_k, ws, s));
+      return to_status(launch_gemv(a, p->tile_n, p->split_k, ws, s));
     }
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G) || p->tile_cfg < 0 || p->tile_cfg >= kMfmaConfigs)

@@ -4,19 +4,25 @@
 // (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 at M = 1..16, BLOCK_M >= 16).
 //
 // Layout of the work:
-//   * a workgroup is 4 waves; all 64 lanes of a wave sit on one packed row and
-//     4 consecutive columns each (one global_load_dwordx4 = 256 columns = 1 KiB);
-//   * the 4 waves split the workgroup's packed rows into contiguous sub-blocks,
-//     so each wave's group index changes every G/8 rows (uniform branch);
-//   * activations are wave-uniform per row and are read through the scalar
-//     cache into SGPRs (8 halves per row and activation row);
-//   * dequant is the packed-fp16 magic-number form (w4a16_device.h) and the dot
+//   * a workgroup (4 waves) owns a block of CW = 4*CWL consecutive columns; in a
+//     wave, CWL lanes cover one packed row (global_load_dwordx4 = 4 columns per
+//     lane) and the wave's 64/CWL row-lanes sit on different packed rows, so a
+//     narrow block still gives each CU a full 1 KiB per wave-load;
+//   * each row-lane owns a contiguous run of packed rows, so its group index
+//     (scale/zero reload) changes every G/8 rows; the weight loads of the next 8
+//     rows are issued before the current 8 are consumed;
+//   * activations come from global memory (L1-resident: each 16-byte octet is
+//     shared by the CWL lanes of a row);
+//   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
 //     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
-//   * the 4 waves' partial sums meet in LDS in a fixed order; with a k-split
-//     (grid.y > 1) each workgroup writes fp32 partials and the last workgroup of
-//     a column block (atomic counter) sums the splits in split order, so the
-//     result does not depend on scheduling.  The last workgroup resets its
-//     counter, leaving the workspace ready for the next call.
+//   * reduction over row-lanes: a fixed xor-shuffle tree inside the wave, then the
+//     4 waves in order through LDS -- deterministic;
+//   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
+//     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
+//     so that neighbouring 64-byte row segments share that XCD's L2 lines;
+//   * optional split-K (only when N is too narrow to fill the device): each
+//     workgroup writes fp32 partials; the last workgroup of a column block (atomic
+//     counter) sums the splits in split order and resets the counter.
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -25,29 +31,39 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kUnroll = 8;
+constexpr int kBatch = 8;
 
-template <int MT>
+template <int MT, int CWL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
     float* __restrict__ part, uint32_t* __restrict__ cnt, int N, int K, int G, int rows_per_wg,
-    int S) {
-  __shared__ float red[kWaves][MT][kGemvCols];
+    int S, int nblk) {
+  constexpr int RW = 64 / CWL;      // row-lanes per wave
+  constexpr int RL = kWaves * RW;   // row-lanes per workgroup
+  constexpr int CW = 4 * CWL;       // columns per workgroup
+  __shared__ float red[kWaves][MT][CW];
   __shared__ int s_last;
+
+  // XCD-aware block order (see header comment).
+  const int nb = (int)gridDim.x;
+  int lin = (int)blockIdx.x;
+  if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
+  const int cb = lin % nblk;
+  const int sk = lin / nblk;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int cb = blockIdx.x;
-  const int sk = blockIdx.y;
-  const int n = cb * kGemvCols + lane * 4;
+  const int cq = lane % CWL;
+  const int rl = wave * RW + lane / CWL;
+  const int n = cb * CW + 4 * cq;
   const bool nv = n < N;
   const int KP = K >> 3;
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
-  const int per_wave = (re - rb + kWaves - 1) / kWaves;
-  const int wb = min(re, rb + wave * per_wave);
-  const int we = min(re, wb + per_wave);
+  const int per = (re - rb + RL - 1) / RL;
+  const int lb = min(re, rb + rl * per);
+  const int le = min(re, lb + per);
 
   float acc[MT][4];
 #pragma unroll
@@ -55,20 +71,25 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
 
-  int gcur = -1;
-  ColQ cq[4];
-  for (int r0 = wb; r0 < we; r0 += kUnroll) {
-    uint4 wv[kUnroll];
+  uint4 cur[kBatch], nxt[kBatch];
+  auto load_batch = [&](int r0, uint4* dst) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const int r = r0 + u;
-      wv[u] = (nv && r < we) ? *reinterpret_cast<const uint4*>(QW + (size_t)r * N + n)
-                             : make_uint4(0u, 0u, 0u, 0u);
+      dst[u] = (nv && r < le) ? *reinterpret_cast<const uint4*>(QW + (size_t)r * N + n)
+                              : make_uint4(0u, 0u, 0u, 0u);
     }
+  };
+
+  int gcur = -1;
+  ColQ cq4[4];
+  load_batch(lb, cur);
+  for (int r0 = lb; r0 < le; r0 += kBatch) {
+    if (r0 + kBatch < le) load_batch(r0 + kBatch, nxt);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const int r = r0 + u;
-      if (r >= we) break;
+      if (r >= le) break;
       const int g = (r * 8) / G;
       if (g != gcur) {
         gcur = g;
@@ -78,20 +99,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
           sv = *reinterpret_cast<const uint2*>(SC + (size_t)g * N + n);
           zv = *reinterpret_cast<const uint2*>(ZR + (size_t)g * N + n);
         }
-        cq[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
-        cq[1] = make_colq(sv.x >> 16, zv.x >> 16);
-        cq[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
-        cq[3] = make_colq(sv.y >> 16, zv.y >> 16);
+        cq4[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
+        cq4[1] = make_colq(sv.x >> 16, zv.x >> 16);
+        cq4[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
+        cq4[3] = make_colq(sv.y >> 16, zv.y >> 16);
       }
       f16x2 d[4][4];
-      dq_word(wv[u].x, cq[0], d[0]);
-      dq_word(wv[u].y, cq[1], d[1]);
-      dq_word(wv[u].z, cq[2], d[2]);
-      dq_word(wv[u].w, cq[3], d[3]);
+      dq_word(cur[u].x, cq4[0], d[0]);
+      dq_word(cur[u].y, cq4[1], d[1]);
+      dq_word(cur[u].z, cq4[2], d[2]);
+      dq_word(cur[u].w, cq4[3], d[3]);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const uint4 xr = *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)r * 8);
-        const uint4 xp = perm_pairs(xr);
+        const uint4 xp =
+            perm_pairs(*reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)r * 8));
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           float a = acc[m][c];
@@ -103,23 +124,37 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
         }
       }
     }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
   }
 
+  // Sum the wave's row-lanes (lanes with equal cq) with a fixed xor tree.
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
-    *reinterpret_cast<float4*>(&red[wave][m][lane * 4]) =
-        make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+  for (int off = CWL; off < 64; off <<= 1)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[m][c] += __shfl_xor(acc[m][c], off);
+  if (lane < CWL) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      *reinterpret_cast<float4*>(&red[wave][m][4 * cq]) =
+          make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+  }
   __syncthreads();
 
   const int t = threadIdx.x;
-  const int col = cb * kGemvCols + t;
-  const bool cv = col < N;
+  const int col = cb * CW + t;
+  const bool cv = (t < CW) && (col < N);
   float v[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
-    float s = red[0][m][t];
+    float s = 0.0f;
+    if (t < CW) {
+      s = red[0][m][t];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) s += red[w][m][t];
+      for (int w = 1; w < kWaves; ++w) s += red[w][m][t];
+    }
     v[m] = s;
   }
 
@@ -160,28 +195,39 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   if (t == 0) cnt[cb] = 0u;
 }
 
-template <int MT>
-hipError_t launch_mt(const GemmArgs& a, int split, void* ws, hipStream_t st) {
-  const int nblk = (a.N + kGemvCols - 1) / kGemvCols;
+template <int MT, int CWL>
+hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
+  constexpr int CW = 4 * CWL;
+  const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
-  const int S = split;
   uint32_t* cnt = nullptr;
   float* part = nullptr;
-  if (S > 1) {
+  if (split > 1) {
     cnt = static_cast<uint32_t*>(ws);
-    const size_t cnt_bytes = ((size_t)nblk * 4 + 255) / 256 * 256;
-    part = reinterpret_cast<float*>(static_cast<char*>(ws) + cnt_bytes);
+    part = reinterpret_cast<float*>(static_cast<char*>(ws) + kGemvCounterBytes);
   }
-  dim3 grid(nblk, S);
-  hipLaunchKernelGGL(gemv_kernel<MT>, grid, dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((gemv_kernel<MT, CWL>), dim3(nblk * split), dim3(kThreads), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), part, cnt, a.N, a.K,
-                     a.G, rows, S);
+                     a.G, rows, split, nblk);
   return hipGetLastError();
 }
 
+template <int MT>
+hipError_t launch_mt(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
+  switch (cols) {
+    case 16: return launch_cwl<MT, 4>(a, split, ws, st);
+    case 32: return launch_cwl<MT, 8>(a, split, ws, st);
+    case 64: return launch_cwl<MT, 16>(a, split, ws, st);
+    case 256: return launch_cwl<MT, 64>(a, split, ws, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
+
+bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 || cols == 256; }
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;
@@ -191,21 +237,19 @@ int gemv_rows_per_split(int K, int split) {
 size_t gemv_workspace_bytes(int M, int N, int K, int split) {
   (void)K;
   if (split <= 1) return 0;
-  const size_t nblk = (size_t)(N + kGemvCols - 1) / kGemvCols;
-  const size_t cnt_bytes = (nblk * 4 + 255) / 256 * 256;
-  return cnt_bytes + (size_t)split * (size_t)M * (size_t)N * sizeof(float);
+  return kGemvCounterBytes + (size_t)split * (size_t)M * (size_t)N * sizeof(float);
 }
 
-hipError_t launch_gemv(const GemmArgs& a, int split, void* ws, hipStream_t st) {
+hipError_t launch_gemv(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
   switch (a.M) {
-    case 1: return launch_mt<1>(a, split, ws, st);
-    case 2: return launch_mt<2>(a, split, ws, st);
-    case 3: return launch_mt<3>(a, split, ws, st);
-    case 4: return launch_mt<4>(a, split, ws, st);
-    case 5: return launch_mt<5>(a, split, ws, st);
-    case 6: return launch_mt<6>(a, split, ws, st);
-    case 7: return launch_mt<7>(a, split, ws, st);
-    case 8: return launch_mt<8>(a, split, ws, st);
+    case 1: return launch_mt<1>(a, cols, split, ws, st);
+    case 2: return launch_mt<2>(a, cols, split, ws, st);
+    case 3: return launch_mt<3>(a, cols, split, ws, st);
+    case 4: return launch_mt<4>(a, cols, split, ws, st);
+    case 5: return launch_mt<5>(a, cols, split, ws, st);
+    case 6: return launch_mt<6>(a, cols, split, ws, st);
+    case 7: return launch_mt<7>(a, cols, split, ws, st);
+    case 8: return launch_mt<8>(a, cols, split, ws, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -19,13 +19,18 @@ struct GemmArgs {
   int M, N, K, G;
 };
 
-// Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  `split` k-splits; when split > 1
-// `ws` holds the counters + fp32 partials described by gemv_workspace_bytes().
+// Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
+// consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; with
+// split > 1, `ws` holds the counters + fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
-constexpr int kGemvCols = 256;
+// Split-K counters live in a fixed-size region at the start of the workspace so
+// that no call's fp32 partials ever overlap another call's counters.
+constexpr int kGemvMaxCounterBlocks = 16384;
+constexpr size_t kGemvCounterBytes = (size_t)kGemvMaxCounterBlocks * 4;
+bool gemv_cols_valid(int cols);
 size_t gemv_workspace_bytes(int M, int N, int K, int split);
 int gemv_rows_per_split(int K, int split);
-hipError_t launch_gemv(const GemmArgs& a, int split, void* ws, hipStream_t st);
+hipError_t launch_gemv(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st);
 
 // Prefill GEMM on MFMA (v_mfma_f32_32x32x16_f16).  `cfg` picks the tile shape.
 struct MfmaTile {
