@@ -54,7 +54,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int64_t G) {
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 bool gemv_applicable(int64_t M, int64_t N, int64_t G) {
-  return M >= 1 && M <= kGemvMaxM && N % 4 == 0 && G % 8 == 0;
+  return M >= 1 && M <= kGemvMaxM && N % 4 == 0 && G % 32 == 0;
 }
 bool mfma_applicable(int64_t N, int64_t G) { return N % 4 == 0 && G % 32 == 0; }
 

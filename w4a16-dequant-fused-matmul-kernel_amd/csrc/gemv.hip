@@ -6,20 +6,23 @@
 // Layout of the work:
 //   * a workgroup (4 waves) owns a block of CW = 4*CWL consecutive columns; in a
 //     wave, CWL lanes cover one packed row (global_load_dwordx4 = 4 columns per
-//     lane) and the wave's 64/CWL row-lanes sit on different packed rows, so a
-//     narrow block still gives each CU a full 1 KiB per wave-load;
-//   * each row-lane owns a contiguous run of packed rows, so its group index
-//     (scale/zero reload) changes every G/8 rows; the weight loads of the next 8
-//     rows are issued before the current 8 are consumed;
-//   * activations come from global memory (L1-resident: each 16-byte octet is
-//     shared by the CWL lanes of a row);
+//     lane) and the wave's 64/CWL row-lanes sit on different packed rows;
+//   * each row-lane owns a contiguous run of packed rows, cut into batches of 8
+//     rows aligned to absolute row multiples of 8 (64 k).  With G % 32 == 0 each
+//     half-batch (4 rows = 32 k) lies in one quantisation group, so a batch
+//     needs at most two scale/zero loads per lane;
+//   * the only vector-memory loads in the main loop are weights and scales, and
+//     all of batch i+1's are issued before batch i is consumed: the in-order
+//     vmcnt counter then waits exactly for batch i.  Activations are staged
+//     once into LDS (permuted to the dequantiser's pair order) and read with
+//     ds_read_b128, which uses the separate LDS counter;
 //   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
 //     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
 //   * reduction over row-lanes: a fixed xor-shuffle tree inside the wave, then the
 //     4 waves in order through LDS -- deterministic;
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
-//     so that neighbouring 64-byte row segments share that XCD's L2 lines;
+//     so that neighbouring row segments share that XCD's L2 lines;
 //   * optional split-K (only when N is too narrow to fill the device): each
 //     workgroup writes fp32 partials; the last workgroup of a column block (atomic
 //     counter) sums the splits in split order and resets the counter.
@@ -31,7 +34,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kBatch = 8;
+constexpr int kBatch = 8;                 // packed rows per batch (64 k)
+constexpr int kXsEntries = 2048;          // LDS activation slots (16 B each): 32 KiB
 
 template <int MT, int CWL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(
@@ -39,9 +43,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
     float* __restrict__ part, uint32_t* __restrict__ cnt, int N, int K, int G, int rows_per_wg,
     int S, int nblk) {
-  constexpr int RW = 64 / CWL;      // row-lanes per wave
-  constexpr int RL = kWaves * RW;   // row-lanes per workgroup
-  constexpr int CW = 4 * CWL;       // columns per workgroup
+  constexpr int RW = 64 / CWL;             // row-lanes per wave
+  constexpr int RL = kWaves * RW;          // row-lanes per workgroup
+  constexpr int CW = 4 * CWL;              // columns per workgroup
+  constexpr int CHUNK = kXsEntries / MT / kBatch * kBatch;   // packed rows of X per stage
+  static_assert(CHUNK % kBatch == 0, "chunk must hold whole batches");
+  __shared__ uint4 xs[MT * CHUNK];
   __shared__ float red[kWaves][MT][CW];
   __shared__ int s_last;
 
@@ -52,8 +59,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int cb = lin % nblk;
   const int sk = lin / nblk;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cq = lane % CWL;
   const int rl = wave * RW + lane / CWL;
   const int n = cb * CW + 4 * cq;
@@ -61,9 +69,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int KP = K >> 3;
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
-  const int per = (re - rb + RL - 1) / RL;
-  const int lb = min(re, rb + rl * per);
-  const int le = min(re, lb + per);
+  const bool g64 = (G & 63) == 0;          // one group per batch
 
   float acc[MT][4];
 #pragma unroll
@@ -71,61 +77,98 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
 
-  uint4 cur[kBatch], nxt[kBatch];
-  auto load_batch = [&](int r0, uint4* dst) {
+  struct Batch {
+    uint4 w[kBatch];
+    uint2 s0, z0, s1, z1;
+  };
+  auto load_batch = [&](int r0, int le, Batch& b) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int r = r0 + u;
-      dst[u] = (nv && r < le) ? *reinterpret_cast<const uint4*>(QW + (size_t)r * N + n)
+      b.w[u] = (nv && r < le) ? *reinterpret_cast<const uint4*>(QW + (size_t)r * N + n)
                               : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const int g0 = (r0 * 8) / G;
+    const int g1 = g64 ? g0 : ((r0 + 4) * 8) / G;
+    const bool ok1 = nv && (r0 + 4) < le;
+    b.s0 = nv ? *reinterpret_cast<const uint2*>(SC + (size_t)g0 * N + n) : make_uint2(0u, 0u);
+    b.z0 = nv ? *reinterpret_cast<const uint2*>(ZR + (size_t)g0 * N + n) : make_uint2(0u, 0u);
+    if (!g64) {
+      b.s1 = ok1 ? *reinterpret_cast<const uint2*>(SC + (size_t)g1 * N + n) : b.s0;
+      b.z1 = ok1 ? *reinterpret_cast<const uint2*>(ZR + (size_t)g1 * N + n) : b.z0;
+    } else {
+      b.s1 = b.s0;
+      b.z1 = b.z0;
     }
   };
 
-  int gcur = -1;
-  ColQ cq4[4];
-  load_batch(lb, cur);
-  for (int r0 = lb; r0 < le; r0 += kBatch) {
-    if (r0 + kBatch < le) load_batch(r0 + kBatch, nxt);
+  for (int c0 = rb; c0 < re; c0 += CHUNK) {
+    const int c1 = min(re, c0 + CHUNK);
+    const int nr = c1 - c0;
+    // this row-lane's rows in the chunk: 8-row aligned run
+    const int per = ((nr + RL - 1) / RL + kBatch - 1) / kBatch * kBatch;
+    const int lb = min(c1, c0 + rl * per);
+    const int le = min(c1, lb + per);
+
+    // Stage X rows [c0, c1) into LDS (loads issued before the first weight batch).
+    if (c0 != rb) __syncthreads();   // previous chunk's readers are done
+    uint4 xv[(MT * CHUNK + kThreads - 1) / kThreads];
+    constexpr int XPT = (MT * CHUNK + kThreads - 1) / kThreads;
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int r = r0 + u;
-      if (r >= le) break;
-      const int g = (r * 8) / G;
-      if (g != gcur) {
-        gcur = g;
-        uint2 sv = make_uint2(0x3C003C00u, 0x3C003C00u);
-        uint2 zv = make_uint2(0u, 0u);
-        if (nv) {
-          sv = *reinterpret_cast<const uint2*>(SC + (size_t)g * N + n);
-          zv = *reinterpret_cast<const uint2*>(ZR + (size_t)g * N + n);
-        }
+    for (int i = 0; i < XPT; ++i) {
+      const int idx = tid + i * kThreads;
+      const int m = idx / CHUNK, r = idx % CHUNK;
+      xv[i] = (m < MT && r < nr)
+                  ? *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)(c0 + r) * 8)
+                  : make_uint4(0u, 0u, 0u, 0u);
+    }
+    Batch cur, nxt;
+    if (lb < le) load_batch(lb, le, cur);
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < MT * CHUNK) xs[idx] = perm_pairs(xv[i]);
+    }
+    __syncthreads();
+
+    for (int r0 = lb; r0 < le; r0 += kBatch) {
+      if (r0 + kBatch < le) load_batch(r0 + kBatch, le, nxt);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint2 sv = h ? cur.s1 : cur.s0;
+        const uint2 zv = h ? cur.z1 : cur.z0;
+        ColQ cq4[4];
         cq4[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
         cq4[1] = make_colq(sv.x >> 16, zv.x >> 16);
         cq4[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
         cq4[3] = make_colq(sv.y >> 16, zv.y >> 16);
-      }
-      f16x2 d[4][4];
-      dq_word(cur[u].x, cq4[0], d[0]);
-      dq_word(cur[u].y, cq4[1], d[1]);
-      dq_word(cur[u].z, cq4[2], d[2]);
-      dq_word(cur[u].w, cq4[3], d[3]);
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const uint4 xp =
-            perm_pairs(*reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)r * 8));
+        for (int uu = 0; uu < kBatch / 2; ++uu) {
+          const int u = h * (kBatch / 2) + uu;
+          const int r = r0 + u;
+          if (r >= le) break;
+          f16x2 d[4][4];
+          dq_word(cur.w[u].x, cq4[0], d[0]);
+          dq_word(cur.w[u].y, cq4[1], d[1]);
+          dq_word(cur.w[u].z, cq4[2], d[2]);
+          dq_word(cur.w[u].w, cq4[3], d[3]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float a = acc[m][c];
-          a = __builtin_amdgcn_fdot2(d[c][0], as_h2(xp.x), a, false);
-          a = __builtin_amdgcn_fdot2(d[c][1], as_h2(xp.y), a, false);
-          a = __builtin_amdgcn_fdot2(d[c][2], as_h2(xp.z), a, false);
-          a = __builtin_amdgcn_fdot2(d[c][3], as_h2(xp.w), a, false);
-          acc[m][c] = a;
+          for (int m = 0; m < MT; ++m) {
+            const uint4 xp = xs[m * CHUNK + (r - c0)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              float a = acc[m][c];
+              a = __builtin_amdgcn_fdot2(d[c][0], as_h2(xp.x), a, false);
+              a = __builtin_amdgcn_fdot2(d[c][1], as_h2(xp.y), a, false);
+              a = __builtin_amdgcn_fdot2(d[c][2], as_h2(xp.z), a, false);
+              a = __builtin_amdgcn_fdot2(d[c][3], as_h2(xp.w), a, false);
+              acc[m][c] = a;
+            }
+          }
         }
       }
+      cur = nxt;
     }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
   }
 
   // Sum the wave's row-lanes (lanes with equal cq) with a fixed xor tree.
@@ -143,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   }
   __syncthreads();
 
-  const int t = threadIdx.x;
+  const int t = tid;
   const int col = cb * CW + t;
   const bool cv = (t < CW) && (col < N);
   float v[MT];
@@ -231,7 +274,9 @@ bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 |
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;
-  return (KP + split - 1) / split;
+  // whole 8-row batches per split keep every batch inside the batch alignment
+  const int rows = (KP + split - 1) / split;
+  return (rows + kBatch - 1) / kBatch * kBatch;
 }
 
 size_t gemv_workspace_bytes(int M, int N, int K, int split) {
