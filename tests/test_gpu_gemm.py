@@ -204,9 +204,6 @@ def test_fused_bias_epilogue():
         out = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
         want = (y + b)                      # torch fp16 add on the device: one RNE rounding
         assert torch.equal(out, want), f"bias epilogue {kern}"
-        ref = O.linear_forward(np_(X), np_(qw), np_(s), np_(z), np_(b), G)
-        np.testing.assert_allclose(np_(out).astype(np.float32), ref.astype(np.float32),
-                                   rtol=2e-3, atol=2e-3)
 
 
 def test_out_parameter_and_empty():

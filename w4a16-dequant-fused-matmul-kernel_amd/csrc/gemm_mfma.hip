@@ -14,15 +14,20 @@
 //     MFMAs that cover columns {4j + c}; a wave's 4 MFMAs cover 128 columns;
 //   * dequant yields k in pair order (0,4,1,5,2,6,3,7); the activation octets are
 //     permuted the same way when they are written to LDS, so A and B agree on k;
-//   * K advances 64 per step, LDS double-buffered with one barrier per step,
-//     next step's A/B/scale loads issued before the current step's MFMAs;
+//   * all global traffic uses buffer loads: the per-step k offset rides in an
+//     SGPR, and rows past M / columns past N read as zero through the buffer
+//     range check instead of branches;
+//   * K advances 64 per step with two register stages used ping-pong (no copies)
+//     and a double-buffered LDS activation tile, one barrier per step; the next
+//     step's loads are issued before the current step's MFMAs;
 //   * LDS rows are padded to 144 bytes so the ds_read_b128 of 16 rows x 16 B
 //     hits 64 distinct banks;
 //   * epilogue: lane l holds 4 consecutive columns per output row, rounded to
 //     fp16 (RNE) and stored as one 8-byte write; optional fp16 bias add
 //     reproduces W4A16Linear's separate `y + bias` (linear.py:90-91).
 // Requirements (checked by the caller): N % 4 == 0, G % 32 == 0, K % G == 0,
-// 16-byte aligned x/qweight, 8-byte aligned scales/zeros/y/bias.
+// 16-byte aligned x/qweight, 8-byte aligned scales/zeros/y/bias, and x, qweight,
+// scales, zeros each below 2 GiB.  KTAIL handles K % 64 == 32.
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -32,7 +37,7 @@ namespace {
 constexpr int kBK = 64;
 constexpr int kLdsRow = 9;  // uint4 per LDS row: 8 octets + 1 pad
 
-template <int WMT, int WAVES_M, int WAVES_N>
+template <int WMT, int WAVES_M, int WAVES_N, bool KTAIL>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
@@ -60,111 +65,139 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
   const int KT = (K + kBK - 1) / kBK;
   const int NG = K / G;
 
+  const MagicRegs mg = make_magic();
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
+
+  // per-thread A slots (row, octet) and their byte offsets at k = 0
+  uint32_t a_off[A_PER_T];
+#pragma unroll
+  for (int i = 0; i < A_PER_T; ++i) {
+    const int o = tid + i * NT;
+    const int gm = m0 + (o >> 3);
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+  }
+  uint32_t b_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    b_off[s] = nv ? ((uint32_t)(2 * s + lhi) * (uint32_t)N + (uint32_t)ncol) * 4u : kOobOffset;
+  const uint32_t s_off = nv ? (uint32_t)ncol * 2u : kOobOffset;
+
+  struct Stage {
+    uint4 a[A_PER_T];
+    uint4 b[4];
+    uint2 sc[2], zr[2];
+  };
+
+  auto load = [&](int kt, Stage& st) {
+    const uint32_t ak = uniform((uint32_t)kt * (uint32_t)(kBK * 2));
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      uint32_t off = a_off[i];
+      if (KTAIL && kt * kBK + ((tid + i * NT) & 7) * 8 >= K) off = kOobOffset;
+      st.a[i] = buf_load16(rx, off, ak);
+    }
+    const uint32_t bk = uniform((uint32_t)kt * 8u * (uint32_t)N * 4u);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (!KTAIL || kt * kBK + 16 * s < K)
+        st.b[s] = buf_load16(rw, b_off[s], bk);
+      else
+        st.b[s] = make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = min((kt * kBK + 32 * h) / G, NG - 1);
+      const uint32_t gs = uniform((uint32_t)g * (uint32_t)N * 2u);
+      st.sc[h] = buf_load8(rs, s_off, gs);
+      st.zr[h] = buf_load8(rz, s_off, gs);
+    }
+  };
+
+  auto store_a = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int o = tid + i * NT;
+      As[buf][(o >> 3) * kLdsRow + (o & 7)] = perm_pairs(st.a[i]);
+    }
+  };
+
   f32x16 acc[WMT][4];
 #pragma unroll
   for (int i = 0; i < WMT; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[i][c] = f32x16{};
 
-  uint4 ra[A_PER_T];
-  uint4 rb[4], nb[4];
-  uint2 rs[2], rz[2], ns[2], nz[2];
-
-  auto load_a = [&](int kt) {
+  const int arow = wm * (32 * WMT) + l32;
+  // One k-step: four 16-k sub-steps.  Sub-step s+1's B dequant (VALU) and A
+  // fragment reads (LDS) are issued alongside sub-step s's MFMAs; a scheduling
+  // barrier between sub-steps keeps the compiler from hoisting further ahead
+  // (which would raise register pressure past the 512-VGPR budget).
+  auto compute = [&](const Stage& st, int buf, int kt) {
+    const int nsub = (KTAIL && kt * kBK + 32 >= K) ? 2 : 4;
+    ColQ cq[2][4];
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int o = tid + i * NT;
-      const int row = o >> 3, oct = o & 7;
-      const int gm = m0 + row;
-      const int k = kt * kBK + oct * 8;
-      ra[i] = (gm < M && k < K) ? *reinterpret_cast<const uint4*>(X + (size_t)gm * K + k)
-                                : make_uint4(0u, 0u, 0u, 0u);
+    for (int h = 0; h < 2; ++h) {
+      cq[h][0] = make_colq(st.sc[h].x & 0xFFFFu, st.zr[h].x & 0xFFFFu);
+      cq[h][1] = make_colq(st.sc[h].x >> 16, st.zr[h].x >> 16);
+      cq[h][2] = make_colq(st.sc[h].y & 0xFFFFu, st.zr[h].y & 0xFFFFu);
+      cq[h][3] = make_colq(st.sc[h].y >> 16, st.zr[h].y >> 16);
     }
-  };
-  auto store_a = [&](int buf) {
+    const uint4* A = &As[buf][arow * kLdsRow + lhi];
+    auto dequant = [&](int s, f16x8 bf[4]) {
+      const uint32_t words[4] = {st.b[s].x, st.b[s].y, st.b[s].z, st.b[s].w};
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int o = tid + i * NT;
-      const int row = o >> 3, oct = o & 7;
-      As[buf][row * kLdsRow + oct] = perm_pairs(ra[i]);
-    }
-  };
-  auto load_b = [&](int kt, uint4* dst) {
+      for (int c = 0; c < 4; ++c) {
+        f16x2 d[4];
+        dq_word_fast(words[c], cq[s >> 1][c], mg, d);
+        bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
+      }
+    };
+    f16x8 af[2][WMT], bf[2][4];
+#pragma unroll
+    for (int mt = 0; mt < WMT; ++mt) af[0][mt] = __builtin_bit_cast(f16x8, A[mt * 32 * kLdsRow]);
+    dequant(0, bf[0]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int pr = kt * 8 + 2 * s + lhi;
-      dst[s] = (nv && pr < KP) ? *reinterpret_cast<const uint4*>(QW + (size_t)pr * N + ncol)
-                               : make_uint4(0u, 0u, 0u, 0u);
-    }
-  };
-  auto load_s = [&](int kt, uint2* sd, uint2* zd) {
+      if (s >= nsub) break;
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < nsub) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int g = min((kt * kBK + 32 * h) / G, NG - 1);
-      if (nv) {
-        sd[h] = *reinterpret_cast<const uint2*>(SC + (size_t)g * N + ncol);
-        zd[h] = *reinterpret_cast<const uint2*>(ZR + (size_t)g * N + ncol);
-      } else {
-        sd[h] = make_uint2(0x3C003C00u, 0x3C003C00u);
-        zd[h] = make_uint2(0u, 0u);
+        for (int mt = 0; mt < WMT; ++mt)
+          af[nxt][mt] = __builtin_bit_cast(f16x8, A[mt * 32 * kLdsRow + 2 * (s + 1)]);
+        dequant(s + 1, bf[nxt]);
       }
+#pragma unroll
+      for (int mt = 0; mt < WMT; ++mt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[mt][c] =
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mt], bf[cur][c], acc[mt][c], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  load_a(0);
-  load_b(0, rb);
-  load_s(0, rs, rz);
-  store_a(0);
+  Stage s0, s1;
+  load(0, s0);
+  store_a(s0, 0);
   __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = (kt + 1) < KT;
-    if (more) {
-      load_a(kt + 1);
-      load_b(kt + 1, nb);
-      load_s(kt + 1, ns, nz);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      ColQ cq[4];
-      cq[0] = make_colq(rs[h].x & 0xFFFFu, rz[h].x & 0xFFFFu);
-      cq[1] = make_colq(rs[h].x >> 16, rz[h].x >> 16);
-      cq[2] = make_colq(rs[h].y & 0xFFFFu, rz[h].y & 0xFFFFu);
-      cq[3] = make_colq(rs[h].y >> 16, rz[h].y >> 16);
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const int s = 2 * h + ss;
-        const uint32_t words[4] = {rb[s].x, rb[s].y, rb[s].z, rb[s].w};
-        f16x8 bf[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          f16x2 d[4];
-          dq_word(words[c], cq[c], d);
-          bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
-        }
-#pragma unroll
-        for (int mt = 0; mt < WMT; ++mt) {
-          const int row = wm * (32 * WMT) + mt * 32 + l32;
-          const f16x8 af = __builtin_bit_cast(f16x8, As[cur][row * kLdsRow + 2 * s + lhi]);
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[c], acc[mt][c], 0, 0, 0);
-        }
-      }
-    }
-    if (more) {
-      store_a(cur ^ 1);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) rb[s] = nb[s];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        rs[h] = ns[h];
-        rz[h] = nz[h];
-      }
-    }
+  // Pairs of steps with ping-pong stages; a single loop exit keeps the
+  // accumulators in one set of registers.
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    load(kt + 1, s1);
+    compute(s0, 0, kt);
+    store_a(s1, 1);
+    __syncthreads();
+    const bool more = kt + 2 < KT;
+    if (more) load(kt + 2, s0);
+    compute(s1, 1, kt + 1);
+    if (more) store_a(s0, 0);
     __syncthreads();
   }
+  if (kt < KT) compute(s0, 0, kt);   // odd step count: the last step sits in s0 / buffer 0
 
   if (!nv) return;
   f16 bv[4] = {(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};
@@ -203,10 +236,19 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 128 * WAVES_N;
   dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N>), grid, dim3(64 * WAVES_M * WAVES_N), 0,
-                     st, static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+  dim3 block(64 * WAVES_M * WAVES_N);
+  const f16* x = static_cast<const f16*>(a.x);
+  const uint32_t* qw = reinterpret_cast<const uint32_t*>(a.qw);
+  const uint16_t* sc = static_cast<const uint16_t*>(a.sc);
+  const uint16_t* zr = static_cast<const uint16_t*>(a.zr);
+  const f16* bias = static_cast<const f16*>(a.bias);
+  f16* y = static_cast<f16*>(a.y);
+  if (a.K % kBK == 0)
+    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, false>), grid, block, 0, st, x, qw, sc,
+                       zr, bias, y, a.M, a.N, a.K, a.G);
+  else
+    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, true>), grid, block, 0, st, x, qw, sc,
+                       zr, bias, y, a.M, a.N, a.K, a.G);
   return hipGetLastError();
 }
 
@@ -215,12 +257,20 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 // cfg 0: 128 x 512 (4 waves along N, each 128 x 128)
 // cfg 1: 128 x 256 (2 x 2 waves, each 64 x 128)
 // cfg 2:  32 x 512 (4 waves along N, each 32 x 128)
+// cfg 3:  64 x 512 (4 waves along N, each 64 x 128)
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
     case 0: return {128, 512};
     case 1: return {128, 256};
-    default: return {32, 512};
+    case 2: return {32, 512};
+    default: return {64, 512};
   }
+}
+
+bool mfma_fits(int M, int N, int K, int G) {
+  const uint64_t xb = (uint64_t)M * K * 2, wb = (uint64_t)(K / 8) * N * 4,
+                 sb = (uint64_t)(K / G) * N * 2;
+  return xb < (1ull << 31) && wb < (1ull << 31) && sb < (1ull << 31);
 }
 
 hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
@@ -228,6 +278,7 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
     case 0: return launch_cfg<4, 1, 4>(a, st);
     case 1: return launch_cfg<2, 2, 2>(a, st);
     case 2: return launch_cfg<1, 1, 4>(a, st);
+    case 3: return launch_cfg<2, 1, 4>(a, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -70,6 +70,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
   const bool g64 = (G & 63) == 0;          // one group per batch
+  const MagicRegs mg = make_magic();
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)(K / G) * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)(K / G) * (uint32_t)N * 2u);
+  const uint32_t row_bytes = (uint32_t)N * 4u;
+  const uint32_t s_voff = (uint32_t)n * 2u;
 
   float acc[MT][4];
 #pragma unroll
@@ -81,24 +87,68 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     uint4 w[kBatch];
     uint2 s0, z0, s1, z1;
   };
+  // Rows r0..r0+7 of this lane's run [.., le).  Row u rides in the SGPR offset;
+  // rows at or past `le` (only in a run's last batch) read as zero.
   auto load_batch = [&](int r0, int le, Batch& b) {
+    const uint32_t base = nv ? ((uint32_t)r0 * (uint32_t)N + (uint32_t)n) * 4u : kOobOffset;
+    if (r0 + kBatch <= le) {
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int r = r0 + u;
-      b.w[u] = (nv && r < le) ? *reinterpret_cast<const uint4*>(QW + (size_t)r * N + n)
-                              : make_uint4(0u, 0u, 0u, 0u);
+      for (int u = 0; u < kBatch; ++u) b.w[u] = buf_load16(rw, base, uniform((uint32_t)u * row_bytes));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        b.w[u] = buf_load16(rw, r0 + u < le ? base : kOobOffset, uniform((uint32_t)u * row_bytes));
     }
+    // the group differs between row-lanes: its offset goes in the VGPR operand
     const int g0 = (r0 * 8) / G;
-    const int g1 = g64 ? g0 : ((r0 + 4) * 8) / G;
-    const bool ok1 = nv && (r0 + 4) < le;
-    b.s0 = nv ? *reinterpret_cast<const uint2*>(SC + (size_t)g0 * N + n) : make_uint2(0u, 0u);
-    b.z0 = nv ? *reinterpret_cast<const uint2*>(ZR + (size_t)g0 * N + n) : make_uint2(0u, 0u);
+    const uint32_t so0 = nv ? s_voff + (uint32_t)g0 * (uint32_t)N * 2u : kOobOffset;
+    b.s0 = buf_load8(rs, so0, 0u);
+    b.z0 = buf_load8(rz, so0, 0u);
     if (!g64) {
-      b.s1 = ok1 ? *reinterpret_cast<const uint2*>(SC + (size_t)g1 * N + n) : b.s0;
-      b.z1 = ok1 ? *reinterpret_cast<const uint2*>(ZR + (size_t)g1 * N + n) : b.z0;
+      const int g1 = min(((r0 + 4) * 8) / G, K / G - 1);
+      const uint32_t so1 = nv ? s_voff + (uint32_t)g1 * (uint32_t)N * 2u : kOobOffset;
+      b.s1 = buf_load8(rs, so1, 0u);
+      b.z1 = buf_load8(rz, so1, 0u);
     } else {
       b.s1 = b.s0;
       b.z1 = b.z0;
+    }
+  };
+
+  auto process = [&](const Batch& b, int r0, int le, int c0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint2 sv = h ? b.s1 : b.s0;
+      const uint2 zv = h ? b.z1 : b.z0;
+      ColQ cq4[4];
+      cq4[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
+      cq4[1] = make_colq(sv.x >> 16, zv.x >> 16);
+      cq4[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
+      cq4[3] = make_colq(sv.y >> 16, zv.y >> 16);
+#pragma unroll
+      for (int uu = 0; uu < kBatch / 2; ++uu) {
+        const int u = h * (kBatch / 2) + uu;
+        const int r = r0 + u;
+        if (r >= le) break;
+        f16x2 d[4][4];
+        dq_word_fast(b.w[u].x, cq4[0], mg, d[0]);
+        dq_word_fast(b.w[u].y, cq4[1], mg, d[1]);
+        dq_word_fast(b.w[u].z, cq4[2], mg, d[2]);
+        dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const uint4 xp = xs[m * CHUNK + (r - c0)];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float a = acc[m][c];
+            a = __builtin_amdgcn_fdot2(d[c][0], as_h2(xp.x), a, false);
+            a = __builtin_amdgcn_fdot2(d[c][1], as_h2(xp.y), a, false);
+            a = __builtin_amdgcn_fdot2(d[c][2], as_h2(xp.z), a, false);
+            a = __builtin_amdgcn_fdot2(d[c][3], as_h2(xp.w), a, false);
+            acc[m][c] = a;
+          }
+        }
+      }
     }
   };
 
@@ -112,8 +162,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
 
     // Stage X rows [c0, c1) into LDS (loads issued before the first weight batch).
     if (c0 != rb) __syncthreads();   // previous chunk's readers are done
-    uint4 xv[(MT * CHUNK + kThreads - 1) / kThreads];
     constexpr int XPT = (MT * CHUNK + kThreads - 1) / kThreads;
+    uint4 xv[XPT];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int idx = tid + i * kThreads;
@@ -122,8 +172,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
                   ? *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)(c0 + r) * 8)
                   : make_uint4(0u, 0u, 0u, 0u);
     }
-    Batch cur, nxt;
-    if (lb < le) load_batch(lb, le, cur);
+    Batch ba, bb;
+    if (lb < le) load_batch(lb, le, ba);
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int idx = tid + i * kThreads;
@@ -131,43 +181,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     }
     __syncthreads();
 
-    for (int r0 = lb; r0 < le; r0 += kBatch) {
-      if (r0 + kBatch < le) load_batch(r0 + kBatch, le, nxt);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint2 sv = h ? cur.s1 : cur.s0;
-        const uint2 zv = h ? cur.z1 : cur.z0;
-        ColQ cq4[4];
-        cq4[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
-        cq4[1] = make_colq(sv.x >> 16, zv.x >> 16);
-        cq4[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
-        cq4[3] = make_colq(sv.y >> 16, zv.y >> 16);
-#pragma unroll
-        for (int uu = 0; uu < kBatch / 2; ++uu) {
-          const int u = h * (kBatch / 2) + uu;
-          const int r = r0 + u;
-          if (r >= le) break;
-          f16x2 d[4][4];
-          dq_word(cur.w[u].x, cq4[0], d[0]);
-          dq_word(cur.w[u].y, cq4[1], d[1]);
-          dq_word(cur.w[u].z, cq4[2], d[2]);
-          dq_word(cur.w[u].w, cq4[3], d[3]);
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            const uint4 xp = xs[m * CHUNK + (r - c0)];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              float a = acc[m][c];
-              a = __builtin_amdgcn_fdot2(d[c][0], as_h2(xp.x), a, false);
-              a = __builtin_amdgcn_fdot2(d[c][1], as_h2(xp.y), a, false);
-              a = __builtin_amdgcn_fdot2(d[c][2], as_h2(xp.z), a, false);
-              a = __builtin_amdgcn_fdot2(d[c][3], as_h2(xp.w), a, false);
-              acc[m][c] = a;
-            }
-          }
-        }
-      }
-      cur = nxt;
+    // two register batches used ping-pong: no copies between iterations
+    for (int r0 = lb; r0 < le; r0 += 2 * kBatch) {
+      if (r0 + kBatch < le) load_batch(r0 + kBatch, le, bb);
+      process(ba, r0, le, c0);
+      if (r0 + kBatch >= le) break;
+      if (r0 + 2 * kBatch < le) load_batch(r0 + 2 * kBatch, le, ba);
+      process(bb, r0 + kBatch, le, c0);
     }
   }
 

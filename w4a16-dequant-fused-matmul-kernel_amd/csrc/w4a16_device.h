@@ -47,6 +47,38 @@ __device__ __forceinline__ ColQ make_colq(uint16_t sbits, uint16_t zbits) {
   return c;
 }
 
+// (w & mask) | magic in one v_and_or_b32.  gfx9 VOP3 encodings take no literal
+// constants and read at most one SGPR, so the mask rides in an SGPR and the
+// magic in a VGPR that the caller materialises once (MagicRegs).
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t magic_vgpr) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(magic_vgpr));
+  return r;
+}
+
+// The two magic words in VGPRs.  Loaded through an opaque move so the compiler
+// keeps them live instead of re-materialising a constant for every use.
+struct MagicRegs {
+  uint32_t m1024, m64;
+};
+__device__ __forceinline__ MagicRegs make_magic() {
+  MagicRegs m;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m.m1024));
+  asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(m.m64));
+  return m;
+}
+
+// As dq_word with the unpack done in five instructions (one shift, four
+// v_and_or_b32); same results bit for bit.
+__device__ __forceinline__ void dq_word_fast(uint32_t w, const ColQ& c, const MagicRegs& mg,
+                                             f16x2 d[4]) {
+  const uint32_t t = w >> 8;
+  d[0] = (as_h2(and_or(w, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
+  d[1] = (as_h2(and_or(w, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
+  d[2] = (as_h2(and_or(t, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
+  d[3] = (as_h2(and_or(t, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
+}
+
 // Dequantise one packed word into four fp16 pairs in "pair order":
 //   d[0] = (w0, w4), d[1] = (w1, w5), d[2] = (w2, w6), d[3] = (w3, w7)
 // where w_j is the weight of row 8i + j.  Consumers permute the activations the
@@ -75,5 +107,28 @@ __device__ __forceinline__ uint4 perm_pairs(uint4 v) {
 }
 
 __device__ __forceinline__ f16 f32_to_f16(float x) { return (f16)x; }  // v_cvt_f16_f32, RNE
+
+// Buffer resource over [p, p + bytes): raw buffer loads outside the range return
+// zero (gfx9-family descriptor word 3 = 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// Byte offset that no buffer range contains: loads from it return zero.
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+// Wave-uniform value promised to the compiler (keeps buffer SGPR offsets scalar).
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// `soff` must be wave-uniform (it is an SGPR operand).
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2((uint32_t)v.x, (uint32_t)v.y);
+}
 
 }  // namespace w4a16
