@@ -50,7 +50,8 @@ enum w4a16_kernel {
   W4A16_KERNEL_AUTO = 0,
   W4A16_KERNEL_GEMV = 1, /* decode: VALU dot2, no MFMA, M <= 8, optional split-K    */
   W4A16_KERNEL_MFMA = 2, /* prefill: v_mfma_f32_32x32x16_f16, LDS-staged activations */
-  W4A16_KERNEL_SIMT = 3  /* sequential-k, one thread per output, any shape           */
+  W4A16_KERNEL_SIMT = 3, /* sequential-k, one thread per output, any shape           */
+  W4A16_KERNEL_SKINNY = 4 /* small batch: v_mfma_f32_16x16x32_f16, weights streamed   */
 };
 
 /* The launch a GEMM call will make.  Filled by w4a16_gemm_plan(). */

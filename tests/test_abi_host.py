@@ -132,9 +132,12 @@ def test_quant_entry_points_reject_bad_args(lib):
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
     (8, 28672, 4096, 128, "gemv"),
-    (9, 4096, 4096, 128, "mfma"),
+    (9, 4096, 4096, 128, "skinny"),
+    (64, 4096, 11008, 64, "skinny"),
+    (65, 4096, 4096, 128, "mfma"),
     (4096, 14336, 4096, 128, "mfma"),
-    (16, 4096, 4096, 32, "mfma"),
+    (16, 4096, 4096, 32, "skinny"),
+    (16, 4098, 4096, 32, "skinny"),   # any N
     (1, 4098, 4096, 128, "simt"),     # N % 4 != 0
     (64, 4096, 4096, 16, "simt"),     # G % 32 != 0 beyond the GEMV's M range
     (1, 8, 8, 4, "simt"),             # G = 4: words straddle groups

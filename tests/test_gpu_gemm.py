@@ -157,6 +157,25 @@ def test_mfma_tile_configs(M, K, N, G):
     assert _lib.KERNEL_NAMES[p.kernel] == "mfma"
 
 
+@pytest.mark.parametrize("M,K,N,G", [
+    (9, 96, 260, 32), (16, 4096, 4096, 128), (17, 160, 7, 32), (32, 11008, 1028, 64),
+    (33, 1024, 130, 32), (48, 4096, 516, 128), (64, 4096, 4100, 64), (1, 4096, 1000, 128),
+    (5, 320, 33, 32),
+])
+def test_skinny_path(M, K, N, G):
+    """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0."""
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+
+    log(f"skinny M={M} K={K} N={N} G={G}")
+    X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
+    p = plan_for(M, N, K, G, "skinny")
+    out = w4a16_matmul_planned(X, qw, s, z, G, p)
+    assert_gemm_close(out, _ref(X, qw, s, z, G), "skinny")
+    b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
+    outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
+    assert torch.equal(outb, out + b)
+
+
 @pytest.mark.parametrize("M,K,N,G", [(1, 64, 130, 32), (17, 96, 7, 32), (4, 24, 12, 12), (2, 8, 5, 4)])
 def test_simt_path_any_shape(M, K, N, G):
     """SIMT kernel: odd N, G not a multiple of 8."""
@@ -194,7 +213,8 @@ def test_fused_bias_epilogue():
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     for (M, K, N, G, kern) in [(1, 4096, 4096, 128, "gemv"), (4, 1024, 516, 32, "gemv"),
-                               (64, 1024, 1028, 32, "mfma"), (3, 64, 10, 32, "simt")]:
+                               (64, 1024, 1028, 32, "mfma"), (3, 64, 10, 32, "simt"),
+                               (24, 1024, 1028, 32, "skinny")]:
         log(f"bias {kern} M={M} K={K} N={N}")
         X, qw, s, z = _build_case(M, K, N, G, seed=7)
         b = (torch.randn(N) * 3).to(torch.float16).to(DEV)

@@ -57,6 +57,10 @@ bool gemv_applicable(int64_t M, int64_t N, int64_t G) {
   return M >= 1 && M <= kGemvMaxM && N % 4 == 0 && G % 32 == 0;
 }
 bool mfma_applicable(int64_t N, int64_t G) { return N % 4 == 0 && G % 32 == 0; }
+bool skinny_applicable(int64_t M, int64_t G) { return M >= 1 && M <= kSkinnyMaxM && G % 32 == 0; }
+bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
+  return operands_fit((int)M, (int)N, (int)K, (int)G);
+}
 
 // Widest column block that still gives every CU a workgroup; split K across
 // workgroups only when even 16-column blocks cannot fill the device.
@@ -91,9 +95,13 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   *p = w4a16_plan{};
   if (kernel == W4A16_KERNEL_AUTO && (M == 0 || N == 0 || K == 0)) kernel = W4A16_KERNEL_SIMT;
   if (kernel == W4A16_KERNEL_AUTO) {
-    if (gemv_applicable(M, N, G))
+    if (!fits(M, N, K, G))
+      kernel = W4A16_KERNEL_SIMT;
+    else if (gemv_applicable(M, N, G))
       kernel = W4A16_KERNEL_GEMV;
-    else if (M > kGemvMaxM && mfma_applicable(N, G))
+    else if (M <= kSkinnyMaxM && skinny_applicable(M, G))
+      kernel = W4A16_KERNEL_SKINNY;
+    else if (mfma_applicable(N, G))
       kernel = W4A16_KERNEL_MFMA;
     else
       kernel = W4A16_KERNEL_SIMT;
@@ -132,6 +140,13 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->grid_y = (M + t.bm - 1) / t.bm;
       return W4A16_OK;
     }
+    case W4A16_KERNEL_SKINNY:
+      if (!skinny_applicable(M, G)) return W4A16_ERR_BAD_PLAN;
+      p->tile_m = (int32_t)((M + 15) / 16 * 16);
+      p->tile_n = 16;
+      p->grid_x = (N + 15) / 16;
+      p->grid_y = 1;
+      return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
       p->tile_n = 64;
@@ -157,8 +172,8 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G};
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
-      if (!gemv_applicable(M, N, G) || p->split_k < 1 || p->split_k > K / 8 ||
-          !gemv_cols_valid(p->tile_n))
+      if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
+          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n))
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;
@@ -170,12 +185,19 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
       return to_status(launch_gemv(a, p->tile_n, p->split_k, ws, s));
     }
     case W4A16_KERNEL_MFMA: {
-      if (!mfma_applicable(N, G) || p->tile_cfg < 0 || p->tile_cfg >= kMfmaConfigs)
+      if (!mfma_applicable(N, G) || !fits(M, N, K, G) || p->tile_cfg < 0 ||
+          p->tile_cfg >= kMfmaConfigs)
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
           !aligned(y, 8) || (bias && !aligned(bias, 8)))
         return W4A16_ERR_BAD_PLAN;
       return to_status(launch_mfma(a, p->tile_cfg, s));
+    }
+    case W4A16_KERNEL_SKINNY: {
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G)) return W4A16_ERR_BAD_PLAN;
+      if (!aligned(x, 16) || !aligned(qw, 4) || !aligned(sc, 2) || !aligned(zr, 2))
+        return W4A16_ERR_BAD_PLAN;
+      return to_status(launch_skinny(a, s));
     }
     case W4A16_KERNEL_SIMT:
       return to_status(launch_simt(a, s));
@@ -225,7 +247,7 @@ int w4a16_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t group_size, int32_t
                     int32_t split_k, w4a16_plan* plan) {
   if (!plan) return W4A16_ERR_NULL_POINTER;
   if (int st = check_gemm_shape(M, N, K, group_size)) return st;
-  if (kernel < 0 || kernel > W4A16_KERNEL_SIMT || split_k < 0) return W4A16_ERR_BAD_PLAN;
+  if (kernel < 0 || kernel > W4A16_KERNEL_SKINNY || split_k < 0) return W4A16_ERR_BAD_PLAN;
   return make_plan(M, N, K, group_size, kernel, split_k, plan);
 }
 

@@ -267,11 +267,13 @@ MfmaTile mfma_tile(int cfg) {
   }
 }
 
-bool mfma_fits(int M, int N, int K, int G) {
+bool operands_fit(int M, int N, int K, int G) {
   const uint64_t xb = (uint64_t)M * K * 2, wb = (uint64_t)(K / 8) * N * 4,
                  sb = (uint64_t)(K / G) * N * 2;
   return xb < (1ull << 31) && wb < (1ull << 31) && sb < (1ull << 31);
 }
+
+bool mfma_fits(int M, int N, int K, int G) { return operands_fit(M, N, K, G); }
 
 hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
   switch (cfg) {

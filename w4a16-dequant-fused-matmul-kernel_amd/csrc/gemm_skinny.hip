@@ -1,0 +1,183 @@
+// Skinny-M W4A16 GEMM (9 <= M <= 64) on gfx950 matrix cores
+// (v_mfma_f32_16x16x32_f16), weights streamed from HBM.
+//
+// Replaces the small-batch regime of the reference's fused kernel
+// (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 with BLOCK_M = 16..64).
+//
+// At these M the GEMM is still bound by the weight stream, and a prefill tiling
+// (hundreds of rows per workgroup) leaves most CUs idle.  Here:
+//   * a workgroup owns 16 columns and the whole of K, so N = 4096 already gives
+//     256 workgroups and no cross-workgroup reduction is needed;
+//   * in v_mfma_f32_16x16x32_f16 lane l holds B[k = 8*(l/16)..+7][n = l%16]: one
+//     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA,
+//     reading 4 packed rows x 64 bytes with one dword load per lane;
+//   * the 4 waves split K into contiguous runs; each wave walks its run in
+//     batches of 8 k-steps (256 k) with two register batches used ping-pong, all
+//     loads of batch i+1 -- weights, scales, zeros and activations -- issued
+//     before batch i is consumed;
+//   * activations (MT x 16 rows) are read directly from global memory: the whole
+//     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
+//     the buffer range check;
+//   * dequant is the packed-fp16 magic-number form, then the pairs are put back
+//     in natural k order (4 v_perm per word) so activations need no permutation;
+//   * the 4 waves' 16x16 fp32 tiles are summed in LDS in wave order
+//     (deterministic) and rounded to fp16 once; optional fp16 bias add;
+//   * workgroup -> column block is XCD-aware (consecutive blocks share an XCD).
+// Requirements (checked by the caller): G % 32 == 0, K % G == 0, 16-byte
+// aligned x, and x, qweight, scales, zeros each below 2 GiB.  Any N.
+#include "w4a16_device.h"
+#include "w4a16_launch.h"
+
+namespace w4a16 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kBatch = 8;  // k-steps (32 k each) per batch
+
+template <int MT>
+__global__ __launch_bounds__(kThreads) void skinny_kernel(
+    const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
+    const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
+    int N, int K, int G, int nblk) {
+  __shared__ f32x4 red[kWaves][MT][64];
+
+  const int nb = (int)gridDim.x;
+  int lin = (int)blockIdx.x;
+  if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
+  const int cb = lin;
+  (void)nblk;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;       // column within the block
+  const int q = lane >> 4;       // octet within a 32-k step
+  const int col = cb * 16 + c;
+  const bool nv = col < N;
+  const int KP = K >> 3;
+  const int KS = K >> 5;         // 32-k steps
+  const int NG = K / G;
+
+  const MagicRegs mg = make_magic();
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
+
+  // this wave's k-steps [kb, ke)
+  const int per = (KS + kWaves - 1) / kWaves;
+  const int kb = min(KS, wave * per);
+  const int ke = min(KS, kb + per);
+
+  // per-lane offsets at k = 0
+  const uint32_t w_off = nv ? ((uint32_t)q * (uint32_t)N + (uint32_t)col) * 4u : kOobOffset;
+  const uint32_t s_off = nv ? (uint32_t)col * 2u : kOobOffset;
+  uint32_t x_off[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = mt * 16 + c;
+    x_off[mt] = row < M ? ((uint32_t)row * (uint32_t)K + (uint32_t)q * 8u) * 2u : kOobOffset;
+  }
+
+  struct Batch {
+    uint32_t w[kBatch];
+    uint32_t sz[kBatch];  // scale bits | zero bits << 16
+    uint4 x[kBatch][MT];
+  };
+  auto load_batch = [&](int s0, Batch& b) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int ks = s0 + j;
+      if (ks < ke) {   // wave-uniform
+        const uint32_t wk = uniform((uint32_t)ks * 4u * (uint32_t)N * 4u);
+        b.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
+        const uint32_t gk = uniform((uint32_t)((ks * 32) / G) * (uint32_t)N * 2u);
+        const uint32_t sv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
+        const uint32_t zv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
+        b.sz[j] = (sv & 0xFFFFu) | (zv << 16);
+        const uint32_t xk = uniform((uint32_t)ks * 64u);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
+      }
+    }
+  };
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{};
+
+  auto process = [&](const Batch& b, int s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (s0 + j >= ke) break;   // wave-uniform
+      const ColQ cq = make_colq(b.sz[j] & 0xFFFFu, b.sz[j] >> 16);
+      f16x2 d[4];
+      dq_word_fast(b.w[j], cq, mg, d);
+      // natural k order: w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
+      const f16x8 bf = f16x8{d[0].x, d[1].x, d[2].x, d[3].x, d[0].y, d[1].y, d[2].y, d[3].y};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b.x[j][mt]),
+                                                         bf, acc[mt], 0, 0, 0);
+    }
+  };
+
+  Batch ba, bb;
+  if (kb < ke) load_batch(kb, ba);
+  for (int s0 = kb; s0 < ke; s0 += 2 * kBatch) {
+    const bool more1 = s0 + kBatch < ke;
+    if (more1) load_batch(s0 + kBatch, bb);
+    process(ba, s0);
+    if (!more1) break;
+    if (s0 + 2 * kBatch < ke) load_batch(s0 + 2 * kBatch, ba);
+    process(bb, s0 + kBatch);
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  // wave w finishes m-tiles w, w+4, ...: sum the 4 waves in order, round, store
+  for (int mt = wave; mt < MT; mt += kWaves) {
+    f32x4 v = red[0][mt][lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += red[w][mt][lane];
+    if (nv) {
+      const f16 bv = bias ? bias[col] : (f16)0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = mt * 16 + 4 * q + r;
+        if (row < M) {
+          f16 y = f32_to_f16(v[r]);
+          if (bias) y = y + bv;
+          Y[(size_t)row * N + col] = y;
+        }
+      }
+    }
+  }
+}
+
+template <int MT>
+hipError_t launch_mt(const GemmArgs& a, hipStream_t st) {
+  const int nblk = (a.N + 15) / 16;
+  hipLaunchKernelGGL((skinny_kernel<MT>), dim3(nblk), dim3(kThreads), 0, st,
+                     static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
+                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
+                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
+                     a.G, nblk);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_skinny(const GemmArgs& a, hipStream_t st) {
+  switch ((a.M + 15) / 16) {
+    case 1: return launch_mt<1>(a, st);
+    case 2: return launch_mt<2>(a, st);
+    case 3: return launch_mt<3>(a, st);
+    case 4: return launch_mt<4>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace w4a16

@@ -36,9 +36,17 @@ hipError_t launch_gemv(const GemmArgs& a, int cols, int split, void* ws, hipStre
 struct MfmaTile {
   int bm, bn;
 };
-constexpr int kMfmaConfigs = 3;
+constexpr int kMfmaConfigs = 4;
 MfmaTile mfma_tile(int cfg);
+bool mfma_fits(int M, int N, int K, int G);
 hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st);
+
+// Buffer-addressed kernels need every operand below 2 GiB.
+bool operands_fit(int M, int N, int K, int G);
+
+// Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM.
+constexpr int kSkinnyMaxM = 64;
+hipError_t launch_skinny(const GemmArgs& a, hipStream_t st);
 
 // Sequential-k SIMT kernel: any N, any G dividing K, no alignment needs.
 hipError_t launch_simt(const GemmArgs& a, hipStream_t st);

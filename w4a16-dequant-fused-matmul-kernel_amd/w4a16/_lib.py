@@ -14,8 +14,9 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a16.so
 ABI_VERSION = 1
 
 # enum w4a16_kernel
-KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT = 0, 1, 2, 3
-KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt"}
+KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT, KERNEL_SKINNY = 0, 1, 2, 3, 4
+KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
+                KERNEL_SKINNY: "skinny"}
 
 # enum w4a16_status
 STATUS = {

@@ -135,7 +135,7 @@ def plan_for(M: int, N: int, K: int, group_size: int, kernel: str | int = 0,
              split_k: int = 0) -> "_lib.Plan":
     """The launch plan for a shape; `kernel` may force "gemv", "mfma" or "simt"."""
     if isinstance(kernel, str):
-        kernel = {"auto": 0, "gemv": 1, "mfma": 2, "simt": 3}[kernel]
+        kernel = {"auto": 0, "gemv": 1, "mfma": 2, "simt": 3, "skinny": 4}[kernel]
     return _lib.plan(M, N, K, group_size, kernel, split_k)
 
 
