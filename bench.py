@@ -48,6 +48,9 @@ def _args():
                     help="also time every C2-C5 case (stderr table, --sweep-json file)")
     ap.add_argument("--sweep-json", default=None)
     ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the workload for rocprofv3 --pmc: a 256 MiB copy (calibration), "
+                         "8 cold C2 decode calls, 3 C4 M=4096 prefill calls; no timing")
     return ap.parse_args()
 
 
@@ -144,8 +147,55 @@ def cpu_baseline(case, budget_s: float = 12.0, max_calls: int = 40) -> dict:
             "ms_per_call": med * 1e3}
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def traffic_probe() -> None:
+    """Kernels for the HBM-traffic counters (FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+    from w4a16 import w4a16_matmul
+    from w4a16 import workloads as wl
+
+    a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)                                   # calibration: 256 MiB read + written
+    torch.cuda.synchronize()
+    print("copy 256 MiB x3", flush=True)
+    c2 = wl.CONFIGS["C2"][0]
+    X, W, Xd, layers, y, _ = _prepare(c2, True)
+    for i in range(8):
+        l = layers[i % len(layers)]
+        w4a16_matmul(Xd, l[0], l[1], l[2], c2.G, out=y)
+    torch.cuda.synchronize()
+    print("C2 x8", flush=True)
+    del layers
+    c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
+    X, W, Xd, layers, y, _ = _prepare(c4, False)
+    for _ in range(3):
+        w4a16_matmul(Xd, layers[0][0], layers[0][1], layers[0][2], c4.G, out=y)
+    torch.cuda.synchronize()
+    print("C4 M=4096 x3", flush=True)
+
+
+def _traffic_for(kernel_prefix: str):
+    """HBM bytes per launch measured for a kernel (profiles/traffic.json), or None."""
+    try:
+        with open(TRAFFIC_JSON) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for k, v in t.get("kernels", {}).items():
+        if k.startswith(kernel_prefix):
+            return v.get("bytes_per_launch")
+    return None
+
+
 def main() -> int:
     args = _args()
+    if args.traffic_probe:
+        traffic_probe()
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build targets a single MI355X; see DESIGN.md for the sharding design)",
@@ -182,7 +232,7 @@ def main() -> int:
                    "timing": "HIP graph of K calls, HIP events" if graph else "eager, HIP events"},
         "roofline": {"bound": "hbm", "achieved": round(head["GB/s"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": _traffic_for("gemv")},
     }
     if not args.no_secondary:
         c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
@@ -194,7 +244,8 @@ def main() -> int:
             "kernel": sec["kernel"], "tile": sec["tile"],
             "roofline": {"bound": "mfma", "achieved": round(sec["TFLOP/s"], 2),
                          "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4), "traffic": None},
+                         "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
+                         "traffic": _traffic_for("mfma")},
         }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c2)

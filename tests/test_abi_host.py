@@ -138,7 +138,8 @@ def test_quant_entry_points_reject_bad_args(lib):
     (4096, 14336, 4096, 128, "mfma"),
     (16, 4096, 4096, 32, "skinny"),
     (16, 4098, 4096, 32, "skinny"),   # any N
-    (1, 4098, 4096, 128, "simt"),     # N % 4 != 0
+    (1, 4098, 4096, 128, "skinny"),   # N % 4 != 0: the 16-column kernel takes any N
+    (1, 4098, 4096, 16, "simt"),      # ... but needs G % 32 == 0
     (64, 4096, 4096, 16, "simt"),     # G % 32 != 0 beyond the GEMV's M range
     (1, 8, 8, 4, "simt"),             # G = 4: words straddle groups
 ])
