@@ -58,7 +58,8 @@ enum w4a16_kernel {
 typedef struct w4a16_plan {
   int32_t kernel;          /* enum w4a16_kernel (never AUTO once planned)       */
   int32_t split_k;         /* GEMV: k-splits across workgroups (1 = none)       */
-  int32_t tile_cfg;        /* MFMA: tile configuration index                   */
+  int32_t tile_cfg;        /* MFMA: tile configuration index;
+                              GEMV: 0 = 4 waves, 1 = 8 waves per workgroup     */
   int32_t tile_m, tile_n;  /* MFMA: workgroup tile; GEMV: 0 x 256               */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */

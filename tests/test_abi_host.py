@@ -91,6 +91,12 @@ def test_split_k_gemv_requires_workspace(lib):
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       a, 16, NULL)
     assert code == -4
+    # a wave configuration the kernel does not have
+    p.tile_cfg = 2
+    code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
+                                      a, 1 << 30, NULL)
+    assert code == -5
+    p.tile_cfg = 1
     # a column width the kernel does not have
     p.tile_n = 48
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
@@ -161,6 +167,7 @@ def test_planner_gemv_split_fills_device():
         rows = -(-512 // p.split_k)
         assert (p.split_k - 1) * rows < 512        # every split owns at least one row
     assert _lib.plan(1, 4096, 4096, 128).split_k == 1
+    assert _lib.plan(1, 4096, 4096, 128).tile_cfg in (0, 1)
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
     p1 = _lib.plan(1, 1024, 4096, 128, _lib.KERNEL_GEMV, 1)
     assert p1.split_k == 1 and p1.workspace_bytes == 0

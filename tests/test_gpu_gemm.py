@@ -119,22 +119,25 @@ RAGGED = [
 
 @pytest.mark.parametrize("M,K,N,G", RAGGED)
 def test_gemv_splits(M, K, N, G):
-    """Decode GEMV with every column-block width and k-splits 1, 2, 3, 7, auto."""
+    """Decode GEMV with every column-block width, both wave counts (4 and 8
+    waves per workgroup) and k-splits 1, 2, 3, 7, auto."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M + K)
     ref = _ref(X, qw, s, z, G)
-    for cols in (16, 32, 64, 256):
-        for split in (1, 2, 3, 7, 0):
-            if split > K // 8:
-                continue
-            p = plan_for(M, N, K, G, "gemv", split)
-            p.tile_n = cols
-            if split == 0:
-                p.split_k = max(1, min(p.split_k, K // 8))
-            log(f"gemv M={M} K={K} N={N} G={G} cols={cols} split={p.split_k}")
-            out = w4a16_matmul_planned(X, qw, s, z, G, p)
-            assert_gemm_close(out, ref, f"gemv cols={cols} split={p.split_k}")
+    for cfg in (0, 1):
+        for cols in (16, 32, 64, 256):
+            for split in (1, 2, 3, 7, 0):
+                if split > K // 8:
+                    continue
+                p = plan_for(M, N, K, G, "gemv", split)
+                p.tile_n = cols
+                p.tile_cfg = cfg
+                if split == 0:
+                    p.split_k = max(1, min(p.split_k, K // 8))
+                log(f"gemv M={M} K={K} N={N} G={G} cfg={cfg} cols={cols} split={p.split_k}")
+                out = w4a16_matmul_planned(X, qw, s, z, G, p)
+                assert_gemm_close(out, ref, f"gemv cfg={cfg} cols={cols} split={p.split_k}")
 
 
 @pytest.mark.parametrize("M,K,N,G", [

@@ -122,6 +122,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       }
       if ((N + cols - 1) / cols > kGemvMaxCounterBlocks) S = 1;
       p->split_k = S;
+      p->tile_cfg = kGemvDefaultConfig;
       p->tile_m = 0;
       p->tile_n = cols;
       p->grid_x = ((N + cols - 1) / cols) * S;
@@ -136,8 +137,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->tile_cfg = cfg;
       p->tile_m = t.bm;
       p->tile_n = t.bn;
-      p->grid_x = (N + t.bn - 1) / t.bn;
-      p->grid_y = (M + t.bm - 1) / t.bm;
+      p->grid_x = ((N + t.bn - 1) / t.bn) * ((M + t.bm - 1) / t.bm);
+      p->grid_y = 1;
       return W4A16_OK;
     }
     case W4A16_KERNEL_SKINNY:
@@ -173,7 +174,7 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
-          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n))
+          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n) || !gemv_cfg_valid(p->tile_cfg))
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;
@@ -182,7 +183,7 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
         return W4A16_ERR_BAD_PLAN;
       const size_t need = gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
       if (need > 0 && (!ws || ws_bytes < need || !aligned(ws, 256))) return W4A16_ERR_WORKSPACE;
-      return to_status(launch_gemv(a, p->tile_n, p->split_k, ws, s));
+      return to_status(launch_gemv(a, p->tile_n, p->tile_cfg, p->split_k, ws, s));
     }
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G) || !fits(M, N, K, G) || p->tile_cfg < 0 ||

@@ -17,11 +17,13 @@
 //   * all global traffic uses buffer loads: the per-step k offset rides in an
 //     SGPR, and rows past M / columns past N read as zero through the buffer
 //     range check instead of branches;
-//   * K advances 64 per step with two register stages used ping-pong (no copies)
-//     and a double-buffered LDS activation tile, one barrier per step; the next
-//     step's loads are issued before the current step's MFMAs;
+//   * K advances 64 per step with three register stages in rotation (no copies)
+//     and a double-buffered LDS activation tile, one barrier per step; loads are
+//     issued two steps before their MFMAs;
 //   * LDS rows are padded to 144 bytes so the ds_read_b128 of 16 rows x 16 B
 //     hits 64 distinct banks;
+//   * XCD-aware grouped tile order (see the kernel) keeps A/B tile re-reads in
+//     each XCD's L2;
 //   * epilogue: lane l holds 4 consecutive columns per output row, rounded to
 //     fp16 (RNE) and stored as one 8-byte write; optional fp16 bias add
 //     reproduces W4A16Linear's separate `y + bias` (linear.py:90-91).
@@ -36,6 +38,7 @@ namespace {
 
 constexpr int kBK = 64;
 constexpr int kLdsRow = 9;  // uint4 per LDS row: 8 octets + 1 pad
+constexpr int kGroupM = 4;  // M-tiles per group of the tile order
 
 template <int WMT, int WAVES_M, int WAVES_N, bool KTAIL>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
@@ -57,8 +60,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
 
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * BN;
+  // Tile order: the hardware deals workgroups to the 8 XCDs round-robin; give
+  // each XCD a contiguous run of the grouped order below, so the tiles one XCD
+  // holds at a time (about 32) share activation rows and weight columns through
+  // that XCD's L2.  Grouped order: kGroupM M-tiles x all N-tiles per group.
+  const int ntn = (N + BN - 1) / BN;
+  const int ntm = (M + BM - 1) / BM;
+  const int total = ntn * ntm;
+  int T = (int)blockIdx.x;
+  if ((total & 7) == 0) T = (T & 7) * (total >> 3) + (T >> 3);
+  const int group = T / (kGroupM * ntn);
+  const int first_m = group * kGroupM;
+  const int gsz = min(ntm - first_m, kGroupM);
+  const int rem = T - group * kGroupM * ntn;
+  const int m0 = (first_m + rem % gsz) * BM;
+  const int n0 = (rem / gsz) * BN;
   const int ncol = n0 + wn * 128 + 4 * l32;
   const bool nv = ncol < N;
   const int KP = K >> 3;
@@ -179,25 +195,41 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     }
   };
 
-  Stage s0, s1;
+  // Three register stages in rotation: step kt computes from stage kt%3 while
+  // step kt+2's loads fly, so each load has two k-steps to arrive.  A single
+  // loop exit keeps the accumulators in one set of registers.
+  Stage s0, s1, s2;
   load(0, s0);
+  if (KT > 1) load(1, s1);
   store_a(s0, 0);
   __syncthreads();
-  // Pairs of steps with ping-pong stages; a single loop exit keeps the
-  // accumulators in one set of registers.
   int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {
-    load(kt + 1, s1);
-    compute(s0, 0, kt);
-    store_a(s1, 1);
+  for (; kt + 2 < KT; kt += 3) {
+    // LDS buffer = step parity; a 3-step body flips it every iteration
+    const int p = kt & 1;
+    load(kt + 2, s2);
+    compute(s0, p, kt);
+    store_a(s1, p ^ 1);
     __syncthreads();
-    const bool more = kt + 2 < KT;
-    if (more) load(kt + 2, s0);
-    compute(s1, 1, kt + 1);
-    if (more) store_a(s0, 0);
+    if (kt + 3 < KT) load(kt + 3, s0);
+    compute(s1, p ^ 1, kt + 1);
+    store_a(s2, p);
+    __syncthreads();
+    if (kt + 4 < KT) load(kt + 4, s1);
+    compute(s2, p, kt + 2);
+    if (kt + 3 < KT) store_a(s0, p ^ 1);
     __syncthreads();
   }
-  if (kt < KT) compute(s0, 0, kt);   // odd step count: the last step sits in s0 / buffer 0
+  // 1 or 2 steps left: step kt in s0, its activations in LDS buffer kt % 2
+  if (kt < KT) {
+    const int b0 = kt & 1;
+    compute(s0, b0, kt);
+    if (kt + 1 < KT) {
+      store_a(s1, b0 ^ 1);
+      __syncthreads();
+      compute(s1, b0 ^ 1, kt + 1);
+    }
+  }
 
   if (!nv) return;
   f16 bv[4] = {(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};
@@ -235,7 +267,7 @@ template <int WMT, int WAVES_M, int WAVES_N>
 hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 128 * WAVES_N;
-  dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+  dim3 grid(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
   dim3 block(64 * WAVES_M * WAVES_N);
   const f16* x = static_cast<const f16*>(a.x);
   const uint32_t* qw = reinterpret_cast<const uint32_t*>(a.qw);

@@ -4,22 +4,25 @@
 // (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 at M = 1..16, BLOCK_M >= 16).
 //
 // Layout of the work:
-//   * a workgroup (4 waves) owns a block of CW = 4*CWL consecutive columns; in a
-//     wave, CWL lanes cover one packed row (global_load_dwordx4 = 4 columns per
+//   * a workgroup (WAVES waves) owns a block of CW = 4*CWL consecutive columns;
+//     in a wave, CWL lanes cover one packed row (one dwordx4 = 4 columns per
 //     lane) and the wave's 64/CWL row-lanes sit on different packed rows;
-//   * each row-lane owns a contiguous run of packed rows, cut into batches of 8
-//     rows aligned to absolute row multiples of 8 (64 k).  With G % 32 == 0 each
-//     half-batch (4 rows = 32 k) lies in one quantisation group, so a batch
-//     needs at most two scale/zero loads per lane;
-//   * the only vector-memory loads in the main loop are weights and scales, and
-//     all of batch i+1's are issued before batch i is consumed: the in-order
-//     vmcnt counter then waits exactly for batch i.  Activations are staged
-//     once into LDS (permuted to the dequantiser's pair order) and read with
-//     ds_read_b128, which uses the separate LDS counter;
+//   * each row-lane owns a contiguous run of packed rows, cut into batches of BR
+//     rows (8 with 4 waves, 4 with 8 waves) aligned to absolute multiples of BR.
+//     With G % 32 == 0 every 4-row half (32 k) lies in one quantisation group,
+//     so a batch needs one scale/zero load per half;
+//   * every load of batch i+1 is issued before batch i is consumed, in the order
+//     scales, activations, weights, so the in-order vmcnt counter releases the
+//     first weight row as soon as it lands.  Weights are read with the
+//     non-temporal hint: each byte is used once;
+//   * activations: for M <= 2 each lane reads its rows' activations directly
+//     (the whole X is a few KiB and stays in L2), with no barrier before the
+//     first weight arrives; for larger M, X is staged once per chunk in LDS,
+//     permuted to the dequantiser's pair order;
 //   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
 //     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
 //   * reduction over row-lanes: a fixed xor-shuffle tree inside the wave, then the
-//     4 waves in order through LDS -- deterministic;
+//     waves in order through LDS -- deterministic;
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
 //     so that neighbouring row segments share that XCD's L2 lines;
@@ -32,24 +35,32 @@
 namespace w4a16 {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kBatch = 8;                 // packed rows per batch (64 k)
 constexpr int kXsEntries = 2048;          // LDS activation slots (16 B each): 32 KiB
+constexpr int kNonTemporal = 2;           // buffer-load cache policy: nt
 
-template <int MT, int CWL>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(
+template <int WAVES>
+struct GemvShape {
+  static constexpr int kThreads = 64 * WAVES;
+  static constexpr int kBatch = WAVES >= 8 ? 4 : 8;   // packed rows per batch
+};
+
+template <int MT, int CWL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
     float* __restrict__ part, uint32_t* __restrict__ cnt, int N, int K, int G, int rows_per_wg,
     int S, int nblk) {
+  constexpr int kThreads = GemvShape<WAVES>::kThreads;
+  constexpr int BR = GemvShape<WAVES>::kBatch;
+  constexpr int H = BR / 4;                // 4-row halves per batch (one group each)
+  constexpr bool XD = MT <= 2;             // activations read directly from global
   constexpr int RW = 64 / CWL;             // row-lanes per wave
-  constexpr int RL = kWaves * RW;          // row-lanes per workgroup
+  constexpr int RL = WAVES * RW;           // row-lanes per workgroup
   constexpr int CW = 4 * CWL;              // columns per workgroup
-  constexpr int CHUNK = kXsEntries / MT / kBatch * kBatch;   // packed rows of X per stage
-  static_assert(CHUNK % kBatch == 0, "chunk must hold whole batches");
-  __shared__ uint4 xs[MT * CHUNK];
-  __shared__ float red[kWaves][MT][CW];
+  constexpr int CHUNK = XD ? BR : kXsEntries / MT / BR * BR;   // packed rows of X per stage
+  static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
+  __shared__ uint4 xs[XD ? 1 : MT * CHUNK];
+  __shared__ float red[CWL <= 16 ? WAVES * 4 : WAVES][MT][CW];
   __shared__ int s_last;
 
   // XCD-aware block order (see header comment).
@@ -67,13 +78,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   const int n = cb * CW + 4 * cq;
   const bool nv = n < N;
   const int KP = K >> 3;
+  const int NG = K / G;
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
-  const bool g64 = (G & 63) == 0;          // one group per batch
   const MagicRegs mg = make_magic();
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)MT * (uint32_t)K * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)(K / G) * (uint32_t)N * 2u);
-  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)(K / G) * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
   const uint32_t row_bytes = (uint32_t)N * 4u;
   const uint32_t s_voff = (uint32_t)n * 2u;
 
@@ -84,50 +96,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
 
   struct Batch {
-    uint4 w[kBatch];
-    uint2 s0, z0, s1, z1;
+    uint2 s[H], z[H];
+    uint4 x[XD ? MT * BR : 1];
+    uint4 w[BR];
   };
-  // Rows r0..r0+7 of this lane's run [.., le).  Row u rides in the SGPR offset;
-  // rows at or past `le` (only in a run's last batch) read as zero.
+  // Rows r0..r0+BR-1 of this lane's run [.., le).  Row u rides in the SGPR
+  // offset; weight rows at or past `le` (only in a run's last batch) read as zero.
   auto load_batch = [&](int r0, int le, Batch& b) {
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      // the group differs between row-lanes: its offset goes in the VGPR operand
+      const int g = min(((r0 + 4 * h) * 8) / G, NG - 1);
+      const uint32_t so = nv ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
+      b.s[h] = buf_load8(rs, so, 0u);
+      b.z[h] = buf_load8(rz, so, 0u);
+    }
+    if constexpr (XD) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int u = 0; u < BR; ++u)
+          b.x[m * BR + u] = buf_load16(rx, ((uint32_t)m * (uint32_t)K + (uint32_t)r0 * 8u) * 2u,
+                                       uniform((uint32_t)u * 16u));
+    }
+    // One path for full and partial batches (a lane-dependent branch here would
+    // move the row offset out of the SGPR and serialise the loads).
     const uint32_t base = nv ? ((uint32_t)r0 * (uint32_t)N + (uint32_t)n) * 4u : kOobOffset;
-    if (r0 + kBatch <= le) {
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) b.w[u] = buf_load16(rw, base, uniform((uint32_t)u * row_bytes));
-    } else {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        b.w[u] = buf_load16(rw, r0 + u < le ? base : kOobOffset, uniform((uint32_t)u * row_bytes));
-    }
-    // the group differs between row-lanes: its offset goes in the VGPR operand
-    const int g0 = (r0 * 8) / G;
-    const uint32_t so0 = nv ? s_voff + (uint32_t)g0 * (uint32_t)N * 2u : kOobOffset;
-    b.s0 = buf_load8(rs, so0, 0u);
-    b.z0 = buf_load8(rz, so0, 0u);
-    if (!g64) {
-      const int g1 = min(((r0 + 4) * 8) / G, K / G - 1);
-      const uint32_t so1 = nv ? s_voff + (uint32_t)g1 * (uint32_t)N * 2u : kOobOffset;
-      b.s1 = buf_load8(rs, so1, 0u);
-      b.z1 = buf_load8(rz, so1, 0u);
-    } else {
-      b.s1 = b.s0;
-      b.z1 = b.z0;
-    }
+    for (int u = 0; u < BR; ++u)
+      b.w[u] = buf_load16<kNonTemporal>(rw, r0 + u < le ? base : kOobOffset,
+                                        uniform((uint32_t)u * row_bytes));
   };
 
   auto process = [&](const Batch& b, int r0, int le, int c0) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint2 sv = h ? b.s1 : b.s0;
-      const uint2 zv = h ? b.z1 : b.z0;
+    for (int h = 0; h < H; ++h) {
       ColQ cq4[4];
-      cq4[0] = make_colq(sv.x & 0xFFFFu, zv.x & 0xFFFFu);
-      cq4[1] = make_colq(sv.x >> 16, zv.x >> 16);
-      cq4[2] = make_colq(sv.y & 0xFFFFu, zv.y & 0xFFFFu);
-      cq4[3] = make_colq(sv.y >> 16, zv.y >> 16);
+      cq4[0] = make_colq(b.s[h].x & 0xFFFFu, b.z[h].x & 0xFFFFu);
+      cq4[1] = make_colq(b.s[h].x >> 16, b.z[h].x >> 16);
+      cq4[2] = make_colq(b.s[h].y & 0xFFFFu, b.z[h].y & 0xFFFFu);
+      cq4[3] = make_colq(b.s[h].y >> 16, b.z[h].y >> 16);
 #pragma unroll
-      for (int uu = 0; uu < kBatch / 2; ++uu) {
-        const int u = h * (kBatch / 2) + uu;
+      for (int uu = 0; uu < 4; ++uu) {
+        const int u = h * 4 + uu;
         const int r = r0 + u;
         if (r >= le) break;
         f16x2 d[4][4];
@@ -137,7 +148,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
         dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const uint4 xp = xs[m * CHUNK + (r - c0)];
+          uint4 xp;
+          if constexpr (XD)
+            xp = perm_pairs(b.x[m * BR + u]);
+          else
+            xp = xs[m * CHUNK + (r - c0)];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             float a = acc[m][c];
@@ -152,53 +167,77 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     }
   };
 
-  for (int c0 = rb; c0 < re; c0 += CHUNK) {
-    const int c1 = min(re, c0 + CHUNK);
+  for (int c0 = rb; c0 < re; c0 += (XD ? re - rb : CHUNK)) {
+    const int c1 = XD ? re : min(re, c0 + CHUNK);
     const int nr = c1 - c0;
-    // this row-lane's rows in the chunk: 8-row aligned run
-    const int per = ((nr + RL - 1) / RL + kBatch - 1) / kBatch * kBatch;
+    // this row-lane's rows in the chunk: BR-row aligned run
+    const int per = ((nr + RL - 1) / RL + BR - 1) / BR * BR;
     const int lb = min(c1, c0 + rl * per);
     const int le = min(c1, lb + per);
 
-    // Stage X rows [c0, c1) into LDS (loads issued before the first weight batch).
-    if (c0 != rb) __syncthreads();   // previous chunk's readers are done
-    constexpr int XPT = (MT * CHUNK + kThreads - 1) / kThreads;
-    uint4 xv[XPT];
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int idx = tid + i * kThreads;
-      const int m = idx / CHUNK, r = idx % CHUNK;
-      xv[i] = (m < MT && r < nr)
-                  ? *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)(c0 + r) * 8)
-                  : make_uint4(0u, 0u, 0u, 0u);
-    }
     Batch ba, bb;
-    if (lb < le) load_batch(lb, le, ba);
+    if constexpr (XD) {
+      if (lb < le) load_batch(lb, le, ba);
+    } else {
+      // Stage X rows [c0, c1) into LDS; its loads go out before the first
+      // weight batch, so the barrier waits only for them.
+      if (c0 != rb) __syncthreads();   // previous chunk's readers are done
+      constexpr int XPT = (MT * CHUNK + kThreads - 1) / kThreads;
+      uint4 xv[XPT];
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < MT * CHUNK) xs[idx] = perm_pairs(xv[i]);
+      for (int i = 0; i < XPT; ++i) {
+        const int idx = tid + i * kThreads;
+        const int m = idx / CHUNK, r = idx % CHUNK;
+        const uint32_t off = (m < MT && r < nr)
+                                 ? ((uint32_t)m * (uint32_t)K + (uint32_t)(c0 + r) * 8u) * 2u
+                                 : kOobOffset;
+        xv[i] = buf_load16(rx, off, 0u);
+      }
+      if (lb < le) load_batch(lb, le, ba);
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) {
+        const int idx = tid + i * kThreads;
+        if (idx < MT * CHUNK) xs[idx] = perm_pairs(xv[i]);
+      }
+      __syncthreads();
     }
-    __syncthreads();
 
     // two register batches used ping-pong: no copies between iterations
-    for (int r0 = lb; r0 < le; r0 += 2 * kBatch) {
-      if (r0 + kBatch < le) load_batch(r0 + kBatch, le, bb);
+    for (int r0 = lb; r0 < le; r0 += 2 * BR) {
+      if (r0 + BR < le) load_batch(r0 + BR, le, bb);
       process(ba, r0, le, c0);
-      if (r0 + kBatch >= le) break;
-      if (r0 + 2 * kBatch < le) load_batch(r0 + 2 * kBatch, le, ba);
-      process(bb, r0 + kBatch, le, c0);
+      if (r0 + BR >= le) break;
+      if (r0 + 2 * BR < le) load_batch(r0 + 2 * BR, le, ba);
+      process(bb, r0 + BR, le, c0);
     }
   }
 
-  // Sum the wave's row-lanes (lanes with equal cq) with a fixed xor tree.
-#pragma unroll
-  for (int off = CWL; off < 64; off <<= 1)
+  // Reduce over row-lanes in a fixed order.  Inside each 16-lane DPP row the
+  // lanes with equal cq are combined by row rotations (register-to-register,
+  // no LDS round trip); the per-row partial sums then go through LDS once and
+  // thread t < CW adds the PS partial sets of its column in set order.
+  constexpr int PS = CWL <= 16 ? WAVES * 4 : WAVES;   // partial sets per workgroup
+  if constexpr (CWL <= 4) {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] += __shfl_xor(acc[m][c], off);
-  if (lane < CWL) {
+      for (int c = 0; c < 4; ++c) acc[m][c] += dpp_row_ror<4>(acc[m][c]);
+  }
+  if constexpr (CWL <= 8) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[m][c] += dpp_row_ror<8>(acc[m][c]);
+  }
+  if constexpr (CWL <= 16) {
+    const int row = lane >> 4;
+    if ((lane & 15) < CWL) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        *reinterpret_cast<float4*>(&red[wave * 4 + row][m][4 * cq]) =
+            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    }
+  } else {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
       *reinterpret_cast<float4*>(&red[wave][m][4 * cq]) =
@@ -216,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
     if (t < CW) {
       s = red[0][m][t];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) s += red[w][m][t];
+      for (int w = 1; w < PS; ++w) s += red[w][m][t];
     }
     v[m] = s;
   }
@@ -258,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(
   if (t == 0) cnt[cb] = 0u;
 }
 
-template <int MT, int CWL>
+template <int MT, int CWL, int WAVES>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;
   const int nblk = (a.N + CW - 1) / CW;
@@ -269,21 +308,31 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
     cnt = static_cast<uint32_t*>(ws);
     part = reinterpret_cast<float*>(static_cast<char*>(ws) + kGemvCounterBytes);
   }
-  hipLaunchKernelGGL((gemv_kernel<MT, CWL>), dim3(nblk * split), dim3(kThreads), 0, st,
-                     static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), part, cnt, a.N, a.K,
-                     a.G, rows, split, nblk);
+  hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES>), dim3(nblk * split),
+                     dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
+                     reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
+                     static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
+                     static_cast<f16*>(a.y), part, cnt, a.N, a.K, a.G, rows, split, nblk);
   return hipGetLastError();
 }
 
-template <int MT>
-hipError_t launch_mt(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
+template <int MT, int WAVES>
+hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
   switch (cols) {
-    case 16: return launch_cwl<MT, 4>(a, split, ws, st);
-    case 32: return launch_cwl<MT, 8>(a, split, ws, st);
-    case 64: return launch_cwl<MT, 16>(a, split, ws, st);
-    case 256: return launch_cwl<MT, 64>(a, split, ws, st);
+    case 16: return launch_cwl<MT, 4, WAVES>(a, split, ws, st);
+    case 32: return launch_cwl<MT, 8, WAVES>(a, split, ws, st);
+    case 64: return launch_cwl<MT, 16, WAVES>(a, split, ws, st);
+    case 256: return launch_cwl<MT, 64, WAVES>(a, split, ws, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int MT>
+hipError_t launch_mt(const GemmArgs& a, int cols, int waves_cfg, int split, void* ws,
+                     hipStream_t st) {
+  switch (waves_cfg) {
+    case 0: return launch_w<MT, 4>(a, cols, split, ws, st);
+    case 1: return launch_w<MT, 8>(a, cols, split, ws, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -291,12 +340,13 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int split, void* ws, hipStream
 }  // namespace
 
 bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 || cols == 256; }
+bool gemv_cfg_valid(int cfg) { return cfg >= 0 && cfg < kGemvConfigs; }
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;
   // whole 8-row batches per split keep every batch inside the batch alignment
   const int rows = (KP + split - 1) / split;
-  return (rows + kBatch - 1) / kBatch * kBatch;
+  return (rows + 7) / 8 * 8;
 }
 
 size_t gemv_workspace_bytes(int M, int N, int K, int split) {
@@ -305,16 +355,16 @@ size_t gemv_workspace_bytes(int M, int N, int K, int split) {
   return kGemvCounterBytes + (size_t)split * (size_t)M * (size_t)N * sizeof(float);
 }
 
-hipError_t launch_gemv(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
+hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {
   switch (a.M) {
-    case 1: return launch_mt<1>(a, cols, split, ws, st);
-    case 2: return launch_mt<2>(a, cols, split, ws, st);
-    case 3: return launch_mt<3>(a, cols, split, ws, st);
-    case 4: return launch_mt<4>(a, cols, split, ws, st);
-    case 5: return launch_mt<5>(a, cols, split, ws, st);
-    case 6: return launch_mt<6>(a, cols, split, ws, st);
-    case 7: return launch_mt<7>(a, cols, split, ws, st);
-    case 8: return launch_mt<8>(a, cols, split, ws, st);
+    case 1: return launch_mt<1>(a, cols, cfg, split, ws, st);
+    case 2: return launch_mt<2>(a, cols, cfg, split, ws, st);
+    case 3: return launch_mt<3>(a, cols, cfg, split, ws, st);
+    case 4: return launch_mt<4>(a, cols, cfg, split, ws, st);
+    case 5: return launch_mt<5>(a, cols, cfg, split, ws, st);
+    case 6: return launch_mt<6>(a, cols, cfg, split, ws, st);
+    case 7: return launch_mt<7>(a, cols, cfg, split, ws, st);
+    case 8: return launch_mt<8>(a, cols, cfg, split, ws, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -106,6 +106,14 @@ __device__ __forceinline__ uint4 perm_pairs(uint4 v) {
   return r;
 }
 
+// v <- v from lane (l - N) mod 16 of the same 16-lane DPP row (row_ror:N).
+template <int kN>
+__device__ __forceinline__ float dpp_row_ror(float v) {
+  static_assert(kN >= 1 && kN <= 15, "row rotation is 1..15 lanes");
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + kN, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ f16 f32_to_f16(float x) { return (f16)x; }  // v_cvt_f16_f32, RNE
 
 // Buffer resource over [p, p + bytes): raw buffer loads outside the range return
@@ -120,9 +128,10 @@ constexpr uint32_t kOobOffset = 0x80000000u;
 __device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // `soff` must be wave-uniform (it is an SGPR operand).
+template <int kPolicy = 0>
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   typedef int v4i __attribute__((ext_vector_type(4)));
-  const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kPolicy);
   return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
 __device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {

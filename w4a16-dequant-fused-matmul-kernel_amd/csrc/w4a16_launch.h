@@ -20,17 +20,24 @@ struct GemmArgs {
 };
 
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
-// consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; with
-// split > 1, `ws` holds the counters + fp32 partials of gemv_workspace_bytes().
+// consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
+// picks 4 (cfg 0) or 8 (cfg 1) waves per workgroup; with split > 1, `ws` holds
+// the counters + fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
+constexpr int kGemvConfigs = 2;
+// 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
+// other's outstanding loads (measured faster on MI355X for M = 1 decode shapes).
+constexpr int kGemvDefaultConfig = 1;
 // Split-K counters live in a fixed-size region at the start of the workspace so
 // that no call's fp32 partials ever overlap another call's counters.
 constexpr int kGemvMaxCounterBlocks = 16384;
 constexpr size_t kGemvCounterBytes = (size_t)kGemvMaxCounterBlocks * 4;
 bool gemv_cols_valid(int cols);
+bool gemv_cfg_valid(int cfg);
 size_t gemv_workspace_bytes(int M, int N, int K, int split);
 int gemv_rows_per_split(int K, int split);
-hipError_t launch_gemv(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st);
+hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws,
+                       hipStream_t st);
 
 // Prefill GEMM on MFMA (v_mfma_f32_32x32x16_f16).  `cfg` picks the tile shape.
 struct MfmaTile {
