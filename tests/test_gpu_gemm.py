@@ -143,20 +143,28 @@ def test_gemv_splits(M, K, N, G):
 @pytest.mark.parametrize("M,K,N,G", [
     (9, 96, 260, 32), (33, 160, 516, 32), (127, 4096, 1028, 128), (129, 4096, 516, 64),
     (200, 1024, 1540, 32), (64, 4096, 4096, 128), (1, 64, 128, 32), (16, 11008, 4096, 64),
+    (600, 1024, 2048, 64), (520, 2112, 772, 96),
 ])
 def test_mfma_tile_configs(M, K, N, G):
-    """Prefill MFMA kernel with every tile configuration over tails in M, N, K."""
+    """Prefill MFMA kernels with every tile configuration over tails in M, N, K
+    (config 4, the LDS-staged 256 x 256 kernel, and configs 7 and 8, two waves
+    per SIMD with 16x16x32 MFMAs, where K % 64 == 0; configs 5 and 6, two
+    waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 3 + N)
     ref = _ref(X, qw, s, z, G)
-    for cfg in range(3):
+    for cfg in range(9):
+        if (cfg in (4, 7, 8) and K % 64) or (cfg in (5, 6) and K % 128):
+            continue
         p = plan_for(M, N, K, G, "mfma")
         p.tile_cfg = cfg
         log(f"mfma M={M} K={K} N={N} G={G} cfg={cfg}")
         out = w4a16_matmul_planned(X, qw, s, z, G, p)
         assert_gemm_close(out, ref, f"mfma cfg={cfg}")
+        b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
+        assert torch.equal(w4a16_matmul_planned(X, qw, s, z, G, p, bias=b), out + b)
     assert _lib.KERNEL_NAMES[p.kernel] == "mfma"
 
 
@@ -239,6 +247,17 @@ def test_out_parameter_and_empty():
     assert_gemm_close(out, _ref(X, qw, s, z, 64), "out=")
     y0 = w4a16_matmul(X[:0], qw, s, z, 64)
     assert y0.shape == (0, 128)
+    # K = 0: Y = 0, and the fused linear gives exactly the bias
+    from w4a16.hip_kernel import w4a16_linear
+    Xk = torch.empty((3, 0), dtype=torch.float16, device=DEV)
+    qk = torch.empty((0, 128), dtype=torch.int32, device=DEV)
+    sk = torch.empty((0, 128), dtype=torch.float16, device=DEV)
+    yk = w4a16_matmul(Xk, qk, sk, sk, 64, out=torch.full((3, 128), 7.0, dtype=torch.float16,
+                                                           device=DEV))
+    assert torch.equal(yk, torch.zeros_like(yk))
+    b = torch.randn(128, dtype=torch.float16, device=DEV)
+    yb = w4a16_linear(Xk, qk, sk, sk, b, 64)
+    assert torch.equal(yb, b.expand(3, 128))
 
 
 def test_kernel_asserts_contiguity():

@@ -82,10 +82,19 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
   return (int)S;
 }
 
-int mfma_cfg_auto(int64_t M, int64_t N, int cus) {
+// Prefill tile configuration by shape (measured on MI355X, C4/C5 shapes):
+//   * M >= 1024: the two-waves-per-SIMD 16x16x32 kernel, 128 x 256 (cfg 7);
+//   * enough 128 x 256 tiles for half the CUs: two-waves-per-SIMD 32x32x16,
+//     128 x 256 (cfg 6);
+//   * fewer tiles (short M, narrow N): narrow 32 x 512 tiles for more
+//     workgroups (cfg 2), else the one-wave-per-SIMD 128 x 256 (cfg 1).
+int mfma_cfg_auto(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) return 2;
-  const int64_t t0 = ((N + 511) / 512) * ((M + 127) / 128);
-  if (t0 >= cus) return 0;
+  const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
+  if (M >= 1024 && mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) return 7;
+  if (2 * t6 >= cus && mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return 6;
+  const int64_t t2 = ((N + 511) / 512) * ((M + 31) / 32);
+  if (2 * t6 < cus && t2 > t6) return 2;
   return 1;
 }
 
@@ -132,7 +141,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     }
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G)) return W4A16_ERR_BAD_PLAN;
-      const int cfg = mfma_cfg_auto(M, N, cus);
+      const int cfg = mfma_cfg_auto(M, N, K, G, cus);
       const MfmaTile t = mfma_tile(cfg);
       p->tile_cfg = cfg;
       p->tile_m = t.bm;
@@ -167,10 +176,12 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   if (!p) return W4A16_ERR_NULL_POINTER;
   if (int st = check_gemm_shape(M, N, K, G)) return st;
   if (M == 0 || N == 0) return W4A16_OK;
-  if (!x || !y || (K > 0 && (!qw || !sc || !zr))) return W4A16_ERR_NULL_POINTER;
+  if (!y || (K > 0 && (!x || !qw || !sc || !zr))) return W4A16_ERR_NULL_POINTER;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (K == 0) return to_status(hipMemsetAsync(y, 0, (size_t)M * (size_t)N * 2, s));
   GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G};
+  // K = 0: Y = 0 (+ bias).  A kernel rather than a memset, so that the call
+  // can be captured into a HIP graph; the SIMT kernel reads no operand then.
+  if (K == 0) return to_status(launch_simt(a, s));
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
@@ -186,8 +197,8 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
       return to_status(launch_gemv(a, p->tile_n, p->tile_cfg, p->split_k, ws, s));
     }
     case W4A16_KERNEL_MFMA: {
-      if (!mfma_applicable(N, G) || !fits(M, N, K, G) || p->tile_cfg < 0 ||
-          p->tile_cfg >= kMfmaConfigs)
+      if (!mfma_applicable(N, G) || !fits(M, N, K, G) ||
+          !mfma_cfg_applicable(p->tile_cfg, (int)M, (int)N, (int)K, (int)G))
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
           !aligned(y, 8) || (bias && !aligned(bias, 8)))

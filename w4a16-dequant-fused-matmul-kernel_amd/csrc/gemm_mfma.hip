@@ -36,6 +36,13 @@
 namespace w4a16 {
 namespace {
 
+#ifndef W4A16_MFMA_INTERLEAVE
+#define W4A16_MFMA_INTERLEAVE 0
+#endif
+#ifndef W4A16_OCC2_INTERLEAVE
+#define W4A16_OCC2_INTERLEAVE 4
+#endif
+
 constexpr int kBK = 64;
 constexpr int kLdsRow = 9;  // uint4 per LDS row: 8 octets + 1 pad
 constexpr int kGroupM = 4;  // M-tiles per group of the tile order
@@ -156,10 +163,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     ColQ cq[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      cq[h][0] = make_colq(st.sc[h].x & 0xFFFFu, st.zr[h].x & 0xFFFFu);
-      cq[h][1] = make_colq(st.sc[h].x >> 16, st.zr[h].x >> 16);
-      cq[h][2] = make_colq(st.sc[h].y & 0xFFFFu, st.zr[h].y & 0xFFFFu);
-      cq[h][3] = make_colq(st.sc[h].y >> 16, st.zr[h].y >> 16);
+      const ColQ2 p01 = make_colq2(st.sc[h].x, st.zr[h].x);
+      const ColQ2 p23 = make_colq2(st.sc[h].y, st.zr[h].y);
+      cq[h][0] = colq_of<0>(p01);
+      cq[h][1] = colq_of<1>(p01);
+      cq[h][2] = colq_of<0>(p23);
+      cq[h][3] = colq_of<1>(p23);
     }
     const uint4* A = &As[buf][arow * kLdsRow + lhi];
     auto dequant = [&](int s, f16x8 bf[4]) {
@@ -191,6 +200,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
         for (int c = 0; c < 4; ++c)
           acc[mt][c] =
               __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mt], bf[cur][c], acc[mt][c], 0, 0, 0);
+#if W4A16_MFMA_INTERLEAVE
+      // Issue pattern for this sub-step: the next sub-step's fragment reads
+      // first, then one MFMA followed by a few dequant VALU ops, so the VALU
+      // work co-issues while the matrix core is busy.
+      __builtin_amdgcn_sched_group_barrier(0x100, WMT, 0);   // DS reads
+#pragma unroll
+      for (int i = 0; i < 4 * WMT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, W4A16_MFMA_INTERLEAVE, 0);  // VALU
+      }
+#endif
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -263,6 +283,217 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
   }
 }
 
+// Two-waves-per-SIMD variant: each wave owns (32*WMT) rows x 64 columns (two
+// columns per lane, 128 accumulator registers), so a SIMD holds two waves (from
+// two workgroups) and one wave's dequant and memory waits overlap the other's
+// MFMAs.  B lane l of n-tile j is column 2*(l%32) + j of the wave's 64; the
+// epilogue stores 2 consecutive columns per lane.  One A register stage and two
+// B register stages; K must be a multiple of 128 (two steps per iteration).
+template <int WMT, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
+                      const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
+                      const f16* __restrict__ bias, f16* __restrict__ Y, int M, int N, int K,
+                      int G) {
+  constexpr int NT = 64 * WAVES_M * WAVES_N;
+  constexpr int BM = 32 * WMT * WAVES_M;
+  constexpr int BN = 64 * WAVES_N;
+  constexpr int A_PER_T = BM * 8 / NT;
+  static_assert((BM * 8) % NT == 0, "A tile must split evenly over threads");
+  __shared__ uint4 As[2][BM * kLdsRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+  const int l32 = lane & 31;
+  const int lhi = lane >> 5;
+
+  const int ntn = (N + BN - 1) / BN;
+  const int ntm = (M + BM - 1) / BM;
+  const int total = ntn * ntm;
+  int T = (int)blockIdx.x;
+  if ((total & 7) == 0) T = (T & 7) * (total >> 3) + (T >> 3);
+  const int group = T / (kGroupM * ntn);
+  const int first_m = group * kGroupM;
+  const int gsz = min(ntm - first_m, kGroupM);
+  const int rem = T - group * kGroupM * ntn;
+  const int m0 = (first_m + rem % gsz) * BM;
+  const int n0 = (rem / gsz) * BN;
+  const int ncol = n0 + wn * 64 + 2 * l32;
+  const bool nv = ncol < N;
+  const int KP = K >> 3;
+  const int KT = K / kBK;
+  const int NG = K / G;
+
+  const MagicRegs mg = make_magic();
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
+
+  uint32_t a_off[A_PER_T];
+#pragma unroll
+  for (int i = 0; i < A_PER_T; ++i) {
+    const int o = tid + i * NT;
+    const int gm = m0 + (o >> 3);
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+  }
+  const uint32_t b_off = nv ? ((uint32_t)lhi * (uint32_t)N + (uint32_t)ncol) * 4u : kOobOffset;
+  const uint32_t s_off = nv ? (uint32_t)ncol * 2u : kOobOffset;
+
+  struct StageB {
+    uint2 b[4];            // k-sub s: packed row 2s + lhi, columns ncol, ncol+1
+    uint32_t sc[2], zr[2];
+  };
+  uint4 ra[A_PER_T];
+
+  auto load_a = [&](int kt) {
+    const uint32_t ak = uniform((uint32_t)kt * (uint32_t)(kBK * 2));
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) ra[i] = buf_load16(rx, a_off[i], ak);
+  };
+  auto load_b = [&](int kt, StageB& st) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      st.b[s] = buf_load8(rw, b_off, uniform(((uint32_t)kt * 8u + 2u * (uint32_t)s) * (uint32_t)N * 4u));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = (kt * kBK + 32 * h) / G;
+      const uint32_t gs = uniform((uint32_t)g * (uint32_t)N * 2u);
+      st.sc[h] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off, (int)gs, 0);
+      st.zr[h] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rz, (int)s_off, (int)gs, 0);
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int o = tid + i * NT;
+      As[buf][(o >> 3) * kLdsRow + (o & 7)] = perm_pairs(ra[i]);
+    }
+  };
+
+  f32x16 acc[WMT][2];
+#pragma unroll
+  for (int i = 0; i < WMT; ++i) {
+    acc[i][0] = f32x16{};
+    acc[i][1] = f32x16{};
+  }
+
+  const int arow = wm * (32 * WMT) + l32;
+  auto compute = [&](const StageB& st, int buf) {
+    ColQ cq[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const ColQ2 q2 = make_colq2(st.sc[h], st.zr[h]);
+      cq[h][0] = colq_of<0>(q2);
+      cq[h][1] = colq_of<1>(q2);
+    }
+    const uint4* A = &As[buf][arow * kLdsRow + lhi];
+    auto dequant = [&](int s, f16x8 bf[2]) {
+      const uint32_t words[2] = {st.b[s].x, st.b[s].y};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        f16x2 d[4];
+        dq_word_fast(words[c], cq[s >> 1][c], mg, d);
+        bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
+      }
+    };
+    f16x8 af[2][WMT], bf[2][2];
+#pragma unroll
+    for (int mt = 0; mt < WMT; ++mt) af[0][mt] = __builtin_bit_cast(f16x8, A[mt * 32 * kLdsRow]);
+    dequant(0, bf[0]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < 4) {
+#pragma unroll
+        for (int mt = 0; mt < WMT; ++mt)
+          af[nxt][mt] = __builtin_bit_cast(f16x8, A[mt * 32 * kLdsRow + 2 * (s + 1)]);
+        dequant(s + 1, bf[nxt]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < WMT; ++mt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          acc[mt][c] =
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][mt], bf[cur][c], acc[mt][c], 0, 0, 0);
+#if W4A16_OCC2_INTERLEAVE
+      __builtin_amdgcn_sched_group_barrier(0x100, WMT, 0);   // DS reads
+#pragma unroll
+      for (int i = 0; i < 2 * WMT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, W4A16_OCC2_INTERLEAVE, 0);  // VALU
+      }
+#endif
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  StageB b0, b1;
+  load_a(0);
+  load_b(0, b0);
+  store_a(0);
+  __syncthreads();
+  load_a(1);
+  load_b(1, b1);
+  for (int kt = 0; kt < KT; kt += 2) {
+    compute(b0, 0);                 // step kt
+    store_a(1);                     // step kt+1
+    __syncthreads();
+    if (kt + 2 < KT) {
+      load_a(kt + 2);
+      load_b(kt + 2, b0);
+    }
+    compute(b1, 1);                 // step kt+1
+    if (kt + 2 < KT) store_a(0);    // step kt+2
+    __syncthreads();
+    if (kt + 3 < KT) {
+      load_a(kt + 3);
+      load_b(kt + 3, b1);
+    }
+  }
+
+  if (!nv) return;
+  f16 bv0 = (f16)0.0f, bv1 = (f16)0.0f;
+  if (bias) {
+    const uint32_t b2 = *reinterpret_cast<const uint32_t*>(bias + ncol);
+    bv0 = as_h(b2 & 0xFFFFu);
+    bv1 = as_h(b2 >> 16);
+  }
+#pragma unroll
+  for (int mt = 0; mt < WMT; ++mt) {
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const int row = m0 + wm * (32 * WMT) + mt * 32 + 8 * (a >> 2) + 4 * lhi + (a & 3);
+      if (row < M) {
+        f16x2 o;
+        o.x = f32_to_f16(acc[mt][0][a]);
+        o.y = f32_to_f16(acc[mt][1][a]);
+        if (bias) {
+          o.x = o.x + bv0;
+          o.y = o.y + bv1;
+        }
+        *reinterpret_cast<f16x2*>(Y + (size_t)row * N + ncol) = o;
+      }
+    }
+  }
+}
+
+template <int WMT, int WAVES_M, int WAVES_N>
+hipError_t launch_occ2(const GemmArgs& a, hipStream_t st) {
+  constexpr int BM = 32 * WMT * WAVES_M;
+  constexpr int BN = 64 * WAVES_N;
+  dim3 grid(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((mfma_occ2_kernel<WMT, WAVES_M, WAVES_N>), grid,
+                     dim3(64 * WAVES_M * WAVES_N), 0, st, static_cast<const f16*>(a.x),
+                     reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
+                     static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
+                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+  return hipGetLastError();
+}
+
 template <int WMT, int WAVES_M, int WAVES_N>
 hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = 32 * WMT * WAVES_M;
@@ -290,13 +521,31 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 // cfg 1: 128 x 256 (2 x 2 waves, each 64 x 128)
 // cfg 2:  32 x 512 (4 waves along N, each 32 x 128)
 // cfg 3:  64 x 512 (4 waves along N, each 64 x 128)
+// cfg 4: 256 x 256 with the weight tile dequantised once into LDS (gemm_lds.hip)
+// cfg 5: 256 x 128, two waves per SIMD (2 x 2 waves, each 128 x 64)
+// cfg 6: 128 x 256, two waves per SIMD (1 x 4 waves, each 128 x 64)
+// cfg 7: 128 x 256, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
+// cfg 8: 256 x 128, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
     case 0: return {128, 512};
     case 1: return {128, 256};
     case 2: return {32, 512};
+    case 4: return {256, 256};
+    case 5: return {256, 128};
+    case 6: return {128, 256};
+    case 7: return {128, 256};
+    case 8: return {256, 128};
     default: return {64, 512};
   }
+}
+
+bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
+  if (cfg < 0 || cfg >= kMfmaConfigs) return false;
+  if (cfg == 4) return lds_gemm_applicable(M, N, K, G);
+  if (cfg == 5 || cfg == 6) return K % (2 * kBK) == 0;
+  if (cfg == 7 || cfg == 8) return occ2_gemm_applicable(M, N, K, G);
+  return true;
 }
 
 bool operands_fit(int M, int N, int K, int G) {
@@ -313,6 +562,17 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
     case 1: return launch_cfg<2, 2, 2>(a, st);
     case 2: return launch_cfg<1, 1, 4>(a, st);
     case 3: return launch_cfg<2, 1, 4>(a, st);
+    case 4:
+      if (!lds_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
+      return launch_lds_gemm(a, st);
+    case 5:
+      if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
+      return launch_occ2<4, 2, 2>(a, st);
+    case 6:
+      if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
+      return launch_occ2<4, 1, 4>(a, st);
+    case 7: return launch_occ2_gemm(a, false, st);
+    case 8: return launch_occ2_gemm(a, true, st);
     default: return hipErrorInvalidValue;
   }
 }

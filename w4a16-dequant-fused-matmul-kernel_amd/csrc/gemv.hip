@@ -131,11 +131,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   auto process = [&](const Batch& b, int r0, int le, int c0) {
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      ColQ cq4[4];
-      cq4[0] = make_colq(b.s[h].x & 0xFFFFu, b.z[h].x & 0xFFFFu);
-      cq4[1] = make_colq(b.s[h].x >> 16, b.z[h].x >> 16);
-      cq4[2] = make_colq(b.s[h].y & 0xFFFFu, b.z[h].y & 0xFFFFu);
-      cq4[3] = make_colq(b.s[h].y >> 16, b.z[h].y >> 16);
+      const ColQ2 p01 = make_colq2(b.s[h].x, b.z[h].x), p23 = make_colq2(b.s[h].y, b.z[h].y);
+      const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu) {
         const int u = h * 4 + uu;

@@ -47,6 +47,30 @@ __device__ __forceinline__ ColQ make_colq(uint16_t sbits, uint16_t zbits) {
   return c;
 }
 
+// Two columns' scale/zero state, packed: lane c of each pair is column c.
+// Used through colq_of<c>(), whose broadcasts fold into the packed ops' op_sel.
+struct ColQ2 {
+  f16x2 s, za, zb;   // scales, 1024 + zeros, 64 + zeros
+};
+
+__device__ __forceinline__ ColQ2 make_colq2(uint32_t sbits2, uint32_t zbits2) {
+  const f16x2 z = as_h2(zbits2);
+  ColQ2 q;
+  q.s = as_h2(sbits2);
+  q.za = z + f16x2{(f16)1024.0f, (f16)1024.0f};
+  q.zb = z + f16x2{(f16)64.0f, (f16)64.0f};
+  return q;
+}
+
+template <int C>
+__device__ __forceinline__ ColQ colq_of(const ColQ2& q) {
+  ColQ c;
+  c.s = __builtin_shufflevector(q.s, q.s, C, C);
+  c.z0 = __builtin_shufflevector(q.za, q.za, C, C);
+  c.z1 = __builtin_shufflevector(q.zb, q.zb, C, C);
+  return c;
+}
+
 // (w & mask) | magic in one v_and_or_b32.  gfx9 VOP3 encodings take no literal
 // constants and read at most one SGPR, so the mask rides in an SGPR and the
 // magic in a VGPR that the caller materialises once (MagicRegs).
@@ -98,11 +122,13 @@ __device__ __forceinline__ void dq_word(uint32_t w, const ColQ& c, f16x2 d[4]) {
 // Permute eight consecutive fp16 activations x0..x7 (four dwords, natural order)
 // into pair order (x0,x4) (x1,x5) (x2,x6) (x3,x7).
 __device__ __forceinline__ uint4 perm_pairs(uint4 v) {
+  // each output dword takes two 16-bit halves of two input dwords: one
+  // v_perm_b32 each (selector bytes index {v.z, v.x} / {v.w, v.y} as 7..0)
   uint4 r;
-  r.x = (v.x & 0xFFFFu) | (v.z << 16);
-  r.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-  r.z = (v.y & 0xFFFFu) | (v.w << 16);
-  r.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+  r.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);   // x.lo, z.lo
+  r.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);   // x.hi, z.hi
+  r.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);   // y.lo, w.lo
+  r.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);   // y.hi, w.hi
   return r;
 }
 

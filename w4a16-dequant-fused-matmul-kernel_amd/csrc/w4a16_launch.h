@@ -43,10 +43,19 @@ hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws
 struct MfmaTile {
   int bm, bn;
 };
-constexpr int kMfmaConfigs = 4;
+constexpr int kMfmaConfigs = 9;
 MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
+// Whether tile configuration `cfg` can run this shape (some need K % 64 or 128).
+bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G);
 hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st);
+// The 256 x 256 LDS-staged-weight kernel (mfma cfg 4): needs K % 64 == 0.
+bool lds_gemm_applicable(int M, int N, int K, int G);
+hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
+// Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256, cfg 8: 256 x 128):
+// needs K % 64 == 0.
+bool occ2_gemm_applicable(int M, int N, int K, int G);
+hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, hipStream_t st);
 
 // Buffer-addressed kernels need every operand below 2 GiB.
 bool operands_fit(int M, int N, int K, int G);
