@@ -51,6 +51,10 @@ def _args():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the workload for rocprofv3 --pmc: a 256 MiB copy (calibration), "
                          "8 cold C2 decode calls, 3 C4 M=4096 prefill calls; no timing")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.json from the counter_collection.csv files "
+                         "of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "--traffic-probe")
     return ap.parse_args()
 
 
@@ -178,23 +182,72 @@ def traffic_probe() -> None:
     print("C4 M=4096 x3", flush=True)
 
 
-def _traffic_for(kernel_prefix: str):
-    """HBM bytes per launch measured for a kernel (profiles/traffic.json), or None."""
+def _counter_rows(path: str, counter: str):
+    """(dispatch id, kernel name, value) per dispatch from a rocprofv3 counter CSV."""
+    import csv
+
+    rows = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            d = int(r["Dispatch_Id"])
+            name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            rows[d] = (name, rows.get(d, (name, 0.0))[1] + v)
+    return [(d, n, v) for d, (n, v) in sorted(rows.items())]
+
+
+def traffic_from(fetch_csv: str, write_csv: str) -> dict:
+    """HBM bytes per launch of the C2 and C4 GEMM kernels from --traffic-probe's
+    counters.  FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; each is scaled by
+    what it reads for the calibration copy (the probe's first three copy
+    dispatches, 256 MiB read and 256 MiB written each)."""
+    out = {"calibration": {"copy_bytes": 256 << 20}, "kernels": {}}
+    per = {}
+    for key, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"),
+                               ("write", write_csv, "WRITE_SIZE")):
+        rows = _counter_rows(path, counter)
+        copies = [v for _, n, v in rows if "copy" in n.lower()][:3]
+        if len(copies) < 3:
+            raise SystemExit(f"{path}: calibration copies not found")
+        raw = sum(copies) / len(copies)
+        scale = (256 << 10) / raw
+        out["calibration"][f"{key}_size_kib_raw"] = raw
+        out["calibration"][f"{key}_scale"] = scale
+        gemm = [(n, v) for _, n, v in rows if "w4a16" in n
+                and not any(t in n for t in ("quantize", "pack", "dequant"))]
+        if len(gemm) != 11:
+            raise SystemExit(f"{path}: expected 8 C2 + 3 C4 GEMM dispatches, got {len(gemm)}")
+        per[key] = {"C2": (gemm[0][0], gemm[:8]), "C4_M4096": (gemm[8][0], gemm[8:])}
+        for wkey, (name, ds) in per[key].items():
+            e = out["kernels"].setdefault(wkey, {"kernel": name})
+            e[f"{key}_kib_raw"] = sum(v for _, v in ds) / len(ds)
+            e[f"{key}_bytes"] = e[f"{key}_kib_raw"] * 1024 * scale
+    for e in out["kernels"].values():
+        e["bytes_per_launch"] = int(round(e["fetch_bytes"] + e["write_bytes"]))
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(out, f, indent=1)
+    return out
+
+
+def _traffic_for(workload: str):
+    """HBM bytes per launch measured for a workload's kernel (profiles/traffic.json),
+    or None when no measurement is recorded."""
     try:
         with open(TRAFFIC_JSON) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    for k, v in t.get("kernels", {}).items():
-        if k.startswith(kernel_prefix):
-            return v.get("bytes_per_launch")
-    return None
+    return t.get("kernels", {}).get(workload, {}).get("bytes_per_launch")
 
 
 def main() -> int:
     args = _args()
     if args.traffic_probe:
         traffic_probe()
+        return 0
+    if args.traffic_from:
+        print(json.dumps(traffic_from(*args.traffic_from), indent=1))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -232,7 +285,7 @@ def main() -> int:
                    "timing": "HIP graph of K calls, HIP events" if graph else "eager, HIP events"},
         "roofline": {"bound": "hbm", "achieved": round(head["GB/s"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4),
-                     "traffic": _traffic_for("gemv")},
+                     "traffic": _traffic_for("C2")},
     }
     if not args.no_secondary:
         c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
@@ -245,7 +298,7 @@ def main() -> int:
             "roofline": {"bound": "mfma", "achieved": round(sec["TFLOP/s"], 2),
                          "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
-                         "traffic": _traffic_for("mfma")},
+                         "traffic": _traffic_for("C4_M4096")},
         }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c2)
