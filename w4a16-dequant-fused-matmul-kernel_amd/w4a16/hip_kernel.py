@@ -5,12 +5,15 @@ Drop-in for the reference's primary backend ``w4a16_matmul``
 preconditions raised as ``AssertionError`` (:153-187), optional ``out``.  The
 kernel is chosen inside ``libw4a16.so`` by shape:
 
-* M <= 8: decode GEMV -- VALU v_dot2_f32_f16, no MFMA, split-K across
-  workgroups with a deterministic in-kernel reduction;
-* M > 8: prefill GEMM -- v_mfma_f32_32x32x16_f16, weights dequantised in
-  registers, activations staged through LDS;
-* shapes the vector kernels do not take (N % 4 != 0, misaligned views): the
-  sequential-k SIMT kernel.
+* M <= 8: decode GEMV -- VALU v_dot2_f32_f16, no MFMA, column blocks wide
+  enough to give every CU a workgroup, split-K only when N is too narrow;
+* 9 <= M <= 64: skinny GEMM on v_mfma_f32_16x16x32_f16, 16 columns per
+  workgroup over the whole of K;
+* M > 64: prefill GEMM on MFMA, tile configuration by shape (two waves per
+  SIMD with 128 x 256 tiles for large M);
+* shapes the vector kernels do not take (N % 4 != 0 beyond the skinny range,
+  G % 32 != 0, misaligned views, operands >= 2 GiB): the sequential-k SIMT
+  kernel.
 
 Group size: the reference's Triton path needs every autotune BLOCK_K to divide
 G (:177-182), i.e. G % 64 == 0.  These kernels need G % 32 == 0, so G = 32 works
@@ -133,7 +136,9 @@ def w4a16_linear(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor,
 
 def plan_for(M: int, N: int, K: int, group_size: int, kernel: str | int = 0,
              split_k: int = 0) -> "_lib.Plan":
-    """The launch plan for a shape; `kernel` may force "gemv", "mfma" or "simt"."""
+    """The launch plan for a shape; `kernel` may force "gemv", "mfma", "simt" or
+    "skinny" (the plan's ``tile_cfg`` then selects the MFMA tile configuration
+    or the GEMV wave count)."""
     if isinstance(kernel, str):
         kernel = {"auto": 0, "gemv": 1, "mfma": 2, "simt": 3, "skinny": 4}[kernel]
     return _lib.plan(M, N, K, group_size, kernel, split_k)
