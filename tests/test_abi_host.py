@@ -92,7 +92,7 @@ def test_split_k_gemv_requires_workspace(lib):
                                       a, 16, NULL)
     assert code == -4
     # a wave configuration the kernel does not have
-    p.tile_cfg = 2
+    p.tile_cfg = 3
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       a, 1 << 30, NULL)
     assert code == -5

@@ -119,13 +119,13 @@ RAGGED = [
 
 @pytest.mark.parametrize("M,K,N,G", RAGGED)
 def test_gemv_splits(M, K, N, G):
-    """Decode GEMV with every column-block width, both wave counts (4 and 8
-    waves per workgroup) and k-splits 1, 2, 3, 7, auto."""
+    """Decode GEMV with every column-block width, every wave count (4, 8, and
+    16 waves per workgroup for M <= 2) and k-splits 1, 2, 3, 7, auto."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M + K)
     ref = _ref(X, qw, s, z, G)
-    for cfg in (0, 1):
+    for cfg in ((0, 1, 2) if M <= 2 else (0, 1)):
         for cols in (16, 32, 64, 256):
             for split in (1, 2, 3, 7, 0):
                 if split > K // 8:
@@ -147,16 +147,16 @@ def test_gemv_splits(M, K, N, G):
 ])
 def test_mfma_tile_configs(M, K, N, G):
     """Prefill MFMA kernels with every tile configuration over tails in M, N, K
-    (config 4, the LDS-staged 256 x 256 kernel, and configs 7 and 8, two waves
-    per SIMD with 16x16x32 MFMAs, where K % 64 == 0; configs 5 and 6, two
-    waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0)."""
+    (configs 4, 9, 10 -- weight tile dequantised into LDS -- and 7, 8 -- two
+    waves per SIMD with 16x16x32 MFMAs -- where K % 64 == 0; configs 5 and 6,
+    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 3 + N)
     ref = _ref(X, qw, s, z, G)
-    for cfg in range(9):
-        if (cfg in (4, 7, 8) and K % 64) or (cfg in (5, 6) and K % 128):
+    for cfg in range(11):
+        if (cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128):
             continue
         p = plan_for(M, N, K, G, "mfma")
         p.tile_cfg = cfg

@@ -185,7 +185,7 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
-          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n) || !gemv_cfg_valid(p->tile_cfg))
+          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n) || !gemv_cfg_valid(p->tile_cfg, (int)M))
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;

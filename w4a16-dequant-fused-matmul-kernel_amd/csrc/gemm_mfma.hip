@@ -526,6 +526,8 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 // cfg 6: 128 x 256, two waves per SIMD (1 x 4 waves, each 128 x 64)
 // cfg 7: 128 x 256, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
 // cfg 8: 256 x 128, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
+// cfg 9: 256 x 224, 8 waves sharing an LDS-dequantised weight tile (gemm_ldsb.hip)
+// cfg 10: 256 x 256, as cfg 9
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
     case 0: return {128, 512};
@@ -536,6 +538,8 @@ MfmaTile mfma_tile(int cfg) {
     case 6: return {128, 256};
     case 7: return {128, 256};
     case 8: return {256, 128};
+    case 9: return {256, 224};
+    case 10: return {256, 256};
     default: return {64, 512};
   }
 }
@@ -545,6 +549,7 @@ bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
   if (cfg == 4) return lds_gemm_applicable(M, N, K, G);
   if (cfg == 5 || cfg == 6) return K % (2 * kBK) == 0;
   if (cfg == 7 || cfg == 8) return occ2_gemm_applicable(M, N, K, G);
+  if (cfg == 9 || cfg == 10) return ldsb_gemm_applicable(M, N, K, G);
   return true;
 }
 
@@ -573,6 +578,8 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
       return launch_occ2<4, 1, 4>(a, st);
     case 7: return launch_occ2_gemm(a, false, st);
     case 8: return launch_occ2_gemm(a, true, st);
+    case 9: return launch_ldsb_gemm(a, false, st);
+    case 10: return launch_ldsb_gemm(a, true, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -154,7 +154,10 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
       cq[h][2] = colq_of<0>(p23);
       cq[h][3] = colq_of<1>(p23);
     }
-    if (more) load_scales(kt + 1, st);
+    // the next step's group(s); with one group per step (G % 64 == 0) they are
+    // reloaded only when the group changes
+    const bool same_group = G64 && ((kt + 1) * kBK) / G == (kt * kBK) / G;
+    if (more && !same_group) load_scales(kt + 1, st);
     const uint4* A = &As[buf][arow * kLdsRow + oct];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

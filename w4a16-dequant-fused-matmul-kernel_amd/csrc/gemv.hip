@@ -41,7 +41,8 @@ constexpr int kNonTemporal = 2;           // buffer-load cache policy: nt
 template <int WAVES>
 struct GemvShape {
   static constexpr int kThreads = 64 * WAVES;
-  static constexpr int kBatch = WAVES >= 8 ? 4 : 8;   // packed rows per batch
+  // packed rows per batch: fewer rows per lane as the wave count grows
+  static constexpr int kBatch = WAVES >= 16 ? 2 : WAVES >= 8 ? 4 : 8;
 };
 
 template <int MT, int CWL, int WAVES>
@@ -52,7 +53,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     int S, int nblk) {
   constexpr int kThreads = GemvShape<WAVES>::kThreads;
   constexpr int BR = GemvShape<WAVES>::kBatch;
-  constexpr int H = BR / 4;                // 4-row halves per batch (one group each)
+  constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
+  constexpr int H = BR / RH;               // halves per batch
   constexpr bool XD = MT <= 2;             // activations read directly from global
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       // the group differs between row-lanes: its offset goes in the VGPR operand
-      const int g = min(((r0 + 4 * h) * 8) / G, NG - 1);
+      const int g = min(((r0 + RH * h) * 8) / G, NG - 1);
       const uint32_t so = nv ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
       b.s[h] = buf_load8(rs, so, 0u);
       b.z[h] = buf_load8(rz, so, 0u);
@@ -134,8 +136,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       const ColQ2 p01 = make_colq2(b.s[h].x, b.z[h].x), p23 = make_colq2(b.s[h].y, b.z[h].y);
       const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
 #pragma unroll
-      for (int uu = 0; uu < 4; ++uu) {
-        const int u = h * 4 + uu;
+      for (int uu = 0; uu < RH; ++uu) {
+        const int u = h * RH + uu;
         const int r = r0 + u;
         if (r >= le) break;
         f16x2 d[4][4];
@@ -330,6 +332,10 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int waves_cfg, int split, void
   switch (waves_cfg) {
     case 0: return launch_w<MT, 4>(a, cols, split, ws, st);
     case 1: return launch_w<MT, 8>(a, cols, split, ws, st);
+    case 2:
+      // 16 waves: only for M <= 2 (the reduction buffer grows with waves x M)
+      if constexpr (MT <= 2) return launch_w<MT, 16>(a, cols, split, ws, st);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -337,7 +343,7 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int waves_cfg, int split, void
 }  // namespace
 
 bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 || cols == 256; }
-bool gemv_cfg_valid(int cfg) { return cfg >= 0 && cfg < kGemvConfigs; }
+bool gemv_cfg_valid(int cfg, int M) { return cfg >= 0 && cfg < kGemvConfigs && (cfg < 2 || M <= 2); }
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;

@@ -21,10 +21,10 @@ struct GemmArgs {
 
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
 // consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
-// picks 4 (cfg 0) or 8 (cfg 1) waves per workgroup; with split > 1, `ws` holds
-// the counters + fp32 partials of gemv_workspace_bytes().
+// picks 4 (cfg 0), 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup; with
+// split > 1, `ws` holds the counters + fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
-constexpr int kGemvConfigs = 2;
+constexpr int kGemvConfigs = 3;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
 // other's outstanding loads (measured faster on MI355X for M = 1 decode shapes).
 constexpr int kGemvDefaultConfig = 1;
@@ -33,7 +33,7 @@ constexpr int kGemvDefaultConfig = 1;
 constexpr int kGemvMaxCounterBlocks = 16384;
 constexpr size_t kGemvCounterBytes = (size_t)kGemvMaxCounterBlocks * 4;
 bool gemv_cols_valid(int cols);
-bool gemv_cfg_valid(int cfg);
+bool gemv_cfg_valid(int cfg, int M);
 size_t gemv_workspace_bytes(int M, int N, int K, int split);
 int gemv_rows_per_split(int K, int split);
 hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws,
@@ -43,7 +43,7 @@ hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws
 struct MfmaTile {
   int bm, bn;
 };
-constexpr int kMfmaConfigs = 9;
+constexpr int kMfmaConfigs = 11;
 MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
 // Whether tile configuration `cfg` can run this shape (some need K % 64 or 128).
@@ -56,6 +56,10 @@ hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
 // needs K % 64 == 0.
 bool occ2_gemm_applicable(int M, int N, int K, int G);
 hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, hipStream_t st);
+// Eight-wave kernel with the weight tile dequantised into LDS (mfma cfg 9:
+// 256 x 224, cfg 10: 256 x 256): needs K % 64 == 0.
+bool ldsb_gemm_applicable(int M, int N, int K, int G);
+hipError_t launch_ldsb_gemm(const GemmArgs& a, bool wide, hipStream_t st);
 
 // Buffer-addressed kernels need every operand below 2 GiB.
 bool operands_fit(int M, int N, int K, int G);
