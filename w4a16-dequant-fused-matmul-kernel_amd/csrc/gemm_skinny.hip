@@ -35,7 +35,10 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 
-template <int MT>
+// GSTEP = k-steps per quantisation group inside an aligned 8-step batch (G/32
+// when that is 1, 2, 4 or 8; 8 for larger powers of two): scales and zeros are
+// loaded once per group.  GSTEP = 1 loads them every k-step (any G % 32 == 0).
+template <int MT, int GSTEP>
 __global__ __launch_bounds__(kThreads) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
@@ -65,8 +68,9 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
 
-  // this wave's k-steps [kb, ke)
-  const int per = (KS + kWaves - 1) / kWaves;
+  // this wave's k-steps [kb, ke): whole 8-step batches, so batch starts are
+  // multiples of 8 k-steps (256 k) and group boundaries fall on fixed slots
+  const int per = ((KS + kWaves - 1) / kWaves + kBatch - 1) / kBatch * kBatch;
   const int kb = min(KS, wave * per);
   const int ke = min(KS, kb + per);
 
@@ -92,10 +96,14 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(
       if (ks < ke) {   // wave-uniform
         const uint32_t wk = uniform((uint32_t)ks * 4u * (uint32_t)N * 4u);
         b.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
-        const uint32_t gk = uniform((uint32_t)((ks * 32) / G) * (uint32_t)N * 2u);
-        const uint32_t sv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
-        const uint32_t zv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
-        b.sz[j] = (sv & 0xFFFFu) | (zv << 16);
+        if (j % GSTEP == 0) {
+          const uint32_t gk = uniform((uint32_t)((ks * 32) / G) * (uint32_t)N * 2u);
+          const uint32_t sv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
+          const uint32_t zv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
+          b.sz[j] = (sv & 0xFFFFu) | (zv << 16);
+        } else {
+          b.sz[j] = b.sz[j - j % GSTEP];   // same group as the batch slot it copies
+        }
         const uint32_t xk = uniform((uint32_t)ks * 64u);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
@@ -157,15 +165,28 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(
   }
 }
 
-template <int MT>
-hipError_t launch_mt(const GemmArgs& a, hipStream_t st) {
+template <int MT, int GSTEP>
+hipError_t launch_g(const GemmArgs& a, hipStream_t st) {
   const int nblk = (a.N + 15) / 16;
-  hipLaunchKernelGGL((skinny_kernel<MT>), dim3(nblk), dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP>), dim3(nblk), dim3(kThreads), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
                      a.G, nblk);
   return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_mt(const GemmArgs& a, hipStream_t st) {
+  // batch slots per group when group boundaries land on fixed slots of an
+  // aligned 8-step (256-k) batch: G / 32 a power of two
+  const int gs = a.G / 32;
+  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, st);
+  switch (gs) {
+    case 4: return launch_g<MT, 4>(a, st);
+    case 2: return launch_g<MT, 2>(a, st);
+    default: return launch_g<MT, 1>(a, st);
+  }
 }
 
 }  // namespace
