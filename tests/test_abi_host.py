@@ -173,6 +173,26 @@ def test_planner_gemv_split_fills_device():
     assert p1.split_k == 1 and p1.workspace_bytes == 0
 
 
+def test_planner_prefill_split_k():
+    from w4a16 import _lib
+
+    # C5 down-projection at M = 256: 64 tiles of 128 x 256 -> split along K
+    p = _lib.plan(256, 8192, 28672, 128)
+    assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 7
+    assert p.split_k > 1 and p.grid_x >= 256
+    assert p.workspace_bytes >= p.split_k * 256 * 8192 * 4
+    # large M: no split, no workspace
+    p = _lib.plan(4096, 14336, 4096, 128)
+    assert p.split_k == 1 and p.workspace_bytes == 0 and p.tile_cfg == 7
+    # a forced split on a tile configuration without split-K support is refused
+    q = _lib.plan(256, 8192, 28672, 128, _lib.KERNEL_MFMA, 4)
+    q.tile_cfg = 6
+    a = ctypes.c_void_p(1 << 12)
+    lib = _lib.load()
+    assert lib.w4a16_gemm_f16_planned(ctypes.byref(q), a, a, a, a, NULL, a, 256, 8192, 28672,
+                                      128, a, 1 << 30, NULL) == -5
+
+
 def test_planner_forced_kernel_must_fit():
     from w4a16 import _lib
 

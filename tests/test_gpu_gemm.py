@@ -158,7 +158,7 @@ def test_mfma_tile_configs(M, K, N, G):
     for cfg in range(11):
         if (cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128):
             continue
-        p = plan_for(M, N, K, G, "mfma")
+        p = plan_for(M, N, K, G, "mfma", 1)
         p.tile_cfg = cfg
         log(f"mfma M={M} K={K} N={N} G={G} cfg={cfg}")
         out = w4a16_matmul_planned(X, qw, s, z, G, p)
@@ -166,6 +166,35 @@ def test_mfma_tile_configs(M, K, N, G):
         b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
         assert torch.equal(w4a16_matmul_planned(X, qw, s, z, G, p, bias=b), out + b)
     assert _lib.KERNEL_NAMES[p.kernel] == "mfma"
+
+
+@pytest.mark.parametrize("M,K,N,G", [
+    (65, 4096, 1028, 128), (200, 2048, 516, 32), (256, 11008, 772, 64), (130, 2112, 260, 96),
+])
+def test_mfma_split_k(M, K, N, G):
+    """Prefill split-K (cfg 7 and 8): fp32 partials per k-split, summed in split
+    order by a second kernel; every split count, fused bias; then a GEMV split-K
+    call on the same cached workspace still sees zeroed counters."""
+    from w4a16 import w4a16_matmul
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+
+    X, qw, s, z = _build_case(M, K, N, G, seed=M + N + K)
+    ref = _ref(X, qw, s, z, G)
+    b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
+    for cfg in (7, 8):
+        for split in (2, 3, 5, K // 64):
+            p = plan_for(M, N, K, G, "mfma", split)
+            p.tile_cfg = cfg
+            assert p.split_k > 1 and p.workspace_bytes > 0
+            log(f"mfma split-K M={M} K={K} N={N} G={G} cfg={cfg} split={p.split_k}")
+            out = w4a16_matmul_planned(X, qw, s, z, G, p)
+            assert_gemm_close(out, ref, f"split-K cfg={cfg} split={p.split_k}")
+            outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
+            assert torch.equal(outb, out + b)
+    Xg, qg, sg, zg = _build_case(1, 4096, 1024, 128, seed=5)
+    assert plan_for(1, 1024, 4096, 128).split_k > 1
+    assert_gemm_close(w4a16_matmul(Xg, qg, sg, zg, 128), _ref(Xg, qg, sg, zg, 128),
+                      "GEMV split-K after prefill split-K")
 
 
 @pytest.mark.parametrize("M,K,N,G", [

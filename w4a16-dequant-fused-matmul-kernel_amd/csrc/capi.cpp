@@ -86,16 +86,32 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
 //   * M >= 1024: the two-waves-per-SIMD 16x16x32 kernel, 128 x 256 (cfg 7);
 //   * enough 128 x 256 tiles for half the CUs: two-waves-per-SIMD 32x32x16,
 //     128 x 256 (cfg 6);
-//   * fewer tiles (short M, narrow N): narrow 32 x 512 tiles for more
-//     workgroups (cfg 2), else the one-wave-per-SIMD 128 x 256 (cfg 1).
-int mfma_cfg_auto(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  if (M <= 64) return 2;
+//   * fewer tiles (short M, narrow N): cfg 7 split along K so that the tiles
+//     times the splits give every CU a workgroup (fp32 partials + one
+//     reduction kernel), when K allows at least 8 k-steps per split; else
+//     narrow 32 x 512 tiles (cfg 2) or the one-wave 128 x 256 (cfg 1).
+struct MfmaChoice {
+  int cfg, split;
+};
+MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  if (M <= 64) return {2, 1};
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
-  if (M >= 1024 && mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) return 7;
-  if (2 * t6 >= cus && mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return 6;
+  if (M >= 1024 && mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) return {7, 1};
+  if (2 * t6 >= cus && mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return {6, 1};
+  if (mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) {
+    const int64_t kt = K / 64;
+    int64_t s = (cus + t6 - 1) / t6;
+    if (s > kt / 8) s = kt / 8;
+    if (s >= 2) return {7, occ2_splits((int)K, (int)s)};
+  }
   const int64_t t2 = ((N + 511) / 512) * ((M + 31) / 32);
-  if (2 * t6 < cus && t2 > t6) return 2;
-  return 1;
+  if (2 * t6 < cus && t2 > t6) return {2, 1};
+  return {1, 1};
+}
+
+size_t mfma_workspace_bytes(int64_t M, int64_t N, int64_t K, int split) {
+  const size_t part = occ2_workspace_bytes((int)M, (int)N, (int)K, split);
+  return part ? kGemvCounterBytes + part : 0;   // partials after the GEMV counters
 }
 
 int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_t split,
@@ -141,13 +157,21 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     }
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G)) return W4A16_ERR_BAD_PLAN;
-      const int cfg = mfma_cfg_auto(M, N, K, G, cus);
-      const MfmaTile t = mfma_tile(cfg);
-      p->tile_cfg = cfg;
+      MfmaChoice c = mfma_choice(M, N, K, G, cus);
+      if (split > 0) {   // a forced split runs on cfg 7
+        c.cfg = split > 1 ? 7 : c.cfg;
+        c.split = split > 1 ? occ2_splits((int)K, split) : 1;
+        if (c.split > 1 && !mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G))
+          return W4A16_ERR_BAD_PLAN;
+      }
+      const MfmaTile t = mfma_tile(c.cfg);
+      p->tile_cfg = c.cfg;
+      p->split_k = c.split;
       p->tile_m = t.bm;
       p->tile_n = t.bn;
-      p->grid_x = ((N + t.bn - 1) / t.bn) * ((M + t.bm - 1) / t.bm);
+      p->grid_x = ((N + t.bn - 1) / t.bn) * ((M + t.bm - 1) / t.bm) * c.split;
       p->grid_y = 1;
+      p->workspace_bytes = (int64_t)mfma_workspace_bytes(M, N, K, c.split);
       return W4A16_OK;
     }
     case W4A16_KERNEL_SKINNY:
@@ -198,12 +222,19 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
     }
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G) || !fits(M, N, K, G) ||
-          !mfma_cfg_applicable(p->tile_cfg, (int)M, (int)N, (int)K, (int)G))
+          !mfma_cfg_applicable(p->tile_cfg, (int)M, (int)N, (int)K, (int)G) || p->split_k < 1 ||
+          (p->split_k > 1 && p->tile_cfg != 7 && p->tile_cfg != 8))
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
           !aligned(y, 8) || (bias && !aligned(bias, 8)))
         return W4A16_ERR_BAD_PLAN;
-      return to_status(launch_mfma(a, p->tile_cfg, s));
+      float* part = nullptr;
+      const size_t need = mfma_workspace_bytes(M, N, K, p->split_k);
+      if (need > 0) {
+        if (!ws || ws_bytes < need || !aligned(ws, 256)) return W4A16_ERR_WORKSPACE;
+        part = reinterpret_cast<float*>(static_cast<char*>(ws) + kGemvCounterBytes);
+      }
+      return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }
     case W4A16_KERNEL_SKINNY: {
       if (!skinny_applicable(M, G) || !fits(M, N, K, G)) return W4A16_ERR_BAD_PLAN;

@@ -561,7 +561,8 @@ bool operands_fit(int M, int N, int K, int G) {
 
 bool mfma_fits(int M, int N, int K, int G) { return operands_fit(M, N, K, G); }
 
-hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
+hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st) {
+  if (split > 1 && cfg != 7 && cfg != 8) return hipErrorInvalidValue;
   switch (cfg) {
     case 0: return launch_cfg<4, 1, 4>(a, st);
     case 1: return launch_cfg<2, 2, 2>(a, st);
@@ -576,8 +577,8 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st) {
     case 6:
       if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
       return launch_occ2<4, 1, 4>(a, st);
-    case 7: return launch_occ2_gemm(a, false, st);
-    case 8: return launch_occ2_gemm(a, true, st);
+    case 7: return launch_occ2_gemm(a, false, split, part, st);
+    case 8: return launch_occ2_gemm(a, true, split, part, st);
     case 9: return launch_ldsb_gemm(a, false, st);
     case 10: return launch_ldsb_gemm(a, true, st);
     default: return hipErrorInvalidValue;

@@ -48,7 +48,8 @@ template <int WAVES_M, int WAVES_N, bool G64>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                  const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
-                 const f16* __restrict__ bias, f16* __restrict__ Y, int M, int N, int K, int G) {
+                 const f16* __restrict__ bias, f16* __restrict__ Y, float* __restrict__ part,
+                 int M, int N, int K, int G, int KTS) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int BM = 16 * kMT * WAVES_M;
   constexpr int BN = 16 * kNTiles * WAVES_N;
@@ -68,11 +69,16 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   // round-robin; each XCD takes a contiguous run of an order that walks kGroupM
   // M-tiles x all N-tiles per group, so concurrent tiles share A rows and B
   // columns in that XCD's L2.
+  // With split-K (part != nullptr) the grid is tiles x splits: workgroup
+  // (tile T, split sp) accumulates k-steps [sp*KTS, (sp+1)*KTS).
   const int ntn = (N + BN - 1) / BN;
   const int ntm = (M + BM - 1) / BM;
   const int total = ntn * ntm;
-  int T = (int)blockIdx.x;
-  if ((total & 7) == 0) T = (T & 7) * (total >> 3) + (T >> 3);
+  const int nb = (int)gridDim.x;
+  int B = (int)blockIdx.x;
+  if ((nb & 7) == 0) B = (B & 7) * (nb >> 3) + (B >> 3);
+  const int sp = B / total;
+  const int T = B - sp * total;
   const int group = T / (kGroupM * ntn);
   const int first_m = group * kGroupM;
   const int gsz = min(ntm - first_m, kGroupM);
@@ -82,7 +88,8 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   const int ncol = n0 + wn * (16 * kNTiles) + 4 * l16;   // this lane's 4 columns
   const bool nv = ncol < N;
   const int KP = K >> 3;
-  const int KT = K / kBK;
+  const int KS0 = sp * KTS;                  // this workgroup's k-steps [KS0, KT)
+  const int KT = min(K / kBK, KS0 + KTS);
   const int NG = K / G;
   constexpr int NH = G64 ? 1 : 2;   // groups per 64-k step (G % 64 == 0: one)
 
@@ -192,19 +199,34 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   };
 
   StageB sb;
-  load_a(0);
-  load_w(0, 0, sb);
-  load_w(0, 1, sb);
-  load_scales(0, sb);
+  load_a(KS0);
+  load_w(KS0, 0, sb);
+  load_w(KS0, 1, sb);
+  load_scales(KS0, sb);
   store_a(0);
   __syncthreads();
-  if (KT > 1) load_a(1);
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
+  if (KS0 + 1 < KT) load_a(KS0 + 1);
+  for (int kt = KS0; kt < KT; ++kt) {
+    const int buf = (kt - KS0) & 1;
     step(sb, kt, buf);
     if (kt + 1 < KT) store_a(buf ^ 1);   // step kt+1's activations
     __syncthreads();
     if (kt + 2 < KT) load_a(kt + 2);
+  }
+
+  if (part) {
+    // fp32 partial sums of this split, 4 columns per lane (16-byte stores)
+    if (!nv) return;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * (16 * kMT) + 16 * i + 4 * oct + r;
+        if (row < M)
+          *reinterpret_cast<float4*>(part + ((size_t)sp * M + row) * N + ncol) =
+              make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+      }
+    return;
   }
 
   if (!nv) return;
@@ -239,15 +261,56 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   }
 }
 
+// Y[row, 4c..4c+3] = fp16(sum over splits, in split order) (+ bias)
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part,
+                                                     const f16* __restrict__ bias,
+                                                     f16* __restrict__ Y, int M, int N, int S) {
+  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;   // 4-column quad index
+  const size_t nq = (size_t)M * (N / 4);
+  if (q >= nq) return;
+  const size_t off = q * 4;
+  float4 s = *reinterpret_cast<const float4*>(part + off);
+  for (int i = 1; i < S; ++i) {
+    const float4 v = *reinterpret_cast<const float4*>(part + (size_t)i * M * N + off);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  f16x4 o;
+  o.x = f32_to_f16(s.x);
+  o.y = f32_to_f16(s.y);
+  o.z = f32_to_f16(s.z);
+  o.w = f32_to_f16(s.w);
+  if (bias) {
+    const int col = (int)(off % (size_t)N);
+    o.x = o.x + bias[col];
+    o.y = o.y + bias[col + 1];
+    o.z = o.z + bias[col + 2];
+    o.w = o.w + bias[col + 3];
+  }
+  *reinterpret_cast<f16x4*>(Y + off) = o;
+}
+
 template <int WAVES_M, int WAVES_N, bool G64>
-hipError_t launch_wg(const GemmArgs& a, hipStream_t st) {
+hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
   constexpr int BM = 16 * kMT * WAVES_M;
   constexpr int BN = 16 * kNTiles * WAVES_N;
-  const dim3 grid(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((occ2_kernel<WAVES_M, WAVES_N, G64>), grid, dim3(64 * WAVES_M * WAVES_N), 0, st,
-                     static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+  const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+  const int KT = a.K / kBK;
+  const int kts = (KT + split - 1) / split;
+  const int nsplit = split > 1 ? (KT + kts - 1) / kts : 1;   // every split non-empty
+  hipLaunchKernelGGL((occ2_kernel<WAVES_M, WAVES_N, G64>), dim3(tiles * nsplit),
+                     dim3(64 * WAVES_M * WAVES_N), 0, st, static_cast<const f16*>(a.x),
+                     reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
+                     static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
+                     static_cast<f16*>(a.y), nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G,
+                     nsplit > 1 ? kts : KT);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nsplit == 1) return e;
+  const size_t nq = (size_t)a.M * (size_t)(a.N / 4);
+  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, part,
+                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, nsplit);
   return hipGetLastError();
 }
 
@@ -258,12 +321,30 @@ bool occ2_gemm_applicable(int M, int N, int K, int G) {
   return K % kBK == 0 && N % 4 == 0 && G % 32 == 0 && K % G == 0;
 }
 
-// waves 1 x 4: 128 x 256 tiles; waves 2 x 2: 256 x 128 tiles.
-hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, hipStream_t st) {
+int occ2_splits(int K, int split) {
+  const int KT = K / kBK;
+  if (split <= 1 || KT <= 1) return 1;
+  const int kts = (KT + split - 1) / split;
+  return (KT + kts - 1) / kts;
+}
+
+size_t occ2_workspace_bytes(int M, int N, int K, int split) {
+  const int s = occ2_splits(K, split);
+  return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+// waves 1 x 4: 128 x 256 tiles; waves 2 x 2: 256 x 128 tiles.  split > 1:
+// fp32 partials in `part` (occ2_workspace_bytes), then one reduction kernel.
+hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
+                            hipStream_t st) {
   if (!occ2_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
+  if (occ2_splits(a.K, split) > 1 && !part) return hipErrorInvalidValue;
   const bool g64 = a.G % 64 == 0;
-  if (tall) return g64 ? launch_wg<2, 2, true>(a, st) : launch_wg<2, 2, false>(a, st);
-  return g64 ? launch_wg<1, 4, true>(a, st) : launch_wg<1, 4, false>(a, st);
+  if (tall)
+    return g64 ? launch_wg<2, 2, true>(a, split, part, st)
+               : launch_wg<2, 2, false>(a, split, part, st);
+  return g64 ? launch_wg<1, 4, true>(a, split, part, st)
+             : launch_wg<1, 4, false>(a, split, part, st);
 }
 
 }  // namespace w4a16

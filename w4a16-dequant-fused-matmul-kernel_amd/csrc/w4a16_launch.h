@@ -48,14 +48,20 @@ MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
 // Whether tile configuration `cfg` can run this shape (some need K % 64 or 128).
 bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G);
-hipError_t launch_mfma(const GemmArgs& a, int cfg, hipStream_t st);
+// split > 1 (cfg 7 and 8 only): fp32 partials in `part`, occ2_workspace_bytes().
+hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st);
 // The 256 x 256 LDS-staged-weight kernel (mfma cfg 4): needs K % 64 == 0.
 bool lds_gemm_applicable(int M, int N, int K, int G);
 hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
 // Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256, cfg 8: 256 x 128):
 // needs K % 64 == 0.
 bool occ2_gemm_applicable(int M, int N, int K, int G);
-hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, hipStream_t st);
+// Split-K of cfg 7/8: the number of non-empty k-splits for a requested count,
+// and the fp32 partial buffer they need (0 when not split).
+int occ2_splits(int K, int split);
+size_t occ2_workspace_bytes(int M, int N, int K, int split);
+hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
+                            hipStream_t st);
 // Eight-wave kernel with the weight tile dequantised into LDS (mfma cfg 9:
 // 256 x 224, cfg 10: 256 x 256): needs K % 64 == 0.
 bool ldsb_gemm_applicable(int M, int N, int K, int G);

@@ -47,10 +47,11 @@ def on_device(device: torch.device):
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     """A zero-initialised workspace of at least `nbytes` for the current stream.
 
-    The GEMV split-K path keeps per-column-block counters in it and leaves them
-    zeroed after every call, so one buffer serves every later call on the same
-    stream.  Calls on one stream are ordered, so sharing is safe; each stream has
-    its own buffer.
+    The GEMV split-K path keeps per-column-block counters at its start and leaves
+    them zeroed after every call; split-K partial sums (GEMV and prefill) go
+    after that region and are rewritten by every call.  So one buffer serves
+    every later call on the same stream.  Calls on one stream are ordered, so
+    sharing is safe; each stream has its own buffer.
     """
     if nbytes <= 0:
         return None
