@@ -203,17 +203,21 @@ def test_mfma_split_k(M, K, N, G):
     (5, 320, 33, 32),
 ])
 def test_skinny_path(M, K, N, G):
-    """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0."""
+    """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
+    with 4 and (M <= 32) 8 waves per workgroup."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
-    log(f"skinny M={M} K={K} N={N} G={G}")
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
-    p = plan_for(M, N, K, G, "skinny")
-    out = w4a16_matmul_planned(X, qw, s, z, G, p)
-    assert_gemm_close(out, _ref(X, qw, s, z, G), "skinny")
+    ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
-    assert torch.equal(outb, out + b)
+    for cfg in ((0, 1) if M <= 32 else (0,)):      # 4 or 8 waves per workgroup
+        log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg}")
+        p = plan_for(M, N, K, G, "skinny")
+        p.tile_cfg = cfg
+        out = w4a16_matmul_planned(X, qw, s, z, G, p)
+        assert_gemm_close(out, ref, f"skinny cfg={cfg}")
+        outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
+        assert torch.equal(outb, out + b)
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 64, 130, 32), (17, 96, 7, 32), (4, 24, 12, 12), (2, 8, 5, 4)])

@@ -180,6 +180,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->tile_n = 16;
       p->grid_x = (N + 15) / 16;
       p->grid_y = 1;
+      // 8 waves per workgroup when the column blocks give about one per CU
+      p->tile_cfg = (M <= 32 && p->grid_x <= cus) ? 1 : 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
@@ -237,10 +239,12 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
       return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }
     case W4A16_KERNEL_SKINNY: {
-      if (!skinny_applicable(M, G) || !fits(M, N, K, G)) return W4A16_ERR_BAD_PLAN;
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 1 ||
+          (p->tile_cfg == 1 && M > 32))
+        return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 4) || !aligned(sc, 2) || !aligned(zr, 2))
         return W4A16_ERR_BAD_PLAN;
-      return to_status(launch_skinny(a, s));
+      return to_status(launch_skinny(a, p->tile_cfg, s));
     }
     case W4A16_KERNEL_SIMT:
       return to_status(launch_simt(a, s));

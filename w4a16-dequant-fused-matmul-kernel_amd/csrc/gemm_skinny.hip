@@ -11,7 +11,9 @@
 //   * in v_mfma_f32_16x16x32_f16 lane l holds B[k = 8*(l/16)..+7][n = l%16]: one
 //     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA,
 //     reading 4 packed rows x 64 bytes with one dword load per lane;
-//   * the 4 waves split K into contiguous runs; each wave walks its run in
+//   * the 4 waves (8 for M <= 32 when there is about one workgroup per CU:
+//     two per SIMD, twice the loads in flight) split K into contiguous runs of
+//     whole batches; each wave walks its run in
 //     batches of 8 k-steps (256 k) with two register batches used ping-pong, all
 //     loads of batch i+1 -- weights, scales, zeros and activations -- issued
 //     before batch i is consumed;
@@ -31,18 +33,17 @@
 namespace w4a16 {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
 constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 
 // GSTEP = k-steps per quantisation group inside an aligned 8-step batch (G/32
 // when that is 1, 2, 4 or 8; 8 for larger powers of two): scales and zeros are
 // loaded once per group.  GSTEP = 1 loads them every k-step (any G % 32 == 0).
-template <int MT, int GSTEP>
-__global__ __launch_bounds__(kThreads) void skinny_kernel(
+template <int MT, int GSTEP, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
     int N, int K, int G, int nblk) {
+  constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][64];
 
   const int nb = (int)gridDim.x;
@@ -166,9 +167,21 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(
 }
 
 template <int MT, int GSTEP>
-hipError_t launch_g(const GemmArgs& a, hipStream_t st) {
+hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
   const int nblk = (a.N + 15) / 16;
-  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP>), dim3(nblk), dim3(kThreads), 0, st,
+  // 8 waves (M <= 32 only, register budget): two per SIMD, twice the weight
+  // loads in flight per CU -- pays when there is about one workgroup per CU
+  if constexpr (MT <= 2) {
+    if (eight_waves) {
+      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 8>), dim3(nblk), dim3(512), 0, st,
+                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
+                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
+                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
+                         a.G, nblk);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4>), dim3(nblk), dim3(256), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
@@ -177,26 +190,28 @@ hipError_t launch_g(const GemmArgs& a, hipStream_t st) {
 }
 
 template <int MT>
-hipError_t launch_mt(const GemmArgs& a, hipStream_t st) {
+hipError_t launch_mt(const GemmArgs& a, bool w8, hipStream_t st) {
   // batch slots per group when group boundaries land on fixed slots of an
   // aligned 8-step (256-k) batch: G / 32 a power of two
   const int gs = a.G / 32;
-  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, st);
+  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, w8, st);
   switch (gs) {
-    case 4: return launch_g<MT, 4>(a, st);
-    case 2: return launch_g<MT, 2>(a, st);
-    default: return launch_g<MT, 1>(a, st);
+    case 4: return launch_g<MT, 4>(a, w8, st);
+    case 2: return launch_g<MT, 2>(a, w8, st);
+    default: return launch_g<MT, 1>(a, w8, st);
   }
 }
 
 }  // namespace
 
-hipError_t launch_skinny(const GemmArgs& a, hipStream_t st) {
+hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st) {
+  if (cfg == 1 && a.M > 32) return hipErrorInvalidValue;
+  const bool w8 = cfg == 1;
   switch ((a.M + 15) / 16) {
-    case 1: return launch_mt<1>(a, st);
-    case 2: return launch_mt<2>(a, st);
-    case 3: return launch_mt<3>(a, st);
-    case 4: return launch_mt<4>(a, st);
+    case 1: return launch_mt<1>(a, w8, st);
+    case 2: return launch_mt<2>(a, w8, st);
+    case 3: return launch_mt<3>(a, w8, st);
+    case 4: return launch_mt<4>(a, w8, st);
     default: return hipErrorInvalidValue;
   }
 }

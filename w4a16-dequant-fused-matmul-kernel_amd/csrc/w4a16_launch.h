@@ -72,7 +72,8 @@ bool operands_fit(int M, int N, int K, int G);
 
 // Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM.
 constexpr int kSkinnyMaxM = 64;
-hipError_t launch_skinny(const GemmArgs& a, hipStream_t st);
+// cfg 0: 4 waves per workgroup; cfg 1: 8 waves (M <= 32).
+hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st);
 
 // Sequential-k SIMT kernel: any N, any G dividing K, no alignment needs.
 hipError_t launch_simt(const GemmArgs& a, hipStream_t st);
