@@ -90,9 +90,10 @@ size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
  * Replaces the reference's fused entry point w4a16_matmul
  * (w4a16-kernel/src/w4a16/triton_kernel.py:131-200) and its native launcher
  * w4a16_gemm_cuda (w4a16-kernel/src/w4a16/cuda/w4a16_gemm.cu:76-115).
- * `workspace` must hold w4a16_gemm_workspace_bytes() bytes, zero-filled before
- * its first use; every call leaves it zero-filled again.  Calls that share one
- * workspace must be ordered (same stream).  M = 0 or N = 0 launches nothing;
+ * `workspace` (256-byte aligned) must hold w4a16_gemm_workspace_bytes() bytes
+ * of fp32 split-K partials; its contents need no initialisation and are
+ * overwritten by every call.  Calls that share one workspace must be ordered
+ * (same stream).  M = 0 or N = 0 launches nothing;
  * K = 0 writes y = 0 (x, qweight, scales and zeros may then be NULL).  The
  * library issues kernel launches only (no memset or copy), so calls can be
  * captured into a HIP graph.

@@ -81,9 +81,9 @@ def test_gemm_rejects_null_pointers(lib):
 def test_split_k_gemv_requires_workspace(lib):
     from w4a16 import _lib
 
-    # N = 1024 is too narrow to fill 256 CUs with 16-column blocks: split-K
-    p = _lib.plan(1, 1024, 4096, 128)
-    assert p.kernel == _lib.KERNEL_GEMV and p.split_k > 1 and p.workspace_bytes > 0
+    # a forced 4-way split-K GEMV needs 4 * M * N fp32 partials
+    p = _lib.plan(1, 1024, 4096, 128, _lib.KERNEL_GEMV, 4)
+    assert p.kernel == _lib.KERNEL_GEMV and p.split_k == 4 and p.workspace_bytes == 4 * 1024 * 4
     a = ctypes.c_void_p(1 << 12)   # aligned fake pointers: never dereferenced
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       NULL, 0, NULL)
@@ -157,18 +157,35 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     assert p.grid_x >= 1 and p.grid_y >= 1
 
 
-def test_planner_gemv_split_fills_device():
+def test_planner_gemv_split_rule():
+    """The automatic decode plan splits K four ways only for long K (>= 8192) with
+    fewer 16-column blocks than CUs (measured faster there, slower at K = 4096
+    and neutral at one block per CU); a forced split gives every split at least one packed row and
+    sizes the fp32 partials."""
     from w4a16 import _lib
 
-    for N in (1024, 4096, 6144, 28672):
+    lib = _lib.load()
+    for N in (512, 1024, 4096, 6144, 28672):
         p = _lib.plan(1, N, 4096, 128)
-        assert p.grid_x * p.grid_y >= 256          # at least one workgroup per CU
+        assert _lib.KERNEL_NAMES[p.kernel] == "gemv"
+        assert p.split_k == 1 and p.workspace_bytes == 0
         assert p.tile_n in (16, 32, 64, 256)
-        rows = -(-512 // p.split_k)
-        assert (p.split_k - 1) * rows < 512        # every split owns at least one row
-    assert _lib.plan(1, 4096, 4096, 128).split_k == 1
-    assert _lib.plan(1, 4096, 4096, 128).tile_cfg in (0, 1)
+        assert p.tile_cfg in (0, 1)
+        assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
+    for M, N, K in ((1, 1024, 14336), (8, 512, 8192), (2, 2048, 28672)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
+        assert p.workspace_bytes == 4 * M * N * 4
+        assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
+    assert _lib.plan(1, 28672, 14336, 128).split_k == 1   # enough column blocks
+    assert _lib.plan(1, 4096, 14336, 128).split_k == 1    # one block per CU
+    for split in (2, 3, 7, 600):
+        p = _lib.plan(2, 1024, 4096, 128, _lib.KERNEL_GEMV, split)
+        rows = -(-512 // p.split_k)
+        assert 1 < p.split_k <= 512
+        assert (p.split_k - 1) * rows < 512        # every split owns at least one row
+        assert p.workspace_bytes == p.split_k * 2 * 1024 * 4
     p1 = _lib.plan(1, 1024, 4096, 128, _lib.KERNEL_GEMV, 1)
     assert p1.split_k == 1 and p1.workspace_bytes == 0
 

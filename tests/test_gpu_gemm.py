@@ -173,8 +173,8 @@ def test_mfma_tile_configs(M, K, N, G):
 ])
 def test_mfma_split_k(M, K, N, G):
     """Prefill split-K (cfg 7 and 8): fp32 partials per k-split, summed in split
-    order by a second kernel; every split count, fused bias; then a GEMV split-K
-    call on the same cached workspace still sees zeroed counters."""
+    order by a second kernel; every split count, fused bias; then a forced GEMV
+    split-K call reuses the same cached workspace."""
     from w4a16 import w4a16_matmul
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
@@ -192,9 +192,11 @@ def test_mfma_split_k(M, K, N, G):
             outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
             assert torch.equal(outb, out + b)
     Xg, qg, sg, zg = _build_case(1, 4096, 1024, 128, seed=5)
-    assert plan_for(1, 1024, 4096, 128).split_k > 1
-    assert_gemm_close(w4a16_matmul(Xg, qg, sg, zg, 128), _ref(Xg, qg, sg, zg, 128),
+    pg = plan_for(1, 1024, 4096, 128, "gemv", 4)
+    assert pg.split_k == 4
+    assert_gemm_close(w4a16_matmul_planned(Xg, qg, sg, zg, 128, pg), _ref(Xg, qg, sg, zg, 128),
                       "GEMV split-K after prefill split-K")
+    assert plan_for(1, 1024, 4096, 128).split_k == 1
 
 
 @pytest.mark.parametrize("M,K,N,G", [
@@ -313,19 +315,42 @@ def test_kernel_rejects_bad_group_size():
         w4a16_matmul(X, qw, s, z, 8)
 
 
-def test_split_k_is_deterministic_and_workspace_stays_clean():
-    """Split-K GEMV sums partials in split order: two runs agree bit for bit, and
-    the counters it leaves in the workspace are zero (checked by reuse)."""
-    from w4a16 import w4a16_matmul
-    from w4a16.hip_kernel import plan_for
+def test_split_k_is_deterministic():
+    """Forced split-K GEMV sums fp32 partials in split order in a second kernel:
+    repeated runs agree bit for bit, whatever the workspace held before (the
+    partials are rewritten by every call, nothing needs to start zeroed)."""
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+    from w4a16 import _runtime
 
     M, K, N, G = 1, 4096, 1024, 128
-    assert plan_for(M, N, K, G).split_k > 1
+    p = plan_for(M, N, K, G, "gemv", 4)
+    assert p.split_k == 4 and p.workspace_bytes == 4 * M * N * 4
     X, qw, s, z = _build_case(M, K, N, G, seed=3)
-    outs = [w4a16_matmul(X, qw, s, z, G).clone() for _ in range(5)]
+    outs = []
+    for i in range(5):
+        ws = _runtime.workspace(X.device, p.workspace_bytes)
+        ws.fill_(0xFF if i % 2 else 0x5A)          # stale garbage between calls
+        outs.append(w4a16_matmul_planned(X, qw, s, z, G, p).clone())
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert_gemm_close(outs[0], _ref(X, qw, s, z, G), "split-K")
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 14336, 1024, 128), (8, 8192, 512, 64), (3, 8256, 260, 96)])
+def test_gemv_auto_split_long_k(M, K, N, G):
+    """Long K, few column blocks: the automatic decode plan splits K four ways
+    (fp32 partials, split-order reduction, fused bias)."""
+    from w4a16 import w4a16_matmul
+    from w4a16.hip_kernel import plan_for, w4a16_linear
+
+    p = plan_for(M, N, K, G)
+    assert p.split_k == 4 and p.workspace_bytes == 4 * M * N * 4
+    log(f"gemv auto split M={M} K={K} N={N} G={G}")
+    X, qw, s, z = _build_case(M, K, N, G, seed=K + N)
+    out = w4a16_matmul(X, qw, s, z, G)
+    assert_gemm_close(out, _ref(X, qw, s, z, G), f"gemv auto split-K M={M} K={K} N={N}")
+    b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
+    assert torch.equal(w4a16_linear(X, qw, s, z, b, G), out + b)
 
 
 def test_baselines_on_gpu():

@@ -71,15 +71,16 @@ int gemv_cols_auto(int64_t N, int cus) {
   return 16;
 }
 
+// GEMV k-split by shape (measured on MI355X, M = 1..8, fp32 partials plus the
+// split-order reduction kernel): with K >= 8192 and fewer column blocks than
+// CUs, four splits win 12-50 % (K = 14336, N = 1024: 11.7 -> 7.3 us;
+// K = 28672, N = 1024: 20.5 -> 10.0 us); at K = 4096 the extra pass costs more
+// than the extra workgroups recover (4.6 -> 5.4 us); at one block per CU it is
+// neutral to 3 % slower; 3 or 6 splits, whose row ranges cut quantisation
+// groups, lose to 4.
 int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
   const int64_t nblk = (N + cols - 1) / cols;
-  const int64_t KP = K / 8;
-  if (nblk <= 0 || KP <= 0 || nblk >= cus) return 1;
-  int64_t S = (cus + nblk - 1) / nblk;
-  const int64_t smax = KP / 16 > 1 ? KP / 16 : 1;   // keep >= 16 rows per workgroup
-  if (S > smax) S = smax;
-  if (S < 1) S = 1;
-  return (int)S;
+  return (K / 8 >= 1024 && nblk < cus) ? 4 : 1;
 }
 
 // Prefill tile configuration by shape (measured on MI355X, C4/C5 shapes):
@@ -110,8 +111,7 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
 }
 
 size_t mfma_workspace_bytes(int64_t M, int64_t N, int64_t K, int split) {
-  const size_t part = occ2_workspace_bytes((int)M, (int)N, (int)K, split);
-  return part ? kGemvCounterBytes + part : 0;   // partials after the GEMV counters
+  return occ2_workspace_bytes((int)M, (int)N, (int)K, split);
 }
 
 int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_t split,
@@ -145,7 +145,6 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
         const int64_t rows = (KP + S - 1) / S;
         S = (int)((KP + rows - 1) / rows);
       }
-      if ((N + cols - 1) / cols > kGemvMaxCounterBlocks) S = 1;
       p->split_k = S;
       p->tile_cfg = kGemvDefaultConfig;
       p->tile_m = 0;
@@ -215,7 +214,6 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;
-      if (p->split_k > 1 && nblk > kGemvMaxCounterBlocks) return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8))
         return W4A16_ERR_BAD_PLAN;
       const size_t need = gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
@@ -234,7 +232,7 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
       const size_t need = mfma_workspace_bytes(M, N, K, p->split_k);
       if (need > 0) {
         if (!ws || ws_bytes < need || !aligned(ws, 256)) return W4A16_ERR_WORKSPACE;
-        part = reinterpret_cast<float*>(static_cast<char*>(ws) + kGemvCounterBytes);
+        part = static_cast<float*>(ws);
       }
       return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }

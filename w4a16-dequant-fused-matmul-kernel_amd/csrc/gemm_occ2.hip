@@ -308,10 +308,7 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
                      nsplit > 1 ? kts : KT);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
-  const size_t nq = (size_t)a.M * (size_t)(a.N / 4);
-  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, part,
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, nsplit);
-  return hipGetLastError();
+  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, nsplit, st);
 }
 
 }  // namespace
@@ -319,6 +316,14 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
 bool occ2_gemm_applicable(int M, int N, int K, int G) {
   (void)M;
   return K % kBK == 0 && N % 4 == 0 && G % 32 == 0 && K % G == 0;
+}
+
+hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int S,
+                                hipStream_t st) {
+  const size_t nq = (size_t)M * (size_t)(N / 4);
+  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, part,
+                     static_cast<const f16*>(bias), static_cast<f16*>(y), M, N, S);
+  return hipGetLastError();
 }
 
 int occ2_splits(int K, int split) {
@@ -334,7 +339,7 @@ size_t occ2_workspace_bytes(int M, int N, int K, int split) {
 }
 
 // waves 1 x 4: 128 x 256 tiles; waves 2 x 2: 256 x 128 tiles.  split > 1:
-// fp32 partials in `part` (occ2_workspace_bytes), then one reduction kernel.
+// fp32 partials in `part` (occ2_workspace_bytes), then launch_splitk_reduce.
 hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
                             hipStream_t st) {
   if (!occ2_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;

@@ -26,9 +26,10 @@
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
 //     so that neighbouring row segments share that XCD's L2 lines;
-//   * optional split-K (only when N is too narrow to fill the device): each
-//     workgroup writes fp32 partials; the last workgroup of a column block (atomic
-//     counter) sums the splits in split order and resets the counter.
+//   * optional split-K (forced through a plan; the automatic plan does not split:
+//     at decode sizes the extra pass costs more than the parallelism gains):
+//     each workgroup writes fp32 partials and a second kernel sums the splits
+//     in split order (deterministic).
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -49,8 +50,7 @@ template <int MT, int CWL, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
-    float* __restrict__ part, uint32_t* __restrict__ cnt, int N, int K, int G, int rows_per_wg,
-    int S, int nblk) {
+    float* __restrict__ part, int N, int K, int G, int rows_per_wg, int S, int nblk) {
   constexpr int kThreads = GemvShape<WAVES>::kThreads;
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
@@ -63,7 +63,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
   __shared__ uint4 xs[XD ? 1 : MT * CHUNK];
   __shared__ float red[CWL <= 16 ? WAVES * 4 : WAVES][MT][CW];
-  __shared__ int s_last;
 
   // XCD-aware block order (see header comment).
   const int nb = (int)gridDim.x;
@@ -272,28 +271,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     return;
   }
 
+  // split-K: fp32 partials [split][M][N]; a second kernel sums the splits
   if (cv) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) part[((size_t)sk * MT + m) * N + col] = v[m];
   }
-  __threadfence();
-  __syncthreads();
-  if (t == 0) s_last = (atomicAdd(&cnt[cb], 1u) == (uint32_t)(S - 1)) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (cv) {
-    const f16 b = bias ? bias[col] : (f16)0.0f;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      float s = 0.0f;
-      for (int q = 0; q < S; ++q) s += part[((size_t)q * MT + m) * N + col];
-      f16 y = f32_to_f16(s);
-      if (bias) y = y + b;
-      Y[(size_t)m * N + col] = y;
-    }
-  }
-  if (t == 0) cnt[cb] = 0u;
 }
 
 template <int MT, int CWL, int WAVES>
@@ -301,18 +283,15 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;
   const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
-  uint32_t* cnt = nullptr;
-  float* part = nullptr;
-  if (split > 1) {
-    cnt = static_cast<uint32_t*>(ws);
-    part = reinterpret_cast<float*>(static_cast<char*>(ws) + kGemvCounterBytes);
-  }
+  float* part = split > 1 ? static_cast<float*>(ws) : nullptr;
   hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES>), dim3(nblk * split),
                      dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), part, cnt, a.N, a.K, a.G, rows, split, nblk);
-  return hipGetLastError();
+                     static_cast<f16*>(a.y), part, a.N, a.K, a.G, rows, split, nblk);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || split == 1) return e;
+  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, split, st);
 }
 
 template <int MT, int WAVES>
@@ -355,7 +334,7 @@ int gemv_rows_per_split(int K, int split) {
 size_t gemv_workspace_bytes(int M, int N, int K, int split) {
   (void)K;
   if (split <= 1) return 0;
-  return kGemvCounterBytes + (size_t)split * (size_t)M * (size_t)N * sizeof(float);
+  return (size_t)split * (size_t)M * (size_t)N * sizeof(float);
 }
 
 hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {

@@ -22,16 +22,12 @@ struct GemmArgs {
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
 // consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
 // picks 4 (cfg 0), 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup; with
-// split > 1, `ws` holds the counters + fp32 partials of gemv_workspace_bytes().
+// split > 1, `ws` holds the fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
 constexpr int kGemvConfigs = 3;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
 // other's outstanding loads (measured faster on MI355X for M = 1 decode shapes).
 constexpr int kGemvDefaultConfig = 1;
-// Split-K counters live in a fixed-size region at the start of the workspace so
-// that no call's fp32 partials ever overlap another call's counters.
-constexpr int kGemvMaxCounterBlocks = 16384;
-constexpr size_t kGemvCounterBytes = (size_t)kGemvMaxCounterBlocks * 4;
 bool gemv_cols_valid(int cols);
 bool gemv_cfg_valid(int cfg, int M);
 size_t gemv_workspace_bytes(int M, int N, int K, int split);
@@ -53,6 +49,11 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipSt
 // The 256 x 256 LDS-staged-weight kernel (mfma cfg 4): needs K % 64 == 0.
 bool lds_gemm_applicable(int M, int N, int K, int G);
 hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
+// Split-K epilogue shared by the GEMV and the prefill kernels: y[M, N] =
+// fp16(sum of the S fp32 partials [S][M][N], in split order) (+ fp16 bias).
+// N % 4 == 0.
+hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int S,
+                                hipStream_t st);
 // Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256, cfg 8: 256 x 128):
 // needs K % 64 == 0.
 bool occ2_gemm_applicable(int M, int N, int K, int G);

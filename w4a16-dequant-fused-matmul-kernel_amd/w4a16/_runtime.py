@@ -45,13 +45,12 @@ def on_device(device: torch.device):
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """A zero-initialised workspace of at least `nbytes` for the current stream.
+    """A workspace of at least `nbytes` for the current stream.
 
-    The GEMV split-K path keeps per-column-block counters at its start and leaves
-    them zeroed after every call; split-K partial sums (GEMV and prefill) go
-    after that region and are rewritten by every call.  So one buffer serves
-    every later call on the same stream.  Calls on one stream are ordered, so
-    sharing is safe; each stream has its own buffer.
+    It holds split-K fp32 partial sums (forced GEMV splits, prefill splits),
+    which every call rewrites before reading, so its contents never matter and
+    one buffer serves every later call on the same stream.  Calls on one stream
+    are ordered, so sharing is safe; each stream has its own buffer.
     """
     if nbytes <= 0:
         return None
@@ -61,7 +60,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
         ws = _WORKSPACES.get(key)
         if ws is None or ws.numel() < nbytes:
             size = max(nbytes, 1 << 20)
-            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
             _WORKSPACES[key] = ws
         return ws
 
