@@ -195,12 +195,15 @@ def test_planner_prefill_split_k():
 
     # C5 down-projection at M = 256: 64 tiles of 128 x 256 -> split along K
     p = _lib.plan(256, 8192, 28672, 128)
-    assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 7
+    assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 11
     assert p.split_k > 1 and p.grid_x >= 256
     assert p.workspace_bytes >= p.split_k * 256 * 8192 * 4
     # large M: no split, no workspace
     p = _lib.plan(4096, 14336, 4096, 128)
-    assert p.split_k == 1 and p.workspace_bytes == 0 and p.tile_cfg == 7
+    assert p.split_k == 1 and p.workspace_bytes == 0 and p.tile_cfg == 11
+    # K % 256 != 0: the register-staged kernel of the same tiles
+    p = _lib.plan(4096, 14336, 4160, 64)
+    assert p.split_k == 1 and p.tile_cfg == 7
     # a forced split on a tile configuration without split-K support is refused
     q = _lib.plan(256, 8192, 28672, 128, _lib.KERNEL_MFMA, 4)
     q.tile_cfg = 6

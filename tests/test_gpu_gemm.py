@@ -143,20 +143,22 @@ def test_gemv_splits(M, K, N, G):
 @pytest.mark.parametrize("M,K,N,G", [
     (9, 96, 260, 32), (33, 160, 516, 32), (127, 4096, 1028, 128), (129, 4096, 516, 64),
     (200, 1024, 1540, 32), (64, 4096, 4096, 128), (1, 64, 128, 32), (16, 11008, 4096, 64),
-    (600, 1024, 2048, 64), (520, 2112, 772, 96),
+    (600, 1024, 2048, 64), (520, 2112, 772, 96), (260, 768, 1028, 96),
 ])
 def test_mfma_tile_configs(M, K, N, G):
     """Prefill MFMA kernels with every tile configuration over tails in M, N, K
     (configs 4, 9, 10 -- weight tile dequantised into LDS -- and 7, 8 -- two
     waves per SIMD with 16x16x32 MFMAs -- where K % 64 == 0; configs 5 and 6,
-    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0)."""
+    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; config 11,
+    activations and weights streamed into LDS, where K % 256 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 3 + N)
     ref = _ref(X, qw, s, z, G)
-    for cfg in range(11):
-        if (cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128):
+    for cfg in range(_lib.MFMA_CONFIGS):
+        if ((cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128)
+                or (cfg == 11 and K % 256)):
             continue
         p = plan_for(M, N, K, G, "mfma", 1)
         p.tile_cfg = cfg
@@ -172,16 +174,16 @@ def test_mfma_tile_configs(M, K, N, G):
     (65, 4096, 1028, 128), (200, 2048, 516, 32), (256, 11008, 772, 64), (130, 2112, 260, 96),
 ])
 def test_mfma_split_k(M, K, N, G):
-    """Prefill split-K (cfg 7 and 8): fp32 partials per k-split, summed in split
-    order by a second kernel; every split count, fused bias; then a forced GEMV
-    split-K call reuses the same cached workspace."""
+    """Prefill split-K (cfg 7, 8 and, where K % 256 == 0, 11): fp32 partials per
+    k-split, summed in split order by a second kernel; every split count, fused
+    bias; then a forced GEMV split-K call reuses the same cached workspace."""
     from w4a16 import w4a16_matmul
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M + N + K)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in (7, 8):
+    for cfg in (7, 8, 11) if K % 256 == 0 else (7, 8):
         for split in (2, 3, 5, K // 64):
             p = plan_for(M, N, K, G, "mfma", split)
             p.tile_cfg = cfg
@@ -351,6 +353,35 @@ def test_gemv_auto_split_long_k(M, K, N, G):
     assert_gemm_close(out, _ref(X, qw, s, z, G), f"gemv auto split-K M={M} K={K} N={N}")
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
     assert torch.equal(w4a16_linear(X, qw, s, z, b, G), out + b)
+
+
+def test_streamed_prefill_far_apart_scales_zeros():
+    """The streamed prefill kernel (cfg 11) reads scales and zeros through one
+    buffer resource based at the lower of the two; placed more than 2 GiB
+    apart they take the register kernel of the same tiles instead.  Both give
+    results within the oracle's tolerance."""
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+
+    M, K, N, G = 256, 1024, 1028, 64
+    X, qw, s, z = _build_case(M, K, N, G, seed=11)
+    ref = _ref(X, qw, s, z, G)
+    p = plan_for(M, N, K, G, "mfma", 1)
+    p.tile_cfg = 11
+    assert_gemm_close(w4a16_matmul_planned(X, qw, s, z, G, p), ref, "cfg 11 adjacent")
+    # 2 MiB buffers come from the caching allocator's large pool, one segment
+    # each, so the 3 GiB block between them separates them
+    sbuf = torch.empty(1 << 20, dtype=torch.float16, device=DEV)
+    gap = torch.empty(3 << 30, dtype=torch.uint8, device=DEV)
+    zbuf = torch.empty(1 << 20, dtype=torch.float16, device=DEV)
+    s_far = sbuf[: s.numel()].view(s.shape).copy_(s)
+    z_far = zbuf[: z.numel()].view(z.shape).copy_(z)
+    dist = abs(z_far.data_ptr() - s_far.data_ptr())
+    log(f"scales/zeros {dist / 2**30:.2f} GiB apart")
+    out = w4a16_matmul_planned(X, qw, s_far, z_far, G, p)
+    assert_gemm_close(out, ref, "cfg 11 scales/zeros far apart")
+    del gap
+    if dist < (1 << 31):
+        pytest.skip("allocator placed the copies within 2 GiB; fallback not exercised")
 
 
 def test_baselines_on_gpu():

@@ -84,11 +84,13 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
 }
 
 // Prefill tile configuration by shape (measured on MI355X, C4/C5 shapes):
-//   * M >= 1024: the two-waves-per-SIMD 16x16x32 kernel, 128 x 256 (cfg 7);
-//   * enough 128 x 256 tiles for half the CUs: two-waves-per-SIMD 32x32x16,
-//     128 x 256 (cfg 6);
-//   * fewer tiles (short M, narrow N): cfg 7 split along K so that the tiles
-//     times the splits give every CU a workgroup (fp32 partials + one
+//   * the 128 x 256 two-waves-per-SIMD 16x16x32 kernel with activations and
+//     weights streamed into LDS (cfg 11, K % 256 == 0) wherever the tiles fill
+//     half the CUs or M >= 1024: 5-8 % faster than cfg 7 at C4 M = 4096,
+//     15-20 % at M = 512 and at C5 M = 256; without K % 256 == 0, cfg 7 for
+//     M >= 1024 and the 32x32x16 two-waves kernel (cfg 6) for the rest;
+//   * fewer tiles (short M, narrow N): cfg 11 (or cfg 7) split along K so that
+//     the tiles times the splits give every CU a workgroup (fp32 partials + one
 //     reduction kernel), when K allows at least 8 k-steps per split; else
 //     narrow 32 x 512 tiles (cfg 2) or the one-wave 128 x 256 (cfg 1).
 struct MfmaChoice {
@@ -96,14 +98,20 @@ struct MfmaChoice {
 };
 MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) return {2, 1};
+  const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
+  const bool c7 = mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G);
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
-  if (M >= 1024 && mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) return {7, 1};
-  if (2 * t6 >= cus && mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return {6, 1};
-  if (mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G)) {
+  if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
+  if (2 * t6 >= cus) {
+    if (c11) return {11, 1};
+    if (mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return {6, 1};
+  }
+  if (c11 || c7) {
     const int64_t kt = K / 64;
     int64_t s = (cus + t6 - 1) / t6;
     if (s > kt / 8) s = kt / 8;
-    if (s >= 2) return {7, occ2_splits((int)K, (int)s)};
+    if (s >= 2) return c11 ? MfmaChoice{11, stream_splits((int)K, (int)s)}
+                           : MfmaChoice{7, occ2_splits((int)K, (int)s)};
   }
   const int64_t t2 = ((N + 511) / 512) * ((M + 31) / 32);
   if (2 * t6 < cus && t2 > t6) return {2, 1};
@@ -157,10 +165,11 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G)) return W4A16_ERR_BAD_PLAN;
       MfmaChoice c = mfma_choice(M, N, K, G, cus);
-      if (split > 0) {   // a forced split runs on cfg 7
-        c.cfg = split > 1 ? 7 : c.cfg;
-        c.split = split > 1 ? occ2_splits((int)K, split) : 1;
-        if (c.split > 1 && !mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G))
+      if (split > 0) {   // a forced split runs on cfg 11 (cfg 7 where K % 256 != 0)
+        const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
+        c.cfg = split > 1 ? (c11 ? 11 : 7) : c.cfg;
+        c.split = split > 1 ? (c11 ? stream_splits((int)K, split) : occ2_splits((int)K, split)) : 1;
+        if (c.split > 1 && !mfma_cfg_applicable(c.cfg, (int)M, (int)N, (int)K, (int)G))
           return W4A16_ERR_BAD_PLAN;
       }
       const MfmaTile t = mfma_tile(c.cfg);
@@ -223,7 +232,7 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G) || !fits(M, N, K, G) ||
           !mfma_cfg_applicable(p->tile_cfg, (int)M, (int)N, (int)K, (int)G) || p->split_k < 1 ||
-          (p->split_k > 1 && p->tile_cfg != 7 && p->tile_cfg != 8))
+          (p->split_k > 1 && !mfma_cfg_splits(p->tile_cfg)))
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
           !aligned(y, 8) || (bias && !aligned(bias, 8)))

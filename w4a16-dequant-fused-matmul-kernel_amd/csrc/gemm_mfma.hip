@@ -528,6 +528,8 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 // cfg 8: 256 x 128, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
 // cfg 9: 256 x 224, 8 waves sharing an LDS-dequantised weight tile (gemm_ldsb.hip)
 // cfg 10: 256 x 256, as cfg 9
+// cfg 11: 128 x 256 as cfg 7, packed weights streamed into LDS four k-steps
+//         ahead (gemm_stream.hip)
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
     case 0: return {128, 512};
@@ -540,9 +542,12 @@ MfmaTile mfma_tile(int cfg) {
     case 8: return {256, 128};
     case 9: return {256, 224};
     case 10: return {256, 256};
+    case 11: return {128, 256};
     default: return {64, 512};
   }
 }
+
+bool mfma_cfg_splits(int cfg) { return cfg == 7 || cfg == 8 || cfg == 11; }
 
 bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
   if (cfg < 0 || cfg >= kMfmaConfigs) return false;
@@ -550,6 +555,7 @@ bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
   if (cfg == 5 || cfg == 6) return K % (2 * kBK) == 0;
   if (cfg == 7 || cfg == 8) return occ2_gemm_applicable(M, N, K, G);
   if (cfg == 9 || cfg == 10) return ldsb_gemm_applicable(M, N, K, G);
+  if (cfg == 11) return stream_gemm_applicable(M, N, K, G);
   return true;
 }
 
@@ -562,7 +568,7 @@ bool operands_fit(int M, int N, int K, int G) {
 bool mfma_fits(int M, int N, int K, int G) { return operands_fit(M, N, K, G); }
 
 hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st) {
-  if (split > 1 && cfg != 7 && cfg != 8) return hipErrorInvalidValue;
+  if (split > 1 && !mfma_cfg_splits(cfg)) return hipErrorInvalidValue;
   switch (cfg) {
     case 0: return launch_cfg<4, 1, 4>(a, st);
     case 1: return launch_cfg<2, 2, 2>(a, st);
@@ -581,6 +587,7 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipSt
     case 8: return launch_occ2_gemm(a, true, split, part, st);
     case 9: return launch_ldsb_gemm(a, false, st);
     case 10: return launch_ldsb_gemm(a, true, st);
+    case 11: return launch_stream_gemm(a, split, part, st);
     default: return hipErrorInvalidValue;
   }
 }
