@@ -190,6 +190,23 @@ def test_planner_gemv_split_rule():
     assert p1.split_k == 1 and p1.workspace_bytes == 0
 
 
+def test_planner_small_batch_wide_weights_stream():
+    """9 <= M <= 64 on wide or long weights takes the streamed prefill kernel
+    split along K (about 448 workgroups, >= 8 k-steps per split); narrow N or
+    small weights stay on the skinny kernel."""
+    from w4a16 import _lib
+
+    for M, N, K, s in ((16, 28672, 4096, 4), (32, 28672, 4096, 4), (16, 8192, 28672, 14),
+                       (64, 28672, 8192, 4), (48, 14336, 4096, 8)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 11, (M, N, K)
+        assert p.split_k == s and p.workspace_bytes >= s * M * N * 4
+        assert p.grid_x == s * ((N + 255) // 256)
+    for M, N, K in ((16, 4096, 4096), (32, 4096, 14336), (64, 4096, 4096), (16, 6144, 4096),
+                    (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
+        assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
+
+
 def test_planner_prefill_split_k():
     from w4a16 import _lib
 

@@ -368,20 +368,17 @@ def test_streamed_prefill_far_apart_scales_zeros():
     p = plan_for(M, N, K, G, "mfma", 1)
     p.tile_cfg = 11
     assert_gemm_close(w4a16_matmul_planned(X, qw, s, z, G, p), ref, "cfg 11 adjacent")
-    # 2 MiB buffers come from the caching allocator's large pool, one segment
-    # each, so the 3 GiB block between them separates them
-    sbuf = torch.empty(1 << 20, dtype=torch.float16, device=DEV)
-    gap = torch.empty(3 << 30, dtype=torch.uint8, device=DEV)
-    zbuf = torch.empty(1 << 20, dtype=torch.float16, device=DEV)
-    s_far = sbuf[: s.numel()].view(s.shape).copy_(s)
-    z_far = zbuf[: z.numel()].view(z.shape).copy_(z)
+    # scales at the start and zeros at the end of one 2.5 GiB allocation
+    big = torch.empty(5 << 29, dtype=torch.uint8, device=DEV)
+    nb = s.numel() * 2
+    s_far = big[:nb].view(torch.float16).view(s.shape).copy_(s)
+    z_far = big[big.numel() - nb:].view(torch.float16).view(z.shape).copy_(z)
     dist = abs(z_far.data_ptr() - s_far.data_ptr())
     log(f"scales/zeros {dist / 2**30:.2f} GiB apart")
+    assert dist >= (1 << 31)
     out = w4a16_matmul_planned(X, qw, s_far, z_far, G, p)
     assert_gemm_close(out, ref, "cfg 11 scales/zeros far apart")
-    del gap
-    if dist < (1 << 31):
-        pytest.skip("allocator placed the copies within 2 GiB; fallback not exercised")
+    del big
 
 
 def test_baselines_on_gpu():

@@ -96,8 +96,39 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
 struct MfmaChoice {
   int cfg, split;
 };
+
+// Small batches (9 <= M <= 64) on wide or long weights: the streamed prefill
+// kernel split along K beats the skinny kernel once the weights are large
+// enough (measured on MI355X: M = 32, K = 4096, N = 28672: 37.8 vs 67.2 us;
+// M = 16, K = 8192, N = 28672: 58 vs 79-95 us; M = 48, K = 4096, N = 14336:
+// 26.8 vs 53.8 us; M = 64, K = 8192, N = 28672: 66 vs 241 us).  It loses
+// below ~32 column tiles (N < 8192: too little work per split; M = 32, K =
+// 14336, N = 4096: 40.6 vs 35.2 us) and on small weights, where its fixed
+// cost (~15 us) dominates; the skinny kernel's cost grows with M, so the size
+// threshold falls with M.
+bool skinny_takes_stream(int64_t M, int64_t N, int64_t K, int64_t G) {
+  if (M <= kGemvMaxM || M > kSkinnyMaxM || N < 8192) return false;
+  if (!mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G)) return false;
+  const int64_t wbytes = K / 2 * N;
+  const int64_t need = M <= 16 ? (48ll << 20) : M <= 32 ? (16ll << 20) : (8ll << 20);
+  return wbytes >= need;
+}
+
+// k-splits for the streamed kernel on few tiles: about 448 workgroups (two
+// per CU at most), at least 8 k-steps per split.
+int stream_split_for(int64_t tiles, int64_t K) {
+  const int64_t kt = K / 64;
+  int64_t s = (448 + tiles - 1) / tiles;
+  if (s > kt / 8) s = kt / 8;
+  return s < 1 ? 1 : (int)s;
+}
+
 MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  if (M <= 64) return {2, 1};
+  if (M <= 64) {
+    if (!skinny_takes_stream(M, N, K, G)) return {2, 1};
+    const int s = stream_split_for((N + 255) / 256 * ((M + 127) / 128), K);
+    return {11, s > 1 ? stream_splits((int)K, s) : 1};
+  }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
   const bool c7 = mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G);
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
@@ -132,7 +163,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       kernel = W4A16_KERNEL_SIMT;
     else if (gemv_applicable(M, N, G))
       kernel = W4A16_KERNEL_GEMV;
-    else if (M <= kSkinnyMaxM && skinny_applicable(M, G))
+    else if (M <= kSkinnyMaxM && skinny_applicable(M, G) && !skinny_takes_stream(M, N, K, G))
       kernel = W4A16_KERNEL_SKINNY;
     else if (mfma_applicable(N, G))
       kernel = W4A16_KERNEL_MFMA;

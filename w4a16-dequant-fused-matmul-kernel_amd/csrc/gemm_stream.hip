@@ -257,9 +257,8 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
     }
   };
 
-  // An AGPR operand anywhere in the kernel lets the compiler select the AGPR
-  // form of the MFMAs: the 128 accumulators then live in AGPRs, each MFMA
-  // updating its own in place, and the VGPRs keep the pipeline's operands.
+  // 128 accumulators in VGPRs (the AGPR form of the MFMAs made the compiler
+  // shuttle accumulators between the two register files and spill).
   f32x4 acc[kMT][kNTiles];
 #pragma unroll
   for (int i = 0; i < kMT; ++i)
