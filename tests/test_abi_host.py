@@ -137,7 +137,11 @@ def test_quant_entry_points_reject_bad_args(lib):
 
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
-    (8, 28672, 4096, 128, "gemv"),
+    (4, 28672, 4096, 128, "gemv"),   # wide N: the GEMV up to M = 4
+    (2, 6144, 4096, 128, "gemv"),
+    (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
+    (8, 4096, 4096, 128, "skinny"),
+    (5, 28672, 4096, 128, "skinny"),  # wide N from M = 5
     (9, 4096, 4096, 128, "skinny"),
     (64, 4096, 11008, 64, "skinny"),
     (65, 4096, 4096, 128, "mfma"),
@@ -160,8 +164,8 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
 def test_planner_gemv_split_rule():
     """The automatic decode plan splits K four ways only for long K (>= 8192) with
     fewer 16-column blocks than CUs (measured faster there, slower at K = 4096
-    and neutral at one block per CU); a forced split gives every split at least one packed row and
-    sizes the fp32 partials."""
+    and neutral at one block per CU); a forced split gives every split at least
+    one packed row and sizes the fp32 partials."""
     from w4a16 import _lib
 
     lib = _lib.load()
@@ -173,7 +177,7 @@ def test_planner_gemv_split_rule():
         assert p.tile_cfg in (0, 1)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
-    for M, N, K in ((1, 1024, 14336), (8, 512, 8192), (2, 2048, 28672)):
+    for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 2048, 28672)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
         assert p.workspace_bytes == 4 * M * N * 4

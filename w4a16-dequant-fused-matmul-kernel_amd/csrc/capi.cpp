@@ -97,6 +97,18 @@ struct MfmaChoice {
   int cfg, split;
 };
 
+// Decode batches 3 <= M <= 8: the MFMA skinny kernel does the M dot products
+// per dequantised pair on the matrix cores where the GEMV spends M v_dot2 on
+// each; measured on MI355X it wins from M = 3 up to N = 16384 (M = 8,
+// K = N = 4096: 7.7 vs 12.1 us; M = 3, K = 14336, N = 4096: 17.2 vs 20.8 us;
+// M = 4, K = 4096, N = 6144: 9.7 vs 11.5 us) and from M = 5 on wider weights
+// (M = 5, K = 4096, N = 28672: 29.7 vs 32.6 us), while at M <= 2, and at M <= 4
+// on N = 28672, the GEMV is faster (M = 4, K = 8192, N = 28672: 47 vs 75 us).
+bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G) {
+  (void)K;
+  return M >= 3 && M <= kGemvMaxM && skinny_applicable(M, G) && (N <= 16384 || M >= 5);
+}
+
 // Small batches (9 <= M <= 64) on wide or long weights: the streamed prefill
 // kernel split along K beats the skinny kernel once the weights are large
 // enough (measured on MI355X: M = 32, K = 4096, N = 28672: 37.8 vs 67.2 us;
@@ -161,7 +173,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
-    else if (gemv_applicable(M, N, G))
+    else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G))
       kernel = W4A16_KERNEL_GEMV;
     else if (M <= kSkinnyMaxM && skinny_applicable(M, G) && !skinny_takes_stream(M, N, K, G))
       kernel = W4A16_KERNEL_SKINNY;
@@ -219,8 +231,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->tile_n = 16;
       p->grid_x = (N + 15) / 16;
       p->grid_y = 1;
-      // 8 waves per workgroup when the column blocks give about one per CU
-      p->tile_cfg = (M <= 32 && p->grid_x <= cus) ? 1 : 0;
+      // 8 waves per workgroup up to one column block per CU, for M <= 16 up
+      // to two (measured at M = 4 / 8, N = 6144: 9.7 / 10.8 vs 10.9 / 11.4
+      // us; at M = 32, N = 6144 the 4-wave form is faster, 20.9 vs 23.4 us)
+      p->tile_cfg = (M <= 32 && (p->grid_x <= cus || (M <= 16 && p->grid_x <= 2 * cus))) ? 1 : 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
