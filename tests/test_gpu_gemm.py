@@ -381,6 +381,42 @@ def test_streamed_prefill_far_apart_scales_zeros():
     del big
 
 
+def test_graph_capture_replays():
+    """Every kernel family captured once in a HIP graph and replayed several
+    times, with eager work in between: each replay equals the eager result bit
+    for bit (the library issues kernel launches only -- no memset -- and every
+    path, split-K included, is deterministic)."""
+    from w4a16 import w4a16_matmul
+    from w4a16.hip_kernel import plan_for
+
+    cases = [(1, 4096, 4096, 128), (1, 14336, 1024, 128), (4, 4096, 4096, 128),
+             (1024, 4096, 4096, 128), (256, 8192, 2048, 64), (32, 4096, 28672, 128),
+             (100, 2112, 520, 96)]
+    for M, K, N, G in cases:
+        p = plan_for(M, N, K, G)
+        log(f"graph M={M} K={K} N={N} G={G} kernel={p.as_dict()['kernel_name']} "
+            f"cfg={p.tile_cfg} split={p.split_k}")
+        X, qw, s, z = _build_case(M, K, N, G, seed=M + K + N)
+        eager = w4a16_matmul(X, qw, s, z, G)
+        out = torch.empty_like(eager)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            w4a16_matmul(X, qw, s, z, G, out=out)     # warm-up: workspace, plan
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            w4a16_matmul(X, qw, s, z, G, out=out)
+        for i in range(3):
+            out.fill_(float("nan"))
+            w4a16_matmul(X * 2, qw, s, z, G)           # eager work between replays
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {i} M={M} K={K} N={N}"
+    assert plan_for(1, 1024, 14336, 128).split_k > 1
+    assert plan_for(32, 28672, 4096, 128).split_k > 1
+
+
 def test_baselines_on_gpu():
     """reference_w4a16 / dequant_then_matmul / fp16_matmul (reference.py:18-67) on the GPU."""
     from w4a16 import dequant_then_matmul, dequantize_weight, fp16_matmul, reference_w4a16
