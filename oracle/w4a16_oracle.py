@@ -26,9 +26,23 @@ Arithmetic contract (what the reference computes when torch runs it on the CPU):
   ``round`` (so a zero-point can be stored as fp16 ``0x8000``), and ``q`` uses the
   fp32 scale, not the fp16-rounded one.
 * group min: when the minimum of a group is a zero and the group holds both
-  ``+0.0`` and ``-0.0``, the zero that comes LAST in k order is the minimum.  This
-  is what torch's vectorised CPU column reduction returns; torch does not document
-  it, so this one corner is a defined convention of this oracle.
+  ``+0.0`` and ``-0.0``, which zero ``amin(dim=1)`` returns depends on the layout
+  of torch's CPU reduction.  N >= 2 (strided rows): the columns in whole blocks
+  of 32 (``n < 32 * (N // 32)``, the vectorised outer reduction, whose
+  ``minimum`` keeps the newer operand on a tie) take the zero that comes LAST in
+  k order, the ``N % 32`` tail columns (its scalar loop, which replaces the
+  running minimum only on ``<``) the FIRST.  N == 1 (contiguous groups): G < 32
+  takes the first zero; G >= 32 follows the vectorised inner reduction (4
+  accumulators x 8 lanes over the first ``32 * (G // 32)`` values, then the
+  scalar tail; ``_inner_zero_min``).  torch does not document any of this; the
+  tests pin it against ``torch.amin`` itself on the CPU (every N up to 70, N = 1
+  for G up to 4096, 4096 x 4100 weights, 1 and 8 threads; identical under its
+  DEFAULT, AVX2 and AVX512 code paths).  Only the sign bit of that group's
+  zero-point depends on it (scale, codes and the dequantised weights do not).
+  **Parity unpinned**: a single group of a single column (``N == 1`` and
+  ``G == K``) with ``K > 32768``, where torch splits the one reduction across its
+  threads and the answer depends on the thread count; the oracle gives the
+  single-thread answer.
 * non-finite weights make the reference's ``pack_int4`` range assertion fire
   (NaN codes cast to int32 fall outside [0, 15]); the oracle raises
   ``AssertionError`` up front for any non-finite weight.
@@ -42,8 +56,10 @@ Arithmetic contract (what the reference computes when torch runs it on the CPU):
 
 Parity pins (each checked by a test under ``tests/``): the spec's packing word
 ``0xC2714F08`` and quantisation example, the reference tests' nibble-position and
-extreme-value cases, hand-derived tie / ``-0.0`` / fp32-scale cases, closed forms
-for dequant, and float64 brute force for the GEMM on small shapes.
+extreme-value cases, hand-derived tie / ``-0.0`` / fp32-scale cases, the fp32
+primitives and the group minimum against torch's own CPU routines (``/ 15``,
+``round``, ``clamp``, ``amin``), closed forms for dequant, and float64 brute
+force for the GEMM on small shapes.
 """
 from __future__ import annotations
 
@@ -114,15 +130,39 @@ def _clamp_keep_neg_zero(x: np.ndarray, lo: float, hi: float) -> np.ndarray:
     return np.where(x > np.float32(hi), np.float32(hi), x).astype(np.float32)
 
 
-def _group_min_last_zero(Wg: np.ndarray) -> np.ndarray:
-    """Minimum over axis 1 of [ng, G, N]; a zero minimum takes the sign of the
-    last zero in k order (see module docstring)."""
+def _inner_zero_min(col: np.ndarray) -> np.float32:
+    """N == 1, G >= 32: the zero torch's vectorised inner reduction returns for a
+    contiguous group whose minimum is a zero.  Positions p < 32 * (G // 32) sit in
+    lane p % 8 of accumulator (p // 8) % 4 (a tie keeps the later value); the
+    accumulators fold 0..3 in turn (a tie keeps the later one) and the lanes
+    toward lane 0 (a tie keeps the lower lane); the G % 32 tail is then scanned
+    (a tie keeps the running minimum).  So: lowest lane, then highest
+    accumulator, then latest position; a tail zero only without a zero before
+    the tail, and then the first."""
+    G = col.size
+    zs = np.nonzero(col == 0)[0]
+    head = zs[zs < 32 * (G // 32)]
+    if head.size == 0:
+        return col[zs[0]]
+    slot = head % 32
+    best = min(zip((slot % 8).tolist(), (-(slot // 8)).tolist(), (-head).tolist(), head.tolist()))
+    return col[best[3]]
+
+
+def _group_min(Wg: np.ndarray) -> np.ndarray:
+    """torch's CPU ``amin(dim=1)`` of [ng, G, N] float32 (quant.py:127), including
+    which zero a group holding both zero signs returns (see module docstring)."""
     gmin = Wg.min(axis=1)
+    G, N = Wg.shape[1], Wg.shape[2]
+    n_block = 32 * (N // 32)
     zg, zn = np.nonzero(gmin == 0)
     for g, n in zip(zg.tolist(), zn.tolist()):
         col = Wg[g, :, n]
-        last = np.nonzero(col == 0)[0][-1]
-        gmin[g, n] = col[last]
+        if N == 1 and G >= 32:
+            gmin[g, n] = _inner_zero_min(col)
+            continue
+        zeros_at = np.nonzero(col == 0)[0]
+        gmin[g, n] = col[zeros_at[-1] if n < n_block else zeros_at[0]]
     return gmin
 
 
@@ -146,8 +186,8 @@ def quantize_weight(W: np.ndarray, group_size: int = 128):
     Wf = W.astype(np.float32)
     assert np.isfinite(Wf).all(), "uint4 values must be in [0,15] (non-finite weight)"
     Wg = Wf.reshape(ng, G, N)
-    gmax = Wg.max(axis=1)
-    gmin = _group_min_last_zero(Wg)
+    gmax = Wg.max(axis=1)                                               # :126
+    gmin = _group_min(Wg)                                               # :127
     scale = ((gmax - gmin) / np.float32(_QMAX)).astype(np.float32)      # :129
     scale = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)  # :132
     zero = _clamp_keep_neg_zero(np.rint(-gmin / scale), 0, _QMAX)           # :134

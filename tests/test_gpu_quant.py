@@ -90,6 +90,37 @@ def test_quantize_special_values():
     _assert_quant_equal(W, 8, "special values G=8")
 
 
+@pytest.mark.parametrize("K,N,G", [
+    (128, 68, 32),       # 4 columns per thread: block columns 0-63, tail 64-67
+    (64, 33, 8),         # one column per thread: block 0-31, tail column 32
+    (64, 70, 16),
+    (48, 40, 12),        # G % 8 != 0 kernel
+    (512, 1, 32),        # N = 1, G >= 32: torch's inner reduction
+    (1024, 1, 64),
+    (576, 1, 36),        # N = 1 through the G % 8 != 0 kernel
+    (4096, 1, 4096),     # one group
+    (256, 1, 16),        # N = 1, G < 32: first zero
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quantize_mixed_zero_minima(K, N, G, dtype):
+    """Groups whose minimum is a zero and that hold both +0.0 and -0.0 at random
+    rows: the zero-point's sign bit follows which zero torch's CPU amin returns
+    (block / tail columns, N = 1 lanes), bit-exact against the oracle."""
+    log(f"quantize mixed zero minima K={K} N={N} G={G} {dtype}")
+    rng = np.random.default_rng(K * 13 + N * 7 + G)
+    ng = K // G
+    W = (np.abs(rng.standard_normal((ng, G, N))) * 0.1 + 0.01).astype(np.float32)
+    for _ in range(3):
+        rows = rng.integers(0, G, (ng, N))
+        gi, ni = np.nonzero(rng.random((ng, N)) < 0.85)
+        W[gi, rows[gi, ni], ni] = np.where(rng.integers(0, 2, gi.size) == 1, -0.0, 0.0)
+    Wt = torch.from_numpy(W.reshape(K, N)).to(dtype)
+    _, _, z = _assert_quant_equal(Wt, G, f"mixed zeros K={K} N={N} G={G}")
+    if ng * N >= 16:
+        zb = np_(z).view(np.uint16)
+        assert (zb == 0x8000).any() and (zb == 0x0000).any()   # both zero signs occur
+
+
 def test_quantize_fp32_tiny_and_denormal_ranges():
     log("quantize fp32 tiny ranges")
     K, N, G = 64, 8, 32
@@ -144,6 +175,8 @@ def test_quantize_full_size_layers(cfg):
     for G in Gs:
         log(f"quantize full {cfg} K={Kdim} N={N} G={G}")
         qw, s, z = quantize_weight(Wd, G)
+        # N and the slice width are multiples of 32, so each column is in a whole
+        # 32-column block of both the slice and the full weight (zero-sign rule)
         for a, b in ((0, 256), (N // 2 - 128, N // 2 + 128), (N - 256, N)):
             rq, rs, rz = O.quantize_weight(W[:, a:b].numpy(), G)
             assert np.array_equal(np_(qw[:, a:b]), rq), (cfg, G, a)

@@ -190,16 +190,94 @@ def test_quantize_reciprocal_scale_would_differ():
     assert (a.view(np.uint32) != b.view(np.uint32)).any()
 
 
-def test_group_min_last_zero_convention():
-    """A group whose minimum is a zero, holding both +0.0 and -0.0: the last zero
-    in k order is the minimum; zero-point = clamp(round(-gmin/scale)) then
-    carries the opposite sign."""
+def test_group_min_zero_sign_block_and_tail_columns():
+    """A group whose minimum is a zero, holding both +0.0 and -0.0 (hand-derived):
+    a column in a whole block of 32 takes the last zero in k order, a tail column
+    (n >= 32 * (N // 32)) the first; zero-point = clamp(round(-gmin/scale)) then
+    carries the opposite sign.  Scale and codes do not depend on it."""
     a = np.array([0.0, -0.0, 1.0, 0.5, 0.25, 0.75, 0.125, 0.375], dtype=np.float16)
     b = np.array([-0.0, 0.0, 1.0, 0.5, 0.25, 0.75, 0.125, 0.375], dtype=np.float16)
-    _, _, za = O.quantize_weight(a.reshape(8, 1), 8)
-    _, _, zb = O.quantize_weight(b.reshape(8, 1), 8)
-    assert int(za.view(np.uint16)[0, 0]) == 0x0000   # gmin = -0.0 -> zero +0
-    assert int(zb.view(np.uint16)[0, 0]) == 0x8000   # gmin = +0.0 -> zero -0
+    W = np.tile(np.ones(8, np.float16)[:, None], (1, 33))
+    W[:, 0], W[:, 1], W[:, 31], W[:, 32] = a, b, a, b
+    qa, sa, za = O.quantize_weight(W, 8)
+    zbits = za.view(np.uint16)[0]
+    assert int(zbits[0]) == 0x0000    # block column, last zero -0.0 -> zero +0
+    assert int(zbits[1]) == 0x8000    # block column, last zero +0.0 -> zero -0
+    assert int(zbits[31]) == 0x0000
+    assert int(zbits[32]) == 0x0000   # tail column, first zero -0.0 -> zero +0
+    Wt = W[:, [32]]                   # N = 1: its only column is a tail column
+    _, _, z1 = O.quantize_weight(Wt, 8)
+    assert int(z1.view(np.uint16)[0, 0]) == 0x0000
+    _, _, z1a = O.quantize_weight(W[:, [0]], 8)
+    assert int(z1a.view(np.uint16)[0, 0]) == 0x8000   # first zero +0.0 -> zero -0
+    # N = 1, G = 32: lane p % 8 of accumulator (p // 8) % 4; the lower lane wins,
+    # then the higher accumulator
+    c = np.ones((32, 1), np.float16)
+    c[0], c[1] = 0.0, -0.0            # lanes 0 and 1: lane 0 (+0.0) -> zero -0
+    assert int(O.quantize_weight(c, 32)[2].view(np.uint16)[0, 0]) == 0x8000
+    c[1], c[8] = 1.0, -0.0            # lane 0 of accumulators 0 and 1: -0.0 -> zero +0
+    assert int(O.quantize_weight(c, 32)[2].view(np.uint16)[0, 0]) == 0x0000
+    # codes and scales are the same for both zero signs
+    assert (qa[:, 0] == qa[:, 1]).all() and sa[0, 0] == sa[0, 1]
+
+
+def _planted_zero_groups(rng, ng, G, N):
+    """Positive groups with 1-3 zeros of random sign at random rows."""
+    W = (np.abs(rng.standard_normal((ng, G, N))) + 0.5).astype(np.float32)
+    for count in range(3):
+        rows = rng.integers(0, G, (ng, N))
+        sign = rng.integers(0, 2, (ng, N)).astype(bool)
+        keep = rng.random((ng, N)) < 0.8
+        gi, ni = np.nonzero(keep)
+        W[gi, rows[gi, ni], ni] = np.where(sign[gi, ni], -0.0, 0.0)
+    return W
+
+
+@pytest.mark.parametrize("threads", [1, 8])
+def test_group_min_matches_torch_amin(threads):
+    """The oracle's group minimum against torch's CPU ``amin(dim=1)`` itself (the
+    routine quant.py:127 calls), bit for bit including the sign of zero minima,
+    on the [ng, G, N] view quant.py:125 reduces: every N from 1 to 70 (tail-only,
+    block-only and mixed layouts), single-column weights with G from 32 to 4096
+    (torch's contiguous inner reduction) and 4096 x 4100 weights."""
+    torch = pytest.importorskip("torch")
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        rng = np.random.default_rng(21 + threads)
+        shapes = [(2, G, N) for N in range(1, 71) for G in (2, 8, 32)] + [(32, 128, 4100)]
+        shapes += [(64, G, 1) for G in (33, 40, 64, 96, 100, 128, 256, 4096)]
+        for ng, G, N in shapes:
+            W = _planted_zero_groups(rng, ng, G, N)
+            # quant.py:124-127: fp32 copy of the [K, N] weight, reshaped, amin over dim 1
+            t = torch.from_numpy(W.reshape(ng * G, N).copy()).reshape(ng, G, N).amin(dim=1)
+            o = O._group_min(W)
+            mism = np.nonzero(t.numpy().view(np.uint32) != o.view(np.uint32))
+            assert mism[0].size == 0, f"ng={ng} G={G} N={N}: first mismatch at {mism[0][0], mism[1][0]}"
+    finally:
+        torch.set_num_threads(prev)
+
+
+def test_quant_primitives_match_torch():
+    """The oracle's fp32 steps against the torch CPU routines quant.py:129-138
+    calls: ``/ 15`` (IEEE division), ``round`` (half to even, -0.0 kept) and
+    ``clamp`` (-0.0 kept) -- bit for bit, on random values, halves and zeros."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        (rng.standard_normal(200000) * 3).astype(np.float32),
+        np.arange(-40, 41, dtype=np.float32) / 2,                       # exact halves
+        np.array([0.0, -0.0, -0.4, 0.4, 15.5, -1e-30, 16.0, 14.5], np.float32),
+    ])
+    t = torch.from_numpy(x)
+    div = (t / 15).numpy()
+    assert (div.view(np.uint32) == (x / np.float32(15)).view(np.uint32)).all()
+    rnd = torch.round(t).numpy()
+    assert (rnd.view(np.uint32) == np.rint(x).view(np.uint32)).all()
+    r = np.rint(x).astype(np.float32)
+    clp = torch.clamp(torch.from_numpy(r), 0, 15).numpy()
+    assert (clp.view(np.uint32) == O._clamp_keep_neg_zero(r, 0, 15).view(np.uint32)).all()
+    assert np.signbit(O._clamp_keep_neg_zero(np.float32([-0.0]), 0, 15)[0])
 
 
 @pytest.mark.parametrize("group_size", [64, 128])

@@ -9,8 +9,18 @@
 // rint is round-half-to-even (v_rndne_f32).  HIP divides fp32 with the correctly
 // rounded sequence by default, and the build never enables fast-math, so the
 // compare-selects are not folded into min/max (which could drop -0.0).
-// Group minimum: when several zeros tie, the last one in k order wins
-// (v <= min ? v : min), matching torch's vectorised CPU column reduction.
+// Group minimum, as torch's CPU amin(dim=1) returns it when a group's minimum
+// is a zero and the group holds both +0.0 and -0.0 (measured on torch's CPU
+// reduction; the same on its DEFAULT, AVX2 and AVX512 code paths):
+//  * N >= 2 (the reduced rows are strided): columns in whole blocks of 32
+//    (n < 32 * (N / 32), the vectorised outer reduction) take the last zero in
+//    k order (v <= min ? v : min), the N % 32 tail columns (its scalar loop) the
+//    first (v < min ? v : min);
+//  * N == 1 (the group's G values are contiguous): G < 32 takes the first zero;
+//    G >= 32 follows the vectorised inner reduction (inner_zero_min below).
+// Only the sign of the zero-point depends on it; the group maximum's zero sign
+// reaches no output (gmax - gmin is the same for either zero, or the scale is
+// replaced by 1).
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -47,6 +57,43 @@ struct InF32 {
   }
 };
 
+// Running group minimum; tie_last selects which of two equal values (only
+// +0.0 / -0.0 differ in bits) is kept.
+__device__ __forceinline__ float min_step(float v, float mn, bool tie_last) {
+  return (v < mn || (tie_last && v == mn)) ? v : mn;
+}
+
+// N == 1, G >= 32, a group whose minimum is a zero: the zero torch's
+// vectorised inner reduction returns.  It reduces the first 32 * (G / 32) values
+// with 4 accumulators of 8 lanes (position p in lane p % 8 of accumulator
+// (p / 8) % 4; a tie keeps the later value), folds accumulator 0 with 1, 2, 3 in
+// turn (a tie keeps the later accumulator) and the lanes toward lane 0 (a tie
+// keeps the lower lane), then scans the G % 32 tail values (a tie keeps the
+// running minimum).  So among the zeros the lowest lane wins, then the highest
+// accumulator, then the latest position; a tail zero only wins when no zero
+// precedes the tail, and then the first one.  Only called when the group's
+// minimum is a zero, so it rescans just those groups.
+template <class IN>
+__device__ float inner_zero_min(const typename IN::T* __restrict__ src, int G) {
+  const int B = 32 * (G / 32);
+  uint64_t best = ~0ull;
+  float z = 0.0f;
+  for (int p = 0; p < G; ++p) {
+    const float v = IN::val(src[p]);
+    if (v != 0.0f) continue;
+    const int s = p & 31;
+    // p >> 5 < 2^26 for any int G, so the chunk term fits its 28 bits
+    const uint64_t key = p < B ? ((uint64_t)(s & 7) << 32) | ((uint64_t)(3 - (s >> 3)) << 28) |
+                                     (uint64_t)(0x0FFFFFFF - (p >> 5))
+                               : (8ull << 32) | (uint64_t)p;
+    if (key < best) {
+      best = key;
+      z = v;
+    }
+  }
+  return z;
+}
+
 __device__ __forceinline__ float clamp_q(float v) {
   v = (v < 0.0f) ? 0.0f : v;
   v = (v > 15.0f) ? 15.0f : v;
@@ -75,6 +122,9 @@ __global__ __launch_bounds__(256) void quantize_kernel(const typename IN::T* __r
   const int g = blockIdx.x;
   if (n >= N) return;
   const T* src = W + (size_t)g * G * N + n;
+  // CPT divides 32 and n is a multiple of CPT: all CPT columns lie on one side.
+  static_assert(32 % CPT == 0, "a thread's columns must not straddle a 32-column block");
+  const bool tie_last = n < 32 * (N / 32);
 
   float mn[CPT], mx[CPT];
   bool bad = false;
@@ -94,11 +144,14 @@ __global__ __launch_bounds__(256) void quantize_kernel(const typename IN::T* __r
     for (int c = 0; c < CPT; ++c) {
       bad |= IN::nonfinite(b[c]);
       const float v = IN::val(b[c]);
-      mn[c] = (v <= mn[c]) ? v : mn[c];
+      mn[c] = min_step(v, mn[c], tie_last);
       mx[c] = (v >= mx[c]) ? v : mx[c];
     }
   }
   if (bad) *flag = 1;
+  if constexpr (CPT == 1) {
+    if (N == 1 && G >= 32 && mn[0] == 0.0f) mn[0] = inner_zero_min<IN>(src, G);
+  }
 
   float sc[CPT], zr[CPT];
 #pragma unroll
@@ -152,13 +205,15 @@ __device__ GroupQ group_stats(const typename IN::T* __restrict__ W, int g, int G
   typename IN::T b = src[0];
   bool bad = IN::nonfinite(b);
   float mn = IN::val(b), mx = mn;
+  const bool tie_last = n < 32 * (N / 32);
   for (int r = 1; r < G; ++r) {
     b = src[(size_t)r * N];
     bad |= IN::nonfinite(b);
     const float v = IN::val(b);
-    mn = (v <= mn) ? v : mn;
+    mn = min_step(v, mn, tie_last);
     mx = (v >= mx) ? v : mx;
   }
+  if (N == 1 && G >= 32 && mn == 0.0f) mn = inner_zero_min<IN>(src, G);
   float s = (mx - mn) / 15.0f;
   s = (s > 0.0f) ? s : 1.0f;
   return GroupQ{s, clamp_q(__builtin_rintf(-mn / s)), bad};
