@@ -50,7 +50,8 @@ template <int MT, int CWL, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
-    float* __restrict__ part, int N, int K, int G, int rows_per_wg, int S, int nblk) {
+    float* __restrict__ part, int N, int K, uint32_t gmagic, int gshift, int rows_per_wg, int S,
+    int nblk) {
   constexpr int kThreads = GemvShape<WAVES>::kThreads;
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
@@ -62,14 +63,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int CHUNK = XD ? BR : kXsEntries / MT / BR * BR;   // packed rows of X per stage
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
   __shared__ uint4 xs[XD ? 1 : MT * CHUNK];
-  __shared__ float red[CWL <= 16 ? WAVES * 4 : WAVES][MT][CW];
+  __shared__ float red[WAVES][MT][CW];
 
   // XCD-aware block order (see header comment).
   const int nb = (int)gridDim.x;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
-  const int cb = lin % nblk;
-  const int sk = lin / nblk;
+  // without a split the block index is the column block (no division)
+  const int cb = S == 1 ? lin : lin % nblk;
+  const int sk = S == 1 ? 0 : lin / nblk;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -79,7 +81,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   const int n = cb * CW + 4 * cq;
   const bool nv = n < N;
   const int KP = K >> 3;
-  const int NG = K / G;
+  // k / G for 0 <= k < 2^31 without a division in front of the first loads:
+  // (umulhi(k, gmagic) + k) >> gshift with gshift = ceil(log2 G) and gmagic =
+  // floor(2^32 (2^gshift - G) / G) + 1 (exact for k < 2^31; 1 for a power of two)
+  auto group_of = [&](int k) {
+    return (int)((__umulhi((uint32_t)k, gmagic) + (uint32_t)k) >> gshift);
+  };
+  const int NG = group_of(K);
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
   const MagicRegs mg = make_magic();
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       // the group differs between row-lanes: its offset goes in the VGPR operand
-      const int g = min(((r0 + RH * h) * 8) / G, NG - 1);
+      const int g = min(group_of((r0 + RH * h) * 8), NG - 1);
       const uint32_t so = nv ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
       b.s[h] = buf_load8(rs, so, 0u);
       b.z[h] = buf_load8(rz, so, 0u);
@@ -211,29 +219,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   }
 
   // Reduce over row-lanes in a fixed order.  Inside each 16-lane DPP row the
-  // lanes with equal cq are combined by row rotations (register-to-register,
-  // no LDS round trip); the per-row partial sums then go through LDS once and
-  // thread t < CW adds the PS partial sets of its column in set order.
-  constexpr int PS = CWL <= 16 ? WAVES * 4 : WAVES;   // partial sets per workgroup
-  if constexpr (CWL <= 4) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] += dpp_row_ror<4>(acc[m][c]);
-  }
-  if constexpr (CWL <= 8) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] += dpp_row_ror<8>(acc[m][c]);
-  }
+  // lanes with equal cq are combined by row rotations, then a transpose-reduce
+  // over the wave's four 16-lane rows leaves column slot c of the lane's quad in
+  // row c (register-to-register, fixed order); the per-wave sums go through LDS
+  // once and thread t < CW adds the WAVES partial sets of its column in wave
+  // order.
+  constexpr int PS = WAVES;   // partial sets per workgroup
   if constexpr (CWL <= 16) {
-    const int row = lane >> 4;
-    if ((lane & 15) < CWL) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
-        *reinterpret_cast<float4*>(&red[wave * 4 + row][m][4 * cq]) =
-            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    for (int m = 0; m < MT; ++m) {
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[c] = acc[m][c];
+        if constexpr (CWL <= 4) v[c] += dpp_row_ror<4>(v[c]);
+        if constexpr (CWL <= 8) v[c] += dpp_row_ror<8>(v[c]);
+      }
+      const float r = fold_rows4(v[0], v[1], v[2], v[3]);
+      if ((lane & 15) < CWL) red[wave][m][4 * cq + (lane >> 4)] = r;
     }
   } else {
 #pragma unroll
@@ -278,17 +281,30 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   }
 }
 
+// Reciprocal form of k / G for the kernel (see group_of).
+struct GroupDiv {
+  uint32_t magic;
+  int shift;
+};
+GroupDiv group_div(int G) {
+  int l = 0;
+  while ((1ll << l) < (long long)G) ++l;
+  const uint64_t m = ((1ull << 32) * (uint64_t)((1ll << l) - G)) / (uint64_t)G + 1;
+  return GroupDiv{(uint32_t)m, l};
+}
+
 template <int MT, int CWL, int WAVES>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;
   const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
   float* part = split > 1 ? static_cast<float*>(ws) : nullptr;
+  const GroupDiv gd = group_div(a.G);
   hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES>), dim3(nblk * split),
                      dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), part, a.N, a.K, a.G, rows, split, nblk);
+                     static_cast<f16*>(a.y), part, a.N, a.K, gd.magic, gd.shift, rows, split, nblk);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, split, st);

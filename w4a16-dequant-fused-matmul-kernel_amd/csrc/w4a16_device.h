@@ -140,6 +140,33 @@ __device__ __forceinline__ float dpp_row_ror(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + kN, 0xF, 0xF, false));
 }
 
+// Row exchanges between two registers (16-lane rows r0..r3 of a wave):
+// v_permlane16_swap swaps the odd rows of `a` with the even rows of `b`,
+// v_permlane32_swap the upper 32 lanes of `a` with the lower 32 lanes of `b`.
+// Inline asm: the compiler's builtins for these instructions hand back the
+// first register for both results.  The s_nops give the VALU -> permlane and
+// permlane -> DPP wait states the compiler cannot see through the asm.
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Transpose-reduce of four values over the four 16-lane rows: on return, row c
+// of the result holds v_c summed over the rows, (r0 + r1) + (r2 + r3), at the
+// same position within the row.
+//   swap16(v0, v1), swap16(v2, v3); s01 = v0 + v1, s23 = v2 + v3:
+//     s01 rows = (v0 r0+r1, v1 r0+r1, v0 r2+r3, v1 r2+r3), s23 likewise;
+//   swap32(s01, s23); s01 + s23: row c = v_c (r0+r1) + v_c (r2+r3).
+__device__ __forceinline__ float fold_rows4(float v0, float v1, float v2, float v3) {
+  permlane16_swap(v0, v1);
+  permlane16_swap(v2, v3);
+  float s01 = v0 + v1, s23 = v2 + v3;
+  permlane32_swap(s01, s23);
+  return s01 + s23;
+}
+
 __device__ __forceinline__ f16 f32_to_f16(float x) { return (f16)x; }  // v_cvt_f16_f32, RNE
 
 // Buffer resource over [p, p + bytes): raw buffer loads outside the range return
