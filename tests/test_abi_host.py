@@ -174,7 +174,7 @@ def test_planner_gemv_split_rule():
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv"
         assert p.split_k == 1 and p.workspace_bytes == 0
         assert p.tile_n in (16, 32, 64, 256)
-        assert p.tile_cfg in (0, 1)
+        assert p.tile_cfg in (1, 2)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
     for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 2048, 28672)):
@@ -192,6 +192,33 @@ def test_planner_gemv_split_rule():
         assert p.workspace_bytes == p.split_k * 2 * 1024 * 4
     p1 = _lib.plan(1, 1024, 4096, 128, _lib.KERNEL_GEMV, 1)
     assert p1.split_k == 1 and p1.workspace_bytes == 0
+
+
+def test_planner_gemv_blocks_and_waves():
+    """Decode block and wave rules (measured on MI355X): 16 waves for M <= 2 on
+    16/32-column blocks with short rows per split, else 8; 32-column blocks
+    where 16-column ones would leave every CU between one and two blocks (K <
+    8192 only)."""
+    from w4a16 import _lib
+
+    p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
+    assert (p.tile_n, p.tile_cfg) == (16, 2)
+    p = _lib.plan(1, 6144, 4096, 128)            # 384 blocks of 16 -> 192 of 32
+    assert (p.tile_n, p.tile_cfg) == (32, 2)
+    p = _lib.plan(2, 6144, 4096, 128)
+    assert (p.tile_n, p.tile_cfg) == (32, 2)
+    p = _lib.plan(1, 6144, 14336, 128)           # long K keeps 16-column blocks
+    assert p.tile_n == 16
+    p = _lib.plan(2, 4096, 14336, 128)           # long rows at M = 2: 8 waves
+    assert p.tile_cfg == 1
+    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1
+    assert p.tile_cfg == 2
+    p = _lib.plan(1, 28672, 4096, 128)           # 64-column blocks: 8 waves
+    assert (p.tile_n, p.tile_cfg) == (64, 1)
+    p = _lib.plan(1, 8192, 28672, 128)
+    assert (p.tile_n, p.tile_cfg) == (32, 1)
+    p = _lib.plan(2, 1024, 8192, 128)            # split 4: 2048 rows per split
+    assert p.split_k == 4 and p.tile_cfg == 2
 
 
 def test_planner_small_batch_wide_weights_stream():

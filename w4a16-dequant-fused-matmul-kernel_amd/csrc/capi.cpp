@@ -64,11 +64,31 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 
 // Widest column block that still gives every CU a workgroup; split K across
 // workgroups only when even 16-column blocks cannot fill the device.
-int gemv_cols_auto(int64_t N, int cus) {
+// GEMV column block (measured on MI355X, M = 1 and 2): the widest block that
+// still gives every CU a workgroup; for K < 8192 (no split), where 16-column
+// blocks would leave the CUs between one and two blocks each, 32-column blocks
+// (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
+// 7.5 us at M = 2).
+int gemv_cols_auto(int64_t N, int64_t K, int cus) {
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
-    if ((N + c - 1) / c >= cus) return c;
+    if ((N + c - 1) / c >= cus) {
+      const int64_t b16 = (N + 15) / 16;
+      if (c == 16 && K < 8192 && b16 > cus && b16 <= 2 * (int64_t)cus) return 32;
+      return c;
+    }
   return 16;
+}
+
+// GEMV waves per workgroup (measured on MI355X): 16 waves (two packed rows per
+// lane) for M <= 2 with 16- or 32-column blocks and short rows per split
+// (K / split <= 8192, or 16384 at M = 1): C2 5.14 -> 5.02 us, M = 2 5.88 ->
+// 5.49 us; 8 waves for wider blocks and longer K (K = 28672, N = 8192: 29.7 us
+// against 33.4).
+int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
+  const int64_t ks = K / (split > 0 ? split : 1);
+  if (M <= 2 && cols <= 32 && ks <= (M == 1 ? 16384 : 8192)) return 2;
+  return kGemvDefaultConfig;
 }
 
 // GEMV k-split by shape (measured on MI355X, M = 1..8, fp32 partials plus the
@@ -187,7 +207,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   switch (kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
-      const int cols = gemv_cols_auto(N, cus);
+      const int cols = gemv_cols_auto(N, K, cus);
       int S = split > 0 ? split : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
@@ -197,7 +217,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
         S = (int)((KP + rows - 1) / rows);
       }
       p->split_k = S;
-      p->tile_cfg = kGemvDefaultConfig;
+      p->tile_cfg = gemv_waves_cfg(M, K, S, cols);
       p->tile_m = 0;
       p->tile_n = cols;
       p->grid_x = ((N + cols - 1) / cols) * S;

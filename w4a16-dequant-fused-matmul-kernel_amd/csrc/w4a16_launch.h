@@ -26,7 +26,8 @@ struct GemmArgs {
 constexpr int kGemvMaxM = 8;
 constexpr int kGemvConfigs = 3;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
-// other's outstanding loads (measured faster on MI355X for M = 1 decode shapes).
+// other's outstanding loads; the planner takes 16 waves (cfg 2) for M <= 2 on
+// narrow blocks and short rows, where they measured faster on MI355X.
 constexpr int kGemvDefaultConfig = 1;
 bool gemv_cols_valid(int cols);
 bool gemv_cfg_valid(int cfg, int M);
