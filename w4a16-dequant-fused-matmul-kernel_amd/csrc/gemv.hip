@@ -65,8 +65,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   __shared__ uint4 xs[XD ? 1 : MT * CHUNK];
   __shared__ float red[WAVES][MT][CW];
 
-  // XCD-aware block order (see header comment).
+  // 16-column blocks: every kernel argument in one batch of scalar loads up
+  // front (left to the compiler, the pointers are read only after the
+  // block-order branches, a second and third dependent kernarg round trip
+  // before the first weight load).  Measured on MI355X: C2 5.01 -> 4.86 us,
+  // M = 2 5.50 -> 5.29 us, but K = 14336 N = 4096 12.96 -> 13.24 us; the
+  // 32-column kernel measured 2-3 % slower with it, so it keeps the compiler's
+  // order.
   const int nb = (int)gridDim.x;
+  if constexpr (CWL <= 4)
+    asm volatile("" ::"s"(X), "s"(QW), "s"(SC), "s"(ZR), "s"(bias), "s"(Y), "s"(part), "s"(N),
+                 "s"(K), "s"(gmagic), "s"(gshift), "s"(rows_per_wg), "s"(S), "s"(nblk), "s"(nb));
+
+  // XCD-aware block order (see header comment).
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
   // without a split the block index is the column block (no division)
