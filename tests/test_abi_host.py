@@ -92,10 +92,17 @@ def test_split_k_gemv_requires_workspace(lib):
                                       a, 16, NULL)
     assert code == -4
     # a wave configuration the kernel does not have
-    p.tile_cfg = 3
+    p.tile_cfg = 6
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       a, 1 << 30, NULL)
     assert code == -5
+    # 16 waves and the LDS-staged activation configurations are for M <= 2 only
+    p4 = _lib.plan(4, 1024, 4096, 128, _lib.KERNEL_GEMV, 4)
+    for cfg in (2, 3, 4, 5):
+        p4.tile_cfg = cfg
+        code = lib.w4a16_gemm_f16_planned(ctypes.byref(p4), a, a, a, a, NULL, a, 4, 1024, 4096,
+                                          128, a, 1 << 30, NULL)
+        assert code == -5
     p.tile_cfg = 1
     # a column width the kernel does not have
     p.tile_n = 48
@@ -174,7 +181,7 @@ def test_planner_gemv_split_rule():
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv"
         assert p.split_k == 1 and p.workspace_bytes == 0
         assert p.tile_n in (16, 32, 64, 256)
-        assert p.tile_cfg in (1, 2)
+        assert p.tile_cfg in (1, 2, 4, 5)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
     for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 2048, 28672)):
@@ -195,10 +202,12 @@ def test_planner_gemv_split_rule():
 
 
 def test_planner_gemv_blocks_and_waves():
-    """Decode block and wave rules (measured on MI355X): 16 waves for M <= 2 on
-    16/32-column blocks with short rows per split, else 8; 32-column blocks
-    where 16-column ones would leave every CU between one and two blocks (K <
-    8192 only)."""
+    """Decode block, wave and activation-staging rules (measured on MI355X): 16
+    waves for M <= 2 on 16/32-column blocks with short rows per split, else 8;
+    32-column blocks where 16-column ones would leave every CU between one and
+    two blocks (K < 8192 only); activations staged in LDS (cfg + 3) for M <= 2
+    on 64-column blocks and for M = 1 on long 16-column rows, one chunk, no
+    split."""
     from w4a16 import _lib
 
     p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
@@ -211,10 +220,14 @@ def test_planner_gemv_blocks_and_waves():
     assert p.tile_n == 16
     p = _lib.plan(2, 4096, 14336, 128)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
-    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1
+    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, staged
+    assert p.tile_cfg == 5
+    p = _lib.plan(1, 28672, 4096, 128)           # 64-column blocks: 8 waves, staged
+    assert (p.tile_n, p.tile_cfg) == (64, 4)
+    p = _lib.plan(2, 28672, 8192, 128)
+    assert (p.tile_n, p.tile_cfg) == (64, 4)
+    p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 28672, 4096, 128)           # 64-column blocks: 8 waves
-    assert (p.tile_n, p.tile_cfg) == (64, 1)
     p = _lib.plan(1, 8192, 28672, 128)
     assert (p.tile_n, p.tile_cfg) == (32, 1)
     p = _lib.plan(2, 1024, 8192, 128)            # split 4: 2048 rows per split

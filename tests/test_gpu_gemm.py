@@ -113,19 +113,21 @@ def test_config_c5_large_layer(KN, G):
 # --------------------------------------------------------------------------- #
 RAGGED = [
     (1, 64, 260, 32), (3, 96, 12, 32), (8, 4096, 4100, 128), (5, 11008, 1028, 64),
-    (2, 1024, 256, 32), (7, 160, 520, 32),
+    (2, 1024, 256, 32), (7, 160, 520, 32), (2, 16640, 132, 128),
 ]
 
 
 @pytest.mark.parametrize("M,K,N,G", RAGGED)
 def test_gemv_splits(M, K, N, G):
     """Decode GEMV with every column-block width, every wave count (4, 8, and
-    16 waves per workgroup for M <= 2) and k-splits 1, 2, 3, 7, auto."""
+    16 waves per workgroup for M <= 2), the LDS-staged activations (cfg 3-5,
+    M <= 2; K = 16640 needs several staging chunks) and k-splits 1, 2, 3, 7,
+    auto."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M + K)
     ref = _ref(X, qw, s, z, G)
-    for cfg in ((0, 1, 2) if M <= 2 else (0, 1)):
+    for cfg in ((0, 1, 2, 3, 4, 5) if M <= 2 else (0, 1)):
         for cols in (16, 32, 64, 256):
             for split in (1, 2, 3, 7, 0):
                 if split > K // 8:

@@ -85,10 +85,21 @@ int gemv_cols_auto(int64_t N, int64_t K, int cus) {
 // (K / split <= 8192, or 16384 at M = 1): C2 5.14 -> 5.02 us, M = 2 5.88 ->
 // 5.49 us; 8 waves for wider blocks and longer K (K = 28672, N = 8192: 29.7 us
 // against 33.4).
+//
+// Activations staged in LDS (cfg + 3, M <= 2): one load and one permute per
+// element instead of one per lane sharing a row, at the cost of a barrier in
+// front of the first dot product.  Measured on MI355X: faster on 64-column
+// blocks (16 lanes per row; M = 2, K = 4096, N = 28672: 23.1 -> 19.6 us;
+// M = 2, K = 8192, N = 28672: 40.2 -> 33.7 us) and for M = 1 on long rows of
+// 16-column blocks (K = 14336, N = 4096: 13.6 -> 12.8 us); slower at short K
+// (C2: 4.84 -> 5.72 us), on 32-column blocks at K = 28672 (two staging chunks)
+// and with splits.
 int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   const int64_t ks = K / (split > 0 ? split : 1);
-  if (M <= 2 && cols <= 32 && ks <= (M == 1 ? 16384 : 8192)) return 2;
-  return kGemvDefaultConfig;
+  const int waves = (M <= 2 && cols <= 32 && ks <= (M == 1 ? 16384 : 8192)) ? 2 : kGemvDefaultConfig;
+  const bool stage = M <= 2 && (split <= 1) && ks <= 16384 &&
+                     (cols >= 64 || (M == 1 && cols == 16 && ks >= 12288));
+  return stage ? waves + 3 : waves;
 }
 
 // GEMV k-split by shape (measured on MI355X, M = 1..8, fp32 partials plus the

@@ -46,7 +46,7 @@ struct GemvShape {
   static constexpr int kBatch = WAVES >= 16 ? 2 : WAVES >= 8 ? 4 : 8;
 };
 
-template <int MT, int CWL, int WAVES>
+template <int MT, int CWL, int WAVES, bool STAGE>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
@@ -56,7 +56,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
   constexpr int H = BR / RH;               // halves per batch
-  constexpr bool XD = MT <= 2;             // activations read directly from global
+  // activations read directly from global (M <= 2 unless STAGE) or staged in LDS
+  constexpr bool XD = MT <= 2 && !STAGE;
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
   constexpr int CW = 4 * CWL;              // columns per workgroup
@@ -210,7 +211,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
                                  : kOobOffset;
         xv[i] = buf_load16(rx, off, 0u);
       }
-      if (lb < le) load_batch(lb, le, ba);
+      // Unconditional (a lane without rows reads only out-of-range weight rows
+      // and a clamped group), so the loads in flight are the same on every
+      // path and the waits below count exactly; the scheduling barrier keeps
+      // the activation permutes, and their waits, behind the weight loads.
+      load_batch(lb, le, ba);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
         const int idx = tid + i * kThreads;
@@ -304,14 +310,14 @@ GroupDiv group_div(int G) {
   return GroupDiv{(uint32_t)m, l};
 }
 
-template <int MT, int CWL, int WAVES>
+template <int MT, int CWL, int WAVES, bool STAGE>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;
   const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
   float* part = split > 1 ? static_cast<float*>(ws) : nullptr;
   const GroupDiv gd = group_div(a.G);
-  hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES>), dim3(nblk * split),
+  hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE>), dim3(nblk * split),
                      dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
@@ -321,28 +327,38 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, split, st);
 }
 
-template <int MT, int WAVES>
+template <int MT, int WAVES, bool STAGE>
 hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_t st) {
   switch (cols) {
-    case 16: return launch_cwl<MT, 4, WAVES>(a, split, ws, st);
-    case 32: return launch_cwl<MT, 8, WAVES>(a, split, ws, st);
-    case 64: return launch_cwl<MT, 16, WAVES>(a, split, ws, st);
-    case 256: return launch_cwl<MT, 64, WAVES>(a, split, ws, st);
+    case 16: return launch_cwl<MT, 4, WAVES, STAGE>(a, split, ws, st);
+    case 32: return launch_cwl<MT, 8, WAVES, STAGE>(a, split, ws, st);
+    case 64: return launch_cwl<MT, 16, WAVES, STAGE>(a, split, ws, st);
+    case 256: return launch_cwl<MT, 64, WAVES, STAGE>(a, split, ws, st);
     default: return hipErrorInvalidValue;
   }
 }
 
+// cfg % 3 picks 4, 8 or 16 waves; cfg >= 3 stages the activations in LDS for
+// M <= 2 (larger M always stages them).  16 waves only for M <= 2 (the
+// reduction buffer grows with waves x M).
 template <int MT>
-hipError_t launch_mt(const GemmArgs& a, int cols, int waves_cfg, int split, void* ws,
-                     hipStream_t st) {
-  switch (waves_cfg) {
-    case 0: return launch_w<MT, 4>(a, cols, split, ws, st);
-    case 1: return launch_w<MT, 8>(a, cols, split, ws, st);
-    case 2:
-      // 16 waves: only for M <= 2 (the reduction buffer grows with waves x M)
-      if constexpr (MT <= 2) return launch_w<MT, 16>(a, cols, split, ws, st);
-      return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
+hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {
+  if constexpr (MT <= 2) {
+    switch (cfg) {
+      case 0: return launch_w<MT, 4, false>(a, cols, split, ws, st);
+      case 1: return launch_w<MT, 8, false>(a, cols, split, ws, st);
+      case 2: return launch_w<MT, 16, false>(a, cols, split, ws, st);
+      case 3: return launch_w<MT, 4, true>(a, cols, split, ws, st);
+      case 4: return launch_w<MT, 8, true>(a, cols, split, ws, st);
+      case 5: return launch_w<MT, 16, true>(a, cols, split, ws, st);
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (cfg) {
+      case 0: return launch_w<MT, 4, false>(a, cols, split, ws, st);
+      case 1: return launch_w<MT, 8, false>(a, cols, split, ws, st);
+      default: return hipErrorInvalidValue;
+    }
   }
 }
 

@@ -21,10 +21,12 @@ struct GemmArgs {
 
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
 // consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
-// picks 4 (cfg 0), 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup; with
-// split > 1, `ws` holds the fp32 partials of gemv_workspace_bytes().
+// picks 4 (cfg 0), 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup, and
+// cfg 3..5 the same with the activations staged in LDS (M <= 2; larger M
+// always stages them); with split > 1, `ws` holds the fp32 partials of
+// gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
-constexpr int kGemvConfigs = 3;
+constexpr int kGemvConfigs = 6;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
 // other's outstanding loads; the planner takes 16 waves (cfg 2) for M <= 2 on
 // narrow blocks and short rows, where they measured faster on MI355X.
