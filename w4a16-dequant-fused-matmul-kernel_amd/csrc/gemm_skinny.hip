@@ -16,7 +16,8 @@
 //     whole batches; each wave walks its run in
 //     batches of 8 k-steps (256 k) with two register batches used ping-pong, all
 //     loads of batch i+1 -- weights, scales, zeros and activations -- issued
-//     before batch i is consumed;
+//     before batch i is consumed, unconditionally (past the range they read
+//     zeros), so the compiler's wait counts are exact;
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
 //     the buffer range check;
@@ -94,18 +95,22 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int ks = s0 + j;
-      if (ks < ke) {   // wave-uniform
-        const uint32_t wk = uniform((uint32_t)ks * 4u * (uint32_t)N * 4u);
+      // every step issues its loads; steps past this wave's range (wave-uniform)
+      // read zeros through an out-of-range offset and are never processed
+      const bool in = ks < ke;
+      {
+        const uint32_t wk = uniform(in ? (uint32_t)ks * 4u * (uint32_t)N * 4u : kOobOffset);
         b.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
         if (j % GSTEP == 0) {
-          const uint32_t gk = uniform((uint32_t)((ks * 32) / G) * (uint32_t)N * 2u);
+          const uint32_t gk =
+              uniform(in ? (uint32_t)((ks * 32) / G) * (uint32_t)N * 2u : kOobOffset);
           const uint32_t sv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
           const uint32_t zv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
           b.sz[j] = (sv & 0xFFFFu) | (zv << 16);
         } else {
           b.sz[j] = b.sz[j - j % GSTEP];   // same group as the batch slot it copies
         }
-        const uint32_t xk = uniform((uint32_t)ks * 64u);
+        const uint32_t xk = uniform(in ? (uint32_t)ks * 64u : kOobOffset);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
       }
@@ -132,15 +137,19 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     }
   };
 
-  Batch ba, bb;
-  if (kb < ke) load_batch(kb, ba);
+  // Two register batches used ping-pong.  The loads are unconditional and the
+  // only branches (skipping a batch past the range, and the step check inside
+  // process) contain no loads, so every path has the same loads in flight and
+  // the compiler's vmcnt waits count exactly; with loads under the branches
+  // its waits at the joins covered the next batch too (C3 M = 4..32 measured
+  // 2-11 % slower that way).
+  Batch bt[2];
+  load_batch(kb, bt[0]);
   for (int s0 = kb; s0 < ke; s0 += 2 * kBatch) {
-    const bool more1 = s0 + kBatch < ke;
-    if (more1) load_batch(s0 + kBatch, bb);
-    process(ba, s0);
-    if (!more1) break;
-    if (s0 + 2 * kBatch < ke) load_batch(s0 + 2 * kBatch, ba);
-    process(bb, s0 + kBatch);
+    load_batch(s0 + kBatch, bt[1]);
+    process(bt[0], s0);
+    load_batch(s0 + 2 * kBatch, bt[0]);
+    if (s0 + kBatch < ke) process(bt[1], s0 + kBatch);
   }
 
 #pragma unroll
