@@ -128,7 +128,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     for (int h = 0; h < H; ++h) {
       // the group differs between row-lanes: its offset goes in the VGPR operand
       const int g = min(group_of((r0 + RH * h) * 8), NG - 1);
-      const uint32_t so = nv ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
+      // a batch past the lane's run (issued only to keep the loads the same
+      // on every path) reads nothing from memory
+      const uint32_t so = (nv && r0 < le) ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
       b.s[h] = buf_load8(rs, so, 0u);
       b.z[h] = buf_load8(rz, so, 0u);
     }
@@ -137,8 +139,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int u = 0; u < BR; ++u)
-          b.x[m * BR + u] = buf_load16(rx, ((uint32_t)m * (uint32_t)K + (uint32_t)r0 * 8u) * 2u,
-                                       uniform((uint32_t)u * 16u));
+          b.x[m * BR + u] = buf_load16(
+              rx, r0 < le ? ((uint32_t)m * (uint32_t)K + (uint32_t)r0 * 8u) * 2u : kOobOffset,
+              uniform((uint32_t)u * 16u));
     }
     // One path for full and partial batches (a lane-dependent branch here would
     // move the row offset out of the SGPR and serialise the loads).
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 
     Batch ba, bb;
     if constexpr (XD) {
-      if (lb < le) load_batch(lb, le, ba);
+      load_batch(lb, le, ba);
     } else {
       // Stage X rows [c0, c1) into LDS; its loads go out before the first
       // weight batch, so the barrier waits only for them.
@@ -225,13 +228,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       __syncthreads();
     }
 
-    // two register batches used ping-pong: no copies between iterations
-    for (int r0 = lb; r0 < le; r0 += 2 * BR) {
-      if (r0 + BR < le) load_batch(r0 + BR, le, bb);
-      process(ba, r0, le, c0);
-      if (r0 + BR >= le) break;
-      if (r0 + 2 * BR < le) load_batch(r0 + 2 * BR, le, ba);
-      process(bb, r0 + BR, le, c0);
+    // Two register batches used ping-pong.  The trip count is the same for
+    // every lane (`per` rows; past its own run a lane's loads read nothing and
+    // process() skips its rows), and the loads are unconditional, so every
+    // path has the same loads in flight and the compiler's waits count
+    // exactly (with lane-dependent branches around the loads, its waits at the
+    // joins covered the next batch too: 2-10 % slower on multi-batch runs).  A
+    // one-batch run (C2) has nothing to prefetch and skips the loop.
+    const int nbat = per / BR;
+    if (nbat == 1) {
+      process(ba, lb, le, c0);
+    } else {
+      for (int i = 0; i < nbat; i += 2) {
+        const int r0 = lb + i * BR;
+        load_batch(r0 + BR, le, bb);
+        process(ba, r0, le, c0);
+        load_batch(r0 + 2 * BR, le, ba);
+        process(bb, r0 + BR, le, c0);
+      }
     }
   }
 
