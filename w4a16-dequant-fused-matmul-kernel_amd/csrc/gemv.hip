@@ -228,22 +228,34 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       __syncthreads();
     }
 
-    // Two register batches used ping-pong.  The trip count is the same for
-    // every lane (`per` rows; past its own run a lane's loads read nothing and
-    // process() skips its rows), and the loads are unconditional, so every
+    // Two register batches used ping-pong.  M <= 2: the trip count is the same
+    // for every lane (`per` rows; past its own run a lane's loads read nothing
+    // and process() skips its rows), and the loads are unconditional, so every
     // path has the same loads in flight and the compiler's waits count
     // exactly (with lane-dependent branches around the loads, its waits at the
-    // joins covered the next batch too: 2-10 % slower on multi-batch runs).  A
-    // one-batch run (C2) has nothing to prefetch and skips the loop.
-    const int nbat = per / BR;
-    if (nbat == 1) {
-      process(ba, lb, le, c0);
+    // joins covered the next batch too: 2-10 % slower on multi-batch runs); a
+    // one-batch run (C2) has nothing to prefetch and skips the loop.  M > 2
+    // keeps the per-lane loop, which measured 6-7 % faster there (M = 3, 4,
+    // K = 4096, N = 28672).
+    if constexpr (MT <= 2) {
+      const int nbat = per / BR;
+      if (nbat == 1) {
+        process(ba, lb, le, c0);
+      } else {
+        for (int i = 0; i < nbat; i += 2) {
+          const int r0 = lb + i * BR;
+          load_batch(r0 + BR, le, bb);
+          process(ba, r0, le, c0);
+          load_batch(r0 + 2 * BR, le, ba);
+          process(bb, r0 + BR, le, c0);
+        }
+      }
     } else {
-      for (int i = 0; i < nbat; i += 2) {
-        const int r0 = lb + i * BR;
-        load_batch(r0 + BR, le, bb);
+      for (int r0 = lb; r0 < le; r0 += 2 * BR) {
+        if (r0 + BR < le) load_batch(r0 + BR, le, bb);
         process(ba, r0, le, c0);
-        load_batch(r0 + 2 * BR, le, ba);
+        if (r0 + BR >= le) break;
+        if (r0 + 2 * BR < le) load_batch(r0 + 2 * BR, le, ba);
         process(bb, r0 + BR, le, c0);
       }
     }
