@@ -60,7 +60,9 @@ typedef struct w4a16_plan {
   int32_t split_k;         /* GEMV, MFMA cfg 7/8/11: k-splits (1 = none)        */
   int32_t tile_cfg;        /* MFMA: tile configuration 0..11 (tile_m x tile_n);
                               GEMV: 0 / 1 / 2 = 4 / 8 / 16 waves per workgroup
-                              (16 for M <= 2); SKINNY: 0 / 1 = 4 / 8 waves
+                              (16 for M <= 2), 3 / 4 / 5 = the same with the
+                              activations staged in LDS (M <= 2; larger M
+                              always stages them); SKINNY: 0 / 1 = 4 / 8 waves
                               (8 for M <= 32)                                  */
   int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup   */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
