@@ -49,7 +49,7 @@ enum w4a16_status {
 enum w4a16_kernel {
   W4A16_KERNEL_AUTO = 0,
   W4A16_KERNEL_GEMV = 1, /* decode: VALU dot2, no MFMA, M <= 8, optional split-K    */
-  W4A16_KERNEL_MFMA = 2, /* prefill: MFMA (32x32x16 / 16x16x32), tile_cfg 0..11     */
+  W4A16_KERNEL_MFMA = 2, /* prefill: MFMA (32x32x16 / 16x16x32), tile_cfg 0..13     */
   W4A16_KERNEL_SIMT = 3, /* sequential-k, one thread per output, any shape           */
   W4A16_KERNEL_SKINNY = 4 /* small batch: v_mfma_f32_16x16x32_f16, weights streamed   */
 };
@@ -57,8 +57,8 @@ enum w4a16_kernel {
 /* The launch a GEMM call will make.  Filled by w4a16_gemm_plan(). */
 typedef struct w4a16_plan {
   int32_t kernel;          /* enum w4a16_kernel (never AUTO once planned)       */
-  int32_t split_k;         /* GEMV, MFMA cfg 7/8/11: k-splits (1 = none)        */
-  int32_t tile_cfg;        /* MFMA: tile configuration 0..11 (tile_m x tile_n);
+  int32_t split_k;         /* GEMV, MFMA cfg 7/8/11-13: k-splits (1 = none)     */
+  int32_t tile_cfg;        /* MFMA: tile configuration 0..13 (tile_m x tile_n);
                               GEMV: 0 / 1 / 2 = 4 / 8 / 16 waves per workgroup
                               (16 for M <= 2), 3 / 4 / 5 = the same with the
                               activations staged in LDS (M <= 2; larger M

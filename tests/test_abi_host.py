@@ -144,13 +144,15 @@ def test_quant_entry_points_reject_bad_args(lib):
 
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
-    (4, 28672, 4096, 128, "gemv"),   # wide N: the GEMV up to M = 4
+    (3, 28672, 4096, 128, "gemv"),   # wide N: the GEMV up to M = 3
+    (4, 28672, 4096, 128, "mfma"),   # ... from M = 4 the streamed small-M tiles
     (2, 6144, 4096, 128, "gemv"),
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
     (8, 4096, 4096, 128, "skinny"),
-    (5, 28672, 4096, 128, "skinny"),  # wide N from M = 5
+    (5, 28672, 4096, 128, "mfma"),
     (9, 4096, 4096, 128, "skinny"),
-    (64, 4096, 11008, 64, "skinny"),
+    (64, 4096, 11008, 64, "mfma"),
+    (24, 4096, 4096, 128, "skinny"),  # 8 MiB of weights: skinny up to M = 32
     (65, 4096, 4096, 128, "mfma"),
     (4096, 14336, 4096, 128, "mfma"),
     (16, 4096, 4096, 32, "skinny"),
@@ -235,29 +237,38 @@ def test_planner_gemv_blocks_and_waves():
 
 
 def test_planner_small_batch_wide_weights_stream():
-    """9 <= M <= 64 on wide or long weights takes the streamed prefill kernel
-    split along K (about 448 workgroups, >= 8 k-steps per split); narrow N or
-    small weights stay on the skinny kernel."""
+    """4 <= M <= 64 on large enough weights takes the streamed prefill kernel
+    with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K for
+    about 448 workgroups with >= 8 k-steps per split; narrow N or small weights
+    stay on the skinny kernel (or the GEMV for M <= 3)."""
     from w4a16 import _lib
 
-    for M, N, K, s in ((16, 28672, 4096, 4), (32, 28672, 4096, 4), (16, 8192, 28672, 14),
-                       (64, 28672, 8192, 4), (48, 14336, 4096, 8)):
+    for M, N, K, cfg, s in ((16, 28672, 4096, 12, 4), (32, 28672, 4096, 12, 4),
+                            (16, 8192, 28672, 12, 14), (8, 28672, 8192, 12, 4),
+                            (32, 4096, 14336, 12, 28), (64, 28672, 8192, 13, 4),
+                            (48, 14336, 4096, 13, 8), (64, 4096, 4096, 13, 8)):
         p = _lib.plan(M, N, K, 128)
-        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 11, (M, N, K)
-        assert p.split_k == s and p.workspace_bytes >= s * M * N * 4
-        assert p.grid_x == s * ((N + 255) // 256)
-    for M, N, K in ((16, 4096, 4096), (32, 4096, 14336), (64, 4096, 4096), (16, 6144, 4096),
-                    (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
+        rows = 32 if cfg == 12 else 64
+        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == cfg, (M, N, K)
+        assert (p.tile_m, p.tile_n) == (rows, 256)
+        assert p.split_k == s and p.workspace_bytes >= s * M * N * 4, (M, N, K, p.split_k)
+        assert p.grid_x == s * ((N + 255) // 256) * ((M + rows - 1) // rows)
+    for M, N, K in ((16, 4096, 4096), (16, 4096, 14336), (24, 4096, 4096), (16, 6144, 4096),
+                    (9, 8192, 8192), (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
 
 
 def test_planner_prefill_split_k():
     from w4a16 import _lib
 
-    # C5 down-projection at M = 256: 64 tiles of 128 x 256 -> split along K
+    # C5 down-projection at M = 256: 64 tiles of 128 x 256 -> 7 splits (~448
+    # workgroups); the up-projection's 224 tiles -> 2
     p = _lib.plan(256, 8192, 28672, 128)
     assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 11
-    assert p.split_k > 1 and p.grid_x >= 256
+    assert p.split_k == 7 and p.grid_x == 448
+    assert _lib.plan(256, 28672, 8192, 128).split_k == 2
+    assert _lib.plan(128, 28672, 8192, 128).split_k == 4
+    assert _lib.plan(2048, 14336, 4096, 128).split_k == 1    # 896 tiles
     assert p.workspace_bytes >= p.split_k * 256 * 8192 * 4
     # large M: no split, no workspace
     p = _lib.plan(4096, 14336, 4096, 128)

@@ -151,8 +151,9 @@ def test_mfma_tile_configs(M, K, N, G):
     """Prefill MFMA kernels with every tile configuration over tails in M, N, K
     (configs 4, 9, 10 -- weight tile dequantised into LDS -- and 7, 8 -- two
     waves per SIMD with 16x16x32 MFMAs -- where K % 64 == 0; configs 5 and 6,
-    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; config 11,
-    activations and weights streamed into LDS, where K % 256 == 0)."""
+    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; configs 11,
+    12 and 13, activations and weights streamed into LDS with 128-, 32- and
+    64-row tiles, where K % 256 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
@@ -160,7 +161,7 @@ def test_mfma_tile_configs(M, K, N, G):
     ref = _ref(X, qw, s, z, G)
     for cfg in range(_lib.MFMA_CONFIGS):
         if ((cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128)
-                or (cfg == 11 and K % 256)):
+                or (cfg >= 11 and K % 256)):
             continue
         p = plan_for(M, N, K, G, "mfma", 1)
         p.tile_cfg = cfg
@@ -176,7 +177,7 @@ def test_mfma_tile_configs(M, K, N, G):
     (65, 4096, 1028, 128), (200, 2048, 516, 32), (256, 11008, 772, 64), (130, 2112, 260, 96),
 ])
 def test_mfma_split_k(M, K, N, G):
-    """Prefill split-K (cfg 7, 8 and, where K % 256 == 0, 11): fp32 partials per
+    """Prefill split-K (cfg 7, 8 and, where K % 256 == 0, 11-13): fp32 partials per
     k-split, summed in split order by a second kernel; every split count, fused
     bias; then a forced GEMV split-K call reuses the same cached workspace."""
     from w4a16 import w4a16_matmul
@@ -185,7 +186,7 @@ def test_mfma_split_k(M, K, N, G):
     X, qw, s, z = _build_case(M, K, N, G, seed=M + N + K)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in (7, 8, 11) if K % 256 == 0 else (7, 8):
+    for cfg in (7, 8, 11, 12, 13) if K % 256 == 0 else (7, 8):
         for split in (2, 3, 5, K // 64):
             p = plan_for(M, N, K, G, "mfma", split)
             p.tile_cfg = cfg

@@ -120,10 +120,14 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
 //     half the CUs or M >= 1024: 5-8 % faster than cfg 7 at C4 M = 4096,
 //     15-20 % at M = 512 and at C5 M = 256; without K % 256 == 0, cfg 7 for
 //     M >= 1024 and the 32x32x16 two-waves kernel (cfg 6) for the rest;
-//   * fewer tiles (short M, narrow N): cfg 11 (or cfg 7) split along K so that
-//     the tiles times the splits give every CU a workgroup (fp32 partials + one
-//     reduction kernel), when K allows at least 8 k-steps per split; else
-//     narrow 32 x 512 tiles (cfg 2) or the one-wave 128 x 256 (cfg 1).
+//   * fewer tiles (short M, narrow N): cfg 11 split along K for about two
+//     workgroups per CU (cfg 7 for one per CU where K % 256 != 0; fp32
+//     partials + one reduction kernel), when K allows at least 8 k-steps per
+//     split; else narrow 32 x 512 tiles (cfg 2) or the one-wave 128 x 256
+//     (cfg 1);
+//   * M <= 64: the same streamed kernel with 32-row (M <= 32, cfg 12) or
+//     64-row tiles (cfg 13), split likewise (small_m_takes_stream below says
+//     when it beats the skinny and decode kernels).
 struct MfmaChoice {
   int cfg, split;
 };
@@ -140,21 +144,26 @@ bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G) {
   return M >= 3 && M <= kGemvMaxM && skinny_applicable(M, G) && (N <= 16384 || M >= 5);
 }
 
-// Small batches (9 <= M <= 64) on wide or long weights: the streamed prefill
-// kernel split along K beats the skinny kernel once the weights are large
-// enough (measured on MI355X: M = 32, K = 4096, N = 28672: 37.8 vs 67.2 us;
-// M = 16, K = 8192, N = 28672: 58 vs 79-95 us; M = 48, K = 4096, N = 14336:
-// 26.8 vs 53.8 us; M = 64, K = 8192, N = 28672: 66 vs 241 us).  It loses
-// below ~32 column tiles (N < 8192: too little work per split; M = 32, K =
-// 14336, N = 4096: 40.6 vs 35.2 us) and on small weights, where its fixed
-// cost (~15 us) dominates; the skinny kernel's cost grows with M, so the size
-// threshold falls with M.
-bool skinny_takes_stream(int64_t M, int64_t N, int64_t K, int64_t G) {
-  if (M <= kGemvMaxM || M > kSkinnyMaxM || N < 8192) return false;
-  if (!mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G)) return false;
-  const int64_t wbytes = K / 2 * N;
-  const int64_t need = M <= 16 ? (48ll << 20) : M <= 32 ? (16ll << 20) : (8ll << 20);
-  return wbytes >= need;
+// Small batches (4 <= M <= 64) on large enough weights: the streamed prefill
+// kernel with 32-row (M <= 32) or 64-row tiles (cfg 12 / 13), split along K
+// for about 448 workgroups, beats the skinny kernel and the decode GEMV
+// (measured on MI355X against each one's best plan): M = 8, K = 8192, N =
+// 28672: 37.2 vs 57.6 us; M = 16, K = 4096, N = 28672: 23.5 vs 38.9 (and vs
+// 67 for the skinny kernel); M = 32, K = 14336, N = 4096: 23.5 vs 31.9; M = 64,
+// K = 4096, N = 14336: 24.6 vs 70.5; M = 4, K = 28672, N = 8192: 40.0 vs 47.2.
+// Its fixed cost (a split-K pass, K-steps of 64) loses on small weights, and
+// the skinny kernel's cost grows with M, so the size threshold falls with M:
+// M = 16 keeps the skinny kernel at K = 14336, N = 4096 (20.3 vs 22.4) and
+// below 20 MB; M = 9 wins only from N = 14336 (16.9 vs 18.1); M <= 3 keeps the
+// GEMV (M = 3, K = 4096, N = 28672: 21.9 vs 22.7).
+bool small_m_takes_stream(int64_t M, int64_t N, int64_t K, int64_t G) {
+  if (M < 4 || M > kSkinnyMaxM) return false;
+  if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return false;
+  const int64_t mb = K / 2 * N >> 20;   // packed weight MiB
+  if (M >= 48) return true;
+  if (M >= 24) return mb > 8;
+  if (M >= 16) return N >= 8192 && mb >= 20;
+  return (N >= 14336 && mb >= 24) || mb >= 64;
 }
 
 // k-splits for the streamed kernel on few tiles: about 448 workgroups (two
@@ -168,24 +177,33 @@ int stream_split_for(int64_t tiles, int64_t K) {
 
 MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) {
-    if (!skinny_takes_stream(M, N, K, G)) return {2, 1};
-    const int s = stream_split_for((N + 255) / 256 * ((M + 127) / 128), K);
-    return {11, s > 1 ? stream_splits((int)K, s) : 1};
+    if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return {2, 1};
+    const int rows = M <= 32 ? 32 : 64;
+    const int s = stream_split_for((N + 255) / 256 * ((M + rows - 1) / rows), K);
+    return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
   const bool c7 = mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G);
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
   if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
+  // cfg 11 on fewer than ~448 tiles: split K for about two workgroups per CU
+  // (measured on MI355X: M = 128, K = 8192, N = 28672: 77.7 us at 4 splits vs
+  // 90.2 at 3; M = 256: 133.2 at 2 vs 149.8 unsplit; M = 256, K = 28672, N =
+  // 8192: 137.9 at 7 vs 146.8 at 4; M = 512, K = 4096, N = 14336: 80.8 at 2 vs
+  // 82.7)
+  if (c11 && t6 < 448) {
+    const int s = stream_split_for(t6, K);
+    if (s >= 2) return {11, stream_splits((int)K, s)};
+  }
   if (2 * t6 >= cus) {
     if (c11) return {11, 1};
     if (mfma_cfg_applicable(6, (int)M, (int)N, (int)K, (int)G)) return {6, 1};
   }
-  if (c11 || c7) {
+  if (c7) {
     const int64_t kt = K / 64;
     int64_t s = (cus + t6 - 1) / t6;
     if (s > kt / 8) s = kt / 8;
-    if (s >= 2) return c11 ? MfmaChoice{11, stream_splits((int)K, (int)s)}
-                           : MfmaChoice{7, occ2_splits((int)K, (int)s)};
+    if (s >= 2) return {7, occ2_splits((int)K, (int)s)};
   }
   const int64_t t2 = ((N + 511) / 512) * ((M + 31) / 32);
   if (2 * t6 < cus && t2 > t6) return {2, 1};
@@ -204,9 +222,11 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
+    else if (small_m_takes_stream(M, N, K, G))
+      kernel = W4A16_KERNEL_MFMA;
     else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G))
       kernel = W4A16_KERNEL_GEMV;
-    else if (M <= kSkinnyMaxM && skinny_applicable(M, G) && !skinny_takes_stream(M, N, K, G))
+    else if (M <= kSkinnyMaxM && skinny_applicable(M, G))
       kernel = W4A16_KERNEL_SKINNY;
     else if (mfma_applicable(N, G))
       kernel = W4A16_KERNEL_MFMA;
@@ -239,9 +259,9 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     case W4A16_KERNEL_MFMA: {
       if (!mfma_applicable(N, G)) return W4A16_ERR_BAD_PLAN;
       MfmaChoice c = mfma_choice(M, N, K, G, cus);
-      if (split > 0) {   // a forced split runs on cfg 11 (cfg 7 where K % 256 != 0)
+      if (split > 0) {   // a forced split runs on the streamed kernel (cfg 7 where K % 256 != 0)
         const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
-        c.cfg = split > 1 ? (c11 ? 11 : 7) : c.cfg;
+        c.cfg = split > 1 ? (c.cfg >= 11 ? c.cfg : (c11 ? 11 : 7)) : c.cfg;
         c.split = split > 1 ? (c11 ? stream_splits((int)K, split) : occ2_splits((int)K, split)) : 1;
         if (c.split > 1 && !mfma_cfg_applicable(c.cfg, (int)M, (int)N, (int)K, (int)G))
           return W4A16_ERR_BAD_PLAN;

@@ -530,6 +530,8 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 // cfg 10: 256 x 256, as cfg 9
 // cfg 11: 128 x 256 as cfg 7, packed weights streamed into LDS four k-steps
 //         ahead (gemm_stream.hip)
+// cfg 12:  32 x 256, the cfg 11 kernel with 2 m-tiles per wave (small M)
+// cfg 13:  64 x 256, the cfg 11 kernel with 4 m-tiles per wave
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
     case 0: return {128, 512};
@@ -543,11 +545,13 @@ MfmaTile mfma_tile(int cfg) {
     case 9: return {256, 224};
     case 10: return {256, 256};
     case 11: return {128, 256};
+    case 12: return {32, 256};
+    case 13: return {64, 256};
     default: return {64, 512};
   }
 }
 
-bool mfma_cfg_splits(int cfg) { return cfg == 7 || cfg == 8 || cfg == 11; }
+bool mfma_cfg_splits(int cfg) { return cfg == 7 || cfg == 8 || cfg >= 11; }
 
 bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
   if (cfg < 0 || cfg >= kMfmaConfigs) return false;
@@ -555,7 +559,7 @@ bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
   if (cfg == 5 || cfg == 6) return K % (2 * kBK) == 0;
   if (cfg == 7 || cfg == 8) return occ2_gemm_applicable(M, N, K, G);
   if (cfg == 9 || cfg == 10) return ldsb_gemm_applicable(M, N, K, G);
-  if (cfg == 11) return stream_gemm_applicable(M, N, K, G);
+  if (cfg >= 11) return stream_gemm_applicable(M, N, K, G);
   return true;
 }
 
@@ -587,7 +591,9 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipSt
     case 8: return launch_occ2_gemm(a, true, split, part, st);
     case 9: return launch_ldsb_gemm(a, false, st);
     case 10: return launch_ldsb_gemm(a, true, st);
-    case 11: return launch_stream_gemm(a, split, part, st);
+    case 11: return launch_stream_gemm(a, 128, split, part, st);
+    case 12: return launch_stream_gemm(a, 32, split, part, st);
+    case 13: return launch_stream_gemm(a, 64, split, part, st);
     default: return hipErrorInvalidValue;
   }
 }

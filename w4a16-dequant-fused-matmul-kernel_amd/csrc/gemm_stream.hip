@@ -59,13 +59,14 @@ namespace {
 
 constexpr int kBK = 64;
 constexpr int kGroupM = 4;     // M-tiles per group of the tile order
-constexpr int kMT = 8;         // 16-row MFMA tiles per wave (128 rows)
 constexpr int kNTiles = 4;     // 16-column MFMA tiles per wave (64 columns)
 constexpr int kStages = 4;     // weight stages per wave (steps in flight)
 constexpr int kWaves = 4;      // waves per workgroup, all along N
 constexpr int kNT = 64 * kWaves;
-constexpr int kBM = 16 * kMT;              // 128 rows
 constexpr int kBN = 16 * kNTiles * kWaves; // 256 columns
+// kMT = 16-row MFMA tiles per wave: 8 (128-row workgroup tiles, prefill), 4
+// or 2 (64 / 32 rows: small M, where a 128-row tile would spend most of its
+// matrix-core time on rows past M; the dequant per weight is the same)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -100,12 +101,19 @@ __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t 
   }
 }
 
+template <int kMT>
 __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
                    uint32_t sz_bytes, const f16* __restrict__ bias, f16* __restrict__ Y,
                    float* __restrict__ part, int M, int N, int K, int G, int KTS) {
   static_assert(kStages == 4, "stage arrays below are written out for four stages");
+  static_assert(kMT == 2 || kMT == 4 || kMT == 8, "8-row activation loads per wave");
+  constexpr int kBM = 16 * kMT;          // rows per workgroup tile
+  constexpr int kRPW = kBM / kWaves;     // activation rows each wave streams
+  constexpr int kAL = kRPW / 8;          // its 8-row loads per step
+  // dequant VALU per MFMA in the interleave: ~64 per half-step over its MFMAs
+  constexpr int kVPM = 64 / (kMT * kNTiles);
   // activation buffers: [row][8 octet slots], slot = octet ^ ((row / 2) % 8)
   __shared__ uint4 As0[kBM * 8], As1[kBM * 8];
   // weight stages, one array each (the compiler tracks at most 8 LDS-direct
@@ -156,15 +164,16 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(SZ, sz_bytes);
   (void)NG;
 
-  // Activation stream: wave w fills rows 32w .. 32w+31 with four loads of 8
-  // rows; lane L writes row 8j + L/8, slot L%8, which holds octet
-  // (L%8) ^ ((row/2)%8) = (L%8) ^ (L/16) ^ (4 if j is odd).  Rows at or past M
-  // lie beyond the buffer range (M*K*2 bytes) and read as zero.
+  // Activation stream: wave w fills rows kRPW w .. kRPW (w+1) - 1 with kAL
+  // loads of 8 rows; lane L writes row r = kRPW w + 8j + L/8, slot L%8, which
+  // holds octet (L%8) ^ ((r/2)%8) = (L%8) ^ (L/16) ^ (4 if kRPW w / 8 + j is
+  // odd).  Rows at or past M lie beyond the buffer range (M*K*2 bytes) and
+  // read as zero.
   const uint32_t a_voff0 =
       ((uint32_t)(lane >> 3) * (uint32_t)K + (uint32_t)((lane & 7) ^ (lane >> 4)) * 8u) * 2u;
   const uint32_t a_voff1 =
       ((uint32_t)(lane >> 3) * (uint32_t)K + (uint32_t)((lane & 7) ^ (lane >> 4) ^ 4) * 8u) * 2u;
-  const uint32_t a_row0 = (uint32_t)(m0 + 32 * wave) * (uint32_t)K * 2u;
+  const uint32_t a_row0 = (uint32_t)(m0 + kRPW * wave) * (uint32_t)K * 2u;
   // A fragment of m-tile i, half-step h: row 16i + l16, octet oct + 4h
   const int a_frag0 = l16 * 8 + ((oct) ^ ((l16 >> 1) & 7));
   const int a_frag1 = l16 * 8 + ((oct + 4) ^ ((l16 >> 1) & 7));
@@ -193,12 +202,12 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   // Past this workgroup's k-range (kt >= KT) the loads below take an offset no
   // buffer range holds and write zeros that are never read.
   auto stream_a = [&](auto bc, int kt) {
-    uint4* a = as(bc) + 32 * wave * 8;
+    uint4* a = as(bc) + kRPW * wave * 8;
     const uint32_t kb = (uint32_t)kt * (uint32_t)(kBK * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kAL; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (lds_void*)(a + 64 * j), 16, (j & 1) ? a_voff1 : a_voff0,
+          rx, (lds_void*)(a + 64 * j), 16, ((kRPW / 8 * wave + j) & 1) ? a_voff1 : a_voff0,
           uniform((kt < KT ? a_row0 + (uint32_t)(8 * j) * (uint32_t)K * 2u + kb : kOobOffset)), 0,
           0);
   };
@@ -283,7 +292,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
 #pragma unroll
     for (int i = 0; i < kMT * kNTiles; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kVPM, 0);
     }
   };
 
@@ -400,7 +409,9 @@ int split_steps(int K, int split) {
   return ((KT + split - 1) / split + kStages - 1) / kStages * kStages;
 }
 
+template <int kMT>
 hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
+  constexpr int kBM = 16 * kMT;
   const int tiles = ((a.N + kBN - 1) / kBN) * ((a.M + kBM - 1) / kBM);
   const int KT = a.K / kBK;
   // never more splits than occ2_splits() gives for the same request, so
@@ -413,7 +424,7 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
   const char* base = sc < zr ? sc : zr;
   const uint32_t sz_bytes = (uint32_t)((sc < zr ? zr : sc) - base) +
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
-  hipLaunchKernelGGL(stream_kernel, dim3(tiles * nsplit), dim3(kNT), 0, st,
+  hipLaunchKernelGGL(stream_kernel<kMT>, dim3(tiles * nsplit), dim3(kNT), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
@@ -435,18 +446,25 @@ bool stream_gemm_applicable(int M, int N, int K, int G) {
   return occ2_gemm_applicable(M, N, K, G) && K % (kBK * kStages) == 0;
 }
 
-// 128 x 256 tiles.  Same applicability and split rule as the two-waves-per-SIMD
-// register kernel, plus K % 256 == 0.  Scales and zeros further than 2 GiB
-// apart (one buffer resource cannot span them) take that register kernel
-// (same tiles, same results up to fp32 summation order inside an MFMA).
-hipError_t launch_stream_gemm(const GemmArgs& a, int split, float* part, hipStream_t st) {
+// rows x 256 tiles, rows = 128, 64 or 32.  Same applicability and split rule
+// as the two-waves-per-SIMD register kernel, plus K % 256 == 0.  Scales and
+// zeros further than 2 GiB apart (one buffer resource cannot span them) take
+// that register kernel (128 x 256 tiles, same results up to fp32 summation
+// order inside an MFMA).
+hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* part,
+                              hipStream_t st) {
   if (!stream_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
   if (occ2_splits(a.K, split) > 1 && !part) return hipErrorInvalidValue;
   const uintptr_t sc = reinterpret_cast<uintptr_t>(a.sc), zr = reinterpret_cast<uintptr_t>(a.zr);
   const uint64_t dist = sc < zr ? zr - sc : sc - zr;
   const uint64_t bytes = (uint64_t)(a.K / a.G) * (uint64_t)a.N * 2u;
   if (dist + bytes >= (1ull << 31)) return launch_occ2_gemm(a, false, split, part, st);
-  return launch_wg(a, split, part, st);
+  switch (rows) {
+    case 128: return launch_wg<8>(a, split, part, st);
+    case 64: return launch_wg<4>(a, split, part, st);
+    case 32: return launch_wg<2>(a, split, part, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace w4a16

@@ -42,7 +42,7 @@ hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws
 struct MfmaTile {
   int bm, bn;
 };
-constexpr int kMfmaConfigs = 12;
+constexpr int kMfmaConfigs = 14;
 MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
 // Whether tile configuration `cfg` can run this shape (some need K % 64 or 128).
@@ -66,13 +66,16 @@ bool occ2_gemm_applicable(int M, int N, int K, int G);
 // and the fp32 partial buffer they need (0 when not split).
 int occ2_splits(int K, int split);
 size_t occ2_workspace_bytes(int M, int N, int K, int split);
-// The same 128 x 256 tiling with the packed weights streamed into LDS four
-// k-steps ahead (mfma cfg 11): needs K % 256 == 0.
+// The 128 x 256 tiling of cfg 7 with the packed weights streamed into LDS
+// four k-steps ahead (mfma cfg 11), or 32 / 64 x 256 tiles of the same kernel
+// (cfg 12 / 13): needs K % 256 == 0.
 bool stream_gemm_applicable(int M, int N, int K, int G);
 // Splits the streamed kernel makes of a split request (whole 4-step blocks per
 // split; never more than occ2_splits() for the same request).
 int stream_splits(int K, int split);
-hipError_t launch_stream_gemm(const GemmArgs& a, int split, float* part, hipStream_t st);
+// rows = 128, 64 or 32 (tile rows of cfg 11, 13, 12).
+hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* part,
+                              hipStream_t st);
 hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
                             hipStream_t st);
 // Eight-wave kernel with the weight tile dequantised into LDS (mfma cfg 9:

@@ -18,7 +18,7 @@ KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT, KERNEL_SKINNY = 0, 1, 2, 3, 
 KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
                 KERNEL_SKINNY: "skinny"}
 # MFMA tile configurations 0 .. MFMA_CONFIGS-1 (w4a16_plan.tile_cfg)
-MFMA_CONFIGS = 12
+MFMA_CONFIGS = 14
 
 # enum w4a16_status
 STATUS = {
