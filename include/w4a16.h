@@ -14,14 +14,14 @@
  *
  * Tensor formats (reference: w4a16-kernel/src/w4a16/quant.py:1-30,
  * W4A16_SPEC.md:109-171), all row-major and contiguous:
- *   x       fp16  [M, K]        activations
+ *   x       fp16  [M, K]        activations (row stride ldx, w4a16_gemm_f16_strided)
  *   qweight int32 [K/8, N]      word (i, n) holds rows 8i..8i+7, row 8i+j in
  *                               bits [4j, 4j+4), unsigned codes 0..15
  *   scales  fp16  [K/G, N]
  *   zeros   fp16  [K/G, N]      integer zero-points (the fused GEMM kernels
  *                               require integers in [-63, 63]; quantize_weight
  *                               produces 0..15)
- *   y       fp16  [M, N]        Y = fp16(fp32-accumulated X @ dequant(W))
+ *   y       fp16  [M, N]        Y = fp16(fp32-accumulated X @ dequant(W)) (row stride ldy)
  */
 #ifndef W4A16_H_
 #define W4A16_H_
@@ -119,6 +119,25 @@ int w4a16_gemm_f16_planned(const w4a16_plan* plan, const void* x, const int32_t*
                            const void* scales, const void* zeros, const void* bias, void* y,
                            int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/*
+ * As w4a16_gemm_f16_planned with row strides: row m of x starts ldx elements
+ * after row m-1 (ldx >= K), row m of y ldy elements after row m-1 (ldy >= N),
+ * so x and y may be column slices of wider row-major buffers (a fused QKV
+ * output, a packed activation buffer).  The reference's kernel takes strides
+ * (w4a16-kernel/src/w4a16/triton_kernel.py:71-75, 94, 127) but its wrapper
+ * asserts contiguity (triton_kernel.py:170-173); this entry point exposes the
+ * row-strided case.  `plan` NULL chooses automatically; the vector kernels
+ * need ldx % 8 == 0 (and ldy % 4 == 0 where they store 4-column quads: MFMA
+ * plans and split-K), else the automatic plan takes the SIMT kernel and an
+ * explicit plan is refused (W4A16_ERR_BAD_PLAN).  ldx < K or ldy < N is
+ * W4A16_ERR_BAD_SHAPE.  The workspace is that of the same shape unstrided.
+ */
+int w4a16_gemm_f16_strided(const w4a16_plan* plan, const void* x, int64_t ldx,
+                           const int32_t* qweight, const void* scales, const void* zeros,
+                           const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                           int64_t group_size, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /*
  * Group-wise asymmetric uint4 quantisation of fp16 W [K, N] with int4 packing,

@@ -126,6 +126,39 @@ def test_planned_rejects_mismatched_plan(lib):
     assert code == -5
 
 
+def test_strided_entry_validates_row_strides(lib):
+    """w4a16_gemm_f16_strided: ldx >= K and ldy >= N (else BAD_SHAPE, before any
+    launch); a vector plan refuses strides its loads / stores cannot take."""
+    from w4a16 import _lib
+
+    a = ctypes.c_void_p(1 << 12)
+    M, N, K, G = 64, 4096, 4096, 128
+    p = _lib.plan(M, N, K, G, _lib.KERNEL_MFMA, 1)
+    for ldx, ldy in ((K - 8, N), (K, N - 4), (1 << 31, N), (K, 1 << 31)):
+        for plan in (ctypes.byref(p), NULL):
+            code = lib.w4a16_gemm_f16_strided(plan, a, ldx, a, a, a, NULL, a, ldy, M, N, K, G,
+                                              NULL, 0, NULL)
+            assert code == -2, (ldx, ldy)
+    # rows of x not 16-byte aligned (ldx % 8 != 0), rows of y not 8-byte
+    # aligned for the MFMA kernels' 4-column stores (ldy % 4 != 0)
+    for ldx, ldy in ((K + 4, N), (K, N + 2)):
+        code = lib.w4a16_gemm_f16_strided(ctypes.byref(p), a, ldx, a, a, a, NULL, a, ldy, M, N,
+                                          K, G, NULL, 0, NULL)
+        assert code == -5, (ldx, ldy)
+    # the skinny kernel stores single elements: any ldy
+    ps = _lib.plan(M, N, K, G, _lib.KERNEL_SKINNY, 0)
+    code = lib.w4a16_gemm_f16_strided(ctypes.byref(ps), a, K + 4, a, a, a, NULL, a, N + 1, M, N,
+                                      K, G, NULL, 0, NULL)
+    assert code == -5    # (ldx still must keep rows 16-byte aligned)
+    # a strided x beyond one buffer resource (2 GiB) is refused by a vector plan
+    code = lib.w4a16_gemm_f16_strided(ctypes.byref(p), a, 1 << 25, a, a, a, NULL, a, N, M, N, K,
+                                      G, NULL, 0, NULL)
+    assert code == -5
+    # empty shapes return before looking at pointers
+    assert lib.w4a16_gemm_f16_strided(NULL, NULL, K, NULL, NULL, NULL, NULL, NULL, N, 0, N, K, G,
+                                      NULL, 0, NULL) == 0
+
+
 def test_quant_entry_points_reject_bad_args(lib):
     a = ctypes.c_void_p(1 << 12)
     assert lib.w4a16_quantize_pack_f16(a, a, a, a, 100, 16, 64, a, NULL) == -2

@@ -300,18 +300,41 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
 
 int to_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : (int)e; }
 
-int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const void* sc,
-                const void* zr, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                int64_t G, void* ws, size_t ws_bytes, void* stream) {
+// Row strides: ldx >= K, ldy >= N, both int32, and the strided extents
+// addressable like the dense ones.
+int check_strides(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
+  if (ldx < K || ldy < N || ldx > INT32_MAX || ldy > INT32_MAX) return W4A16_ERR_BAD_SHAPE;
+  if (M > 0 && ((uint64_t)(M - 1) * (uint64_t)ldx > (1ull << 46) ||
+                (uint64_t)(M - 1) * (uint64_t)ldy > (1ull << 46)))
+    return W4A16_ERR_BAD_SHAPE;
+  return W4A16_OK;
+}
+
+// What the vector kernels need of the strides: 16-byte x rows (16-byte loads)
+// and x within one buffer resource (< 2 GiB); kernels that store 4-column
+// quads of y (the MFMA family and the split-K reduction) also 8-byte y rows.
+bool strides_vec_ok(const GemmArgs& a, int kernel, int split) {
+  const bool quad_stores = kernel == W4A16_KERNEL_MFMA || split > 1;
+  return a.ldx % 8 == 0 && (!quad_stores || a.ldy % 4 == 0) &&
+         x_extent_bytes(a) < (1ull << 31);
+}
+
+int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* qw,
+                const void* sc, const void* zr, const void* bias, void* y, int64_t ldy,
+                int64_t M, int64_t N, int64_t K, int64_t G, void* ws, size_t ws_bytes,
+                void* stream) {
   if (!p) return W4A16_ERR_NULL_POINTER;
   if (int st = check_gemm_shape(M, N, K, G)) return st;
+  if (int st = check_strides(M, N, K, ldx, ldy)) return st;
   if (M == 0 || N == 0) return W4A16_OK;
   if (!y || (K > 0 && (!x || !qw || !sc || !zr))) return W4A16_ERR_NULL_POINTER;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G};
+  GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy};
   // K = 0: Y = 0 (+ bias).  A kernel rather than a memset, so that the call
   // can be captured into a HIP graph; the SIMT kernel reads no operand then.
   if (K == 0) return to_status(launch_simt(a, s));
+  if (p->kernel != W4A16_KERNEL_SIMT && !strides_vec_ok(a, p->kernel, p->split_k))
+    return W4A16_ERR_BAD_PLAN;
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
@@ -319,7 +342,8 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;
-      if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8))
+      if (!aligned(x, 16) || !aligned(qw, 16) || !aligned(sc, 8) || !aligned(zr, 8) ||
+          (p->split_k > 1 && (!aligned(y, 8) || (bias && !aligned(bias, 8)))))
         return W4A16_ERR_BAD_PLAN;
       const size_t need = gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
       if (need > 0 && (!ws || ws_bytes < need || !aligned(ws, 256))) return W4A16_ERR_WORKSPACE;
@@ -356,20 +380,23 @@ int run_planned(const w4a16_plan* p, const void* x, const int32_t* qw, const voi
   }
 }
 
-// Automatic plan, falling back to the SIMT kernel when the pointers do not meet
-// the vector kernels' alignment.
-int run_auto(const void* x, const int32_t* qw, const void* sc, const void* zr, const void* bias,
-             void* y, int64_t M, int64_t N, int64_t K, int64_t G, void* ws, size_t ws_bytes,
-             void* stream) {
+// Automatic plan, falling back to the SIMT kernel when the pointers or row
+// strides do not meet the vector kernels' alignment.
+int run_auto(const void* x, int64_t ldx, const int32_t* qw, const void* sc, const void* zr,
+             const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t G,
+             void* ws, size_t ws_bytes, void* stream) {
   if (int st = check_gemm_shape(M, N, K, G)) return st;
+  if (int st = check_strides(M, N, K, ldx, ldy)) return st;
   w4a16_plan p;
   if (int st = make_plan(M, N, K, G, W4A16_KERNEL_AUTO, 0, &p)) return st;
+  const GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy};
   const bool vec_aligned = aligned(x, 16) && aligned(qw, 16) && aligned(sc, 8) &&
-                           aligned(zr, 8) && aligned(y, 8) && (!bias || aligned(bias, 8));
+                           aligned(zr, 8) && aligned(y, 8) && (!bias || aligned(bias, 8)) &&
+                           strides_vec_ok(a, p.kernel, p.split_k);
   if (p.kernel != W4A16_KERNEL_SIMT && !vec_aligned) {
     if (int st = make_plan(M, N, K, G, W4A16_KERNEL_SIMT, 0, &p)) return st;
   }
-  return run_planned(&p, x, qw, sc, zr, bias, y, M, N, K, G, ws, ws_bytes, stream);
+  return run_planned(&p, x, ldx, qw, sc, zr, bias, y, ldy, M, N, K, G, ws, ws_bytes, stream);
 }
 
 }  // namespace
@@ -411,7 +438,7 @@ size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
 int w4a16_gemm_f16(const void* x, const int32_t* qweight, const void* scales, const void* zeros,
                    void* y, int64_t M, int64_t N, int64_t K, int64_t group_size,
                    void* workspace, size_t workspace_bytes, void* stream) {
-  return run_auto(x, qweight, scales, zeros, nullptr, y, M, N, K, group_size, workspace,
+  return run_auto(x, K, qweight, scales, zeros, nullptr, y, N, M, N, K, group_size, workspace,
                   workspace_bytes, stream);
 }
 
@@ -419,7 +446,7 @@ int w4a16_linear_f16(const void* x, const int32_t* qweight, const void* scales,
                      const void* zeros, const void* bias, void* y, int64_t M, int64_t N,
                      int64_t K, int64_t group_size, void* workspace, size_t workspace_bytes,
                      void* stream) {
-  return run_auto(x, qweight, scales, zeros, bias, y, M, N, K, group_size, workspace,
+  return run_auto(x, K, qweight, scales, zeros, bias, y, N, M, N, K, group_size, workspace,
                   workspace_bytes, stream);
 }
 
@@ -427,8 +454,20 @@ int w4a16_gemm_f16_planned(const w4a16_plan* plan, const void* x, const int32_t*
                            const void* scales, const void* zeros, const void* bias, void* y,
                            int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
                            size_t workspace_bytes, void* stream) {
-  return run_planned(plan, x, qweight, scales, zeros, bias, y, M, N, K, group_size, workspace,
-                     workspace_bytes, stream);
+  return run_planned(plan, x, K, qweight, scales, zeros, bias, y, N, M, N, K, group_size,
+                     workspace, workspace_bytes, stream);
+}
+
+int w4a16_gemm_f16_strided(const w4a16_plan* plan, const void* x, int64_t ldx,
+                           const int32_t* qweight, const void* scales, const void* zeros,
+                           const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                           int64_t group_size, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (!plan)
+    return run_auto(x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size, workspace,
+                    workspace_bytes, stream);
+  return run_planned(plan, x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size,
+                     workspace, workspace_bytes, stream);
 }
 
 static int quantize_common(const void* W, bool f32, int32_t* qweight, void* scales, void* zeros,

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kNT) void lds_kernel(const f16* __restrict__ X,
                                                   const uint16_t* __restrict__ ZR,
                                                   const f16* __restrict__ bias,
                                                   f16* __restrict__ Y, int M, int N, int K,
-                                                  int G) {
+                                                  int G, int ldx, int ldy) {
   __shared__ uint4 As[2][kBM * kLdsRow];
   __shared__ uint4 Bs[2][kBN * kLdsRow];
 
@@ -94,7 +94,9 @@ __global__ __launch_bounds__(kNT) void lds_kernel(const f16* __restrict__ X,
   const int NG = K / G;
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(kNT) void lds_kernel(const f16* __restrict__ X,
   for (int i = 0; i < kAPerT; ++i) {
     const int o = tid + i * kNT;
     const int gm = m0 + (o >> 3);
-    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)ldx + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
   }
   // B slots: quad q = tid + i*kNT -> packed row q/64 (wave-uniform), columns
   // n0 + 4*(q%64) .. +3.  Slot i = 0 covers packed rows 0-3, i = 1 rows 4-7.
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(kNT) void lds_kernel(const f16* __restrict__ X,
           o.z = o.z + bv[2];
           o.w = o.w + bv[3];
         }
-        *reinterpret_cast<f16x4*>(Y + (size_t)row * N + ncol) = o;
+        *reinterpret_cast<f16x4*>(Y + (size_t)row * ldy + ncol) = o;
       }
     }
   }
@@ -272,7 +274,7 @@ hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(lds_kernel, dim3(tiles), dim3(kNT), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
 

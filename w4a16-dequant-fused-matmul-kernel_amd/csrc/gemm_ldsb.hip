@@ -47,7 +47,8 @@ template <int NTW>
 __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void ldsb_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                  const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
-                 const f16* __restrict__ bias, f16* __restrict__ Y, int M, int N, int K, int G) {
+                 const f16* __restrict__ bias, f16* __restrict__ Y, int M, int N, int K, int G,
+                 int ldx, int ldy) {
   constexpr int BNW = 16 * NTW;             // columns per wave
   constexpr int BN = BNW * kWavesN;         // columns per workgroup
   constexpr int QPR = BN / 4;               // weight quads per packed row
@@ -80,7 +81,9 @@ void ldsb_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   const int NG = K / G;
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -91,7 +94,7 @@ void ldsb_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   for (int i = 0; i < kAPerT; ++i) {
     const int o = tid + i * kNT;
     const int gm = m0 + (o >> 3);
-    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)ldx + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
   }
   // weight quad of this thread: packed row brow (0..7) of the step, columns bcol..+3
   const bool bq = tid < NQ;
@@ -187,7 +190,7 @@ void ldsb_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
         if (row < M) {
           f16 y = f32_to_f16(acc[i][c][r]);
           if (bias) y = y + bv;
-          Y[(size_t)row * N + col] = y;
+          Y[(size_t)row * ldy + col] = y;
         }
       }
     }
@@ -201,7 +204,7 @@ hipError_t launch_ntw(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((ldsb_kernel<NTW>), grid, dim3(kNT), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
 

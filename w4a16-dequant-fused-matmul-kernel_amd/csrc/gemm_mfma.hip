@@ -51,7 +51,7 @@ template <int WMT, int WAVES_M, int WAVES_N, bool KTAIL>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
-    int N, int K, int G) {
+    int N, int K, int G, int ldx, int ldy) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 128 * WAVES_N;
@@ -89,7 +89,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
   const int NG = K / G;
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
   for (int i = 0; i < A_PER_T; ++i) {
     const int o = tid + i * NT;
     const int gm = m0 + (o >> 3);
-    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)ldx + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
   }
   uint32_t b_off[4];
 #pragma unroll
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
           o.z = o.z + bv[2];
           o.w = o.w + bv[3];
         }
-        *reinterpret_cast<f16x4*>(Y + (size_t)row * N + ncol) = o;
+        *reinterpret_cast<f16x4*>(Y + (size_t)row * ldy + ncol) = o;
       }
     }
   }
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
 void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                       const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
                       const f16* __restrict__ bias, f16* __restrict__ Y, int M, int N, int K,
-                      int G) {
+                      int G, int ldx, int ldy) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 64 * WAVES_N;
@@ -328,7 +330,9 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
   const int NG = K / G;
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -338,7 +342,7 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
   for (int i = 0; i < A_PER_T; ++i) {
     const int o = tid + i * NT;
     const int gm = m0 + (o >> 3);
-    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)ldx + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
   }
   const uint32_t b_off = nv ? ((uint32_t)lhi * (uint32_t)N + (uint32_t)ncol) * 4u : kOobOffset;
   const uint32_t s_off = nv ? (uint32_t)ncol * 2u : kOobOffset;
@@ -475,7 +479,7 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
           o.x = o.x + bv0;
           o.y = o.y + bv1;
         }
-        *reinterpret_cast<f16x2*>(Y + (size_t)row * N + ncol) = o;
+        *reinterpret_cast<f16x2*>(Y + (size_t)row * ldy + ncol) = o;
       }
     }
   }
@@ -490,7 +494,7 @@ hipError_t launch_occ2(const GemmArgs& a, hipStream_t st) {
                      dim3(64 * WAVES_M * WAVES_N), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
 
@@ -508,10 +512,10 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   f16* y = static_cast<f16*>(a.y);
   if (a.K % kBK == 0)
     hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, false>), grid, block, 0, st, x, qw, sc,
-                       zr, bias, y, a.M, a.N, a.K, a.G);
+                       zr, bias, y, a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   else
     hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, true>), grid, block, 0, st, x, qw, sc,
-                       zr, bias, y, a.M, a.N, a.K, a.G);
+                       zr, bias, y, a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
 

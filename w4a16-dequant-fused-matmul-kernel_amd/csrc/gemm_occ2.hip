@@ -49,7 +49,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
 void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                  const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
                  const f16* __restrict__ bias, f16* __restrict__ Y, float* __restrict__ part,
-                 int M, int N, int K, int G, int KTS) {
+                 int M, int N, int K, int G, int KTS, int ldx, int ldy) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int BM = 16 * kMT * WAVES_M;
   constexpr int BN = 16 * kNTiles * WAVES_N;
@@ -94,7 +94,9 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   constexpr int NH = G64 ? 1 : 2;   // groups per 64-k step (G % 64 == 0: one)
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; rows at or past M fall outside the range
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -104,7 +106,7 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   for (int i = 0; i < A_PER_T; ++i) {
     const int o = tid + i * NT;
     const int gm = m0 + (o >> 3);
-    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)K + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
+    a_off[i] = gm < M ? ((uint32_t)gm * (uint32_t)ldx + (uint32_t)(o & 7) * 8u) * 2u : kOobOffset;
   }
   const uint32_t b_off = nv ? ((uint32_t)oct * (uint32_t)N + (uint32_t)ncol) * 4u : kOobOffset;
   const uint32_t s_off = nv ? (uint32_t)ncol * 2u : kOobOffset;
@@ -255,16 +257,18 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
           o.z = o.z + bv[2];
           o.w = o.w + bv[3];
         }
-        *reinterpret_cast<f16x4*>(Y + (size_t)row * N + ncol) = o;
+        *reinterpret_cast<f16x4*>(Y + (size_t)row * ldy + ncol) = o;
       }
     }
   }
 }
 
-// Y[row, 4c..4c+3] = fp16(sum over splits, in split order) (+ bias)
+// Y[row, 4c..4c+3] = fp16(sum over splits, in split order) (+ bias); the
+// partials are [S][M][N], Y's rows lie ldy elements apart
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ part,
                                                      const f16* __restrict__ bias,
-                                                     f16* __restrict__ Y, int M, int N, int S) {
+                                                     f16* __restrict__ Y, int M, int N, int ldy,
+                                                     int S) {
   const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;   // 4-column quad index
   const size_t nq = (size_t)M * (N / 4);
   if (q >= nq) return;
@@ -282,14 +286,15 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
   o.y = f32_to_f16(s.y);
   o.z = f32_to_f16(s.z);
   o.w = f32_to_f16(s.w);
+  const size_t row = off / (size_t)N;
+  const int col = (int)(off - row * (size_t)N);
   if (bias) {
-    const int col = (int)(off % (size_t)N);
     o.x = o.x + bias[col];
     o.y = o.y + bias[col + 1];
     o.z = o.z + bias[col + 2];
     o.w = o.w + bias[col + 3];
   }
-  *reinterpret_cast<f16x4*>(Y + off) = o;
+  *reinterpret_cast<f16x4*>(Y + row * (size_t)ldy + col) = o;
 }
 
 template <int WAVES_M, int WAVES_N, bool G64>
@@ -305,10 +310,10 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
                      static_cast<f16*>(a.y), nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G,
-                     nsplit > 1 ? kts : KT);
+                     nsplit > 1 ? kts : KT, a.ldx, a.ldy);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
-  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, nsplit, st);
+  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
 }
 
 }  // namespace
@@ -318,11 +323,11 @@ bool occ2_gemm_applicable(int M, int N, int K, int G) {
   return K % kBK == 0 && N % 4 == 0 && G % 32 == 0 && K % G == 0;
 }
 
-hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int S,
-                                hipStream_t st) {
+hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int ldy,
+                                int S, hipStream_t st) {
   const size_t nq = (size_t)M * (size_t)(N / 4);
   hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, part,
-                     static_cast<const f16*>(bias), static_cast<f16*>(y), M, N, S);
+                     static_cast<const f16*>(bias), static_cast<f16*>(y), M, N, ldy, S);
   return hipGetLastError();
 }
 

@@ -43,7 +43,7 @@ template <int MT, int GSTEP, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
-    int N, int K, int G, int nblk) {
+    int N, int K, int G, int nblk, int ldx, int ldy) {
   constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][64];
 
@@ -65,7 +65,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const int NG = K / G;
 
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int row = mt * 16 + c;
-    x_off[mt] = row < M ? ((uint32_t)row * (uint32_t)K + (uint32_t)q * 8u) * 2u : kOobOffset;
+    x_off[mt] = row < M ? ((uint32_t)row * (uint32_t)ldx + (uint32_t)q * 8u) * 2u : kOobOffset;
   }
 
   struct Batch {
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
         if (row < M) {
           f16 y = f32_to_f16(v[r]);
           if (bias) y = y + bv;
-          Y[(size_t)row * N + col] = y;
+          Y[(size_t)row * ldy + col] = y;
         }
       }
     }
@@ -186,7 +188,7 @@ hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
                          static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                          static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                          static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                         a.G, nblk);
+                         a.G, nblk, a.ldx, a.ldy);
       return hipGetLastError();
     }
   }
@@ -194,7 +196,7 @@ hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                     a.G, nblk);
+                     a.G, nblk, a.ldx, a.ldy);
   return hipGetLastError();
 }
 

@@ -106,7 +106,8 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
                    uint32_t sz_bytes, const f16* __restrict__ bias, f16* __restrict__ Y,
-                   float* __restrict__ part, int M, int N, int K, int G, int KTS) {
+                   float* __restrict__ part, int M, int N, int K, int G, int KTS, int ldx,
+                   int ldy) {
   static_assert(kStages == 4, "stage arrays below are written out for four stages");
   static_assert(kMT == 2 || kMT == 4 || kMT == 8, "8-row activation loads per wave");
   constexpr int kBM = 16 * kMT;          // rows per workgroup tile
@@ -159,7 +160,9 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
 
   uint32_t magic_mix;
   asm volatile("v_mov_b32 %0, 0x54006400" : "=v"(magic_mix));
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row M - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(SZ, sz_bytes);
   (void)NG;
@@ -170,10 +173,10 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   // odd).  Rows at or past M lie beyond the buffer range (M*K*2 bytes) and
   // read as zero.
   const uint32_t a_voff0 =
-      ((uint32_t)(lane >> 3) * (uint32_t)K + (uint32_t)((lane & 7) ^ (lane >> 4)) * 8u) * 2u;
+      ((uint32_t)(lane >> 3) * (uint32_t)ldx + (uint32_t)((lane & 7) ^ (lane >> 4)) * 8u) * 2u;
   const uint32_t a_voff1 =
-      ((uint32_t)(lane >> 3) * (uint32_t)K + (uint32_t)((lane & 7) ^ (lane >> 4) ^ 4) * 8u) * 2u;
-  const uint32_t a_row0 = (uint32_t)(m0 + kRPW * wave) * (uint32_t)K * 2u;
+      ((uint32_t)(lane >> 3) * (uint32_t)ldx + (uint32_t)((lane & 7) ^ (lane >> 4) ^ 4) * 8u) * 2u;
+  const uint32_t a_row0 = (uint32_t)(m0 + kRPW * wave) * (uint32_t)ldx * 2u;
   // A fragment of m-tile i, half-step h: row 16i + l16, octet oct + 4h
   const int a_frag0 = l16 * 8 + ((oct) ^ ((l16 >> 1) & 7));
   const int a_frag1 = l16 * 8 + ((oct + 4) ^ ((l16 >> 1) & 7));
@@ -208,7 +211,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
     for (int j = 0; j < kAL; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rx, (lds_void*)(a + 64 * j), 16, ((kRPW / 8 * wave + j) & 1) ? a_voff1 : a_voff0,
-          uniform((kt < KT ? a_row0 + (uint32_t)(8 * j) * (uint32_t)K * 2u + kb : kOobOffset)), 0,
+          uniform((kt < KT ? a_row0 + (uint32_t)(8 * j) * (uint32_t)ldx * 2u + kb : kOobOffset)), 0,
           0);
   };
   auto stream_w = [&](auto sc, int kt) {
@@ -397,7 +400,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
           o.z = o.z + bv[2];
           o.w = o.w + bv[3];
         }
-        *reinterpret_cast<f16x4*>(Y + (size_t)row * N + ncol) = o;
+        *reinterpret_cast<f16x4*>(Y + (size_t)row * ldy + ncol) = o;
       }
     }
   }
@@ -428,10 +431,11 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
-                     nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : KT);
+                     nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : KT, a.ldx,
+                     a.ldy);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
-  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, nsplit, st);
+  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
 }
 
 }  // namespace

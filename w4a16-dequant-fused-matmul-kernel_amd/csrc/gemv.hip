@@ -50,8 +50,8 @@ template <int MT, int CWL, int WAVES, bool STAGE>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
-    float* __restrict__ part, int N, int K, uint32_t gmagic, int gshift, int rows_per_wg, int S,
-    int nblk) {
+    float* __restrict__ part, int N, int K, int ldx, int ldy, uint32_t gmagic, int gshift,
+    int rows_per_wg, int S, int nblk) {
   constexpr int kThreads = GemvShape<WAVES>::kThreads;
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
@@ -76,7 +76,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   const int nb = (int)gridDim.x;
   if constexpr (CWL <= 4)
     asm volatile("" ::"s"(X), "s"(QW), "s"(SC), "s"(ZR), "s"(bias), "s"(Y), "s"(part), "s"(N),
-                 "s"(K), "s"(gmagic), "s"(gshift), "s"(rows_per_wg), "s"(S), "s"(nblk), "s"(nb));
+                 "s"(K), "s"(ldx), "s"(ldy), "s"(gmagic), "s"(gshift), "s"(rows_per_wg), "s"(S),
+                 "s"(nblk), "s"(nb));
 
   // XCD-aware block order (see header comment).
   int lin = (int)blockIdx.x;
@@ -103,7 +104,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   const int rb = sk * rows_per_wg;
   const int re = min(KP, rb + rows_per_wg);
   const MagicRegs mg = make_magic();
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, (uint32_t)MT * (uint32_t)K * 2u);
+  // rows of X lie ldx elements apart; the range ends after row MT - 1's K
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(MT - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 #pragma unroll
         for (int u = 0; u < BR; ++u)
           b.x[m * BR + u] = buf_load16(
-              rx, r0 < le ? ((uint32_t)m * (uint32_t)K + (uint32_t)r0 * 8u) * 2u : kOobOffset,
+              rx, r0 < le ? ((uint32_t)m * (uint32_t)ldx + (uint32_t)r0 * 8u) * 2u : kOobOffset,
               uniform((uint32_t)u * 16u));
     }
     // One path for full and partial batches (a lane-dependent branch here would
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         const int idx = tid + i * kThreads;
         const int m = idx / CHUNK, r = idx % CHUNK;
         const uint32_t off = (m < MT && r < nr)
-                                 ? ((uint32_t)m * (uint32_t)K + (uint32_t)(c0 + r) * 8u) * 2u
+                                 ? ((uint32_t)m * (uint32_t)ldx + (uint32_t)(c0 + r) * 8u) * 2u
                                  : kOobOffset;
         xv[i] = buf_load16(rx, off, 0u);
       }
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       for (int m = 0; m < MT; ++m) {
         f16 y = f32_to_f16(v[m]);
         if (bias) y = y + b;
-        Y[(size_t)m * N + col] = y;
+        Y[(size_t)m * ldy + col] = y;
       }
     }
     return;
@@ -347,10 +350,11 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
                      dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), part, a.N, a.K, gd.magic, gd.shift, rows, split, nblk);
+                     static_cast<f16*>(a.y), part, a.N, a.K, a.ldx, a.ldy, gd.magic, gd.shift, rows,
+                     split, nblk);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
-  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, split, st);
+  return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, split, st);
 }
 
 template <int MT, int WAVES, bool STAGE>

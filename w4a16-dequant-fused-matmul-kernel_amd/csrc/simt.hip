@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256) void simt_kernel(const f16* __restrict__ X,
                                                    const f16* __restrict__ ZR,
                                                    const f16* __restrict__ bias,
                                                    f16* __restrict__ Y, int M, int N, int K,
-                                                   int G) {
+                                                   int G, int ldx, int ldy) {
   const int n = blockIdx.x * 64 + (threadIdx.x & 63);
   const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (n >= N || m >= M) return;
@@ -30,11 +30,11 @@ __global__ __launch_bounds__(256) void simt_kernel(const f16* __restrict__ X,
     const f16 s = SC[(size_t)g * N + n];
     const f16 z = ZR[(size_t)g * N + n];
     const f16 wd = ((f16)(float)q - z) * s;
-    acc = __builtin_fmaf((float)X[(size_t)m * K + k], (float)wd, acc);
+    acc = __builtin_fmaf((float)X[(size_t)m * ldx + k], (float)wd, acc);
   }
   f16 y = f32_to_f16(acc);
   if (bias) y = y + bias[n];
-  Y[(size_t)m * N + n] = y;
+  Y[(size_t)m * ldy + n] = y;
 }
 
 }  // namespace
@@ -44,7 +44,7 @@ hipError_t launch_simt(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(simt_kernel, grid, dim3(256), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const f16*>(a.sc),
                      static_cast<const f16*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G);
+                     static_cast<f16*>(a.y), a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
 

@@ -10,14 +10,22 @@ namespace w4a16 {
 
 // One W4A16 GEMM call: Y[M,N] = X[M,K] @ dequant(qweight, scales, zeros) (+ bias).
 struct GemmArgs {
-  const void* x;        // fp16 [M, K]
+  const void* x;        // fp16 [M, K], rows ldx elements apart
   const int32_t* qw;    // int32 [K/8, N]
   const void* sc;       // fp16 [K/G, N]
   const void* zr;       // fp16 [K/G, N]
   const void* bias;     // fp16 [N] or nullptr
-  void* y;              // fp16 [M, N]
+  void* y;              // fp16 [M, N], rows ldy elements apart
   int M, N, K, G;
+  int ldx, ldy;         // row strides (>= K, >= N); the vector kernels need
+                        // ldx % 8 == 0 and ldy % 4 == 0 (16- / 8-byte rows)
 };
+
+// Bytes from the first element of x to one past its last: (M - 1) ldx + K
+// elements (0 for an empty x).
+inline uint64_t x_extent_bytes(const GemmArgs& a) {
+  return a.M > 0 && a.K > 0 ? ((uint64_t)(a.M - 1) * (uint64_t)a.ldx + (uint64_t)a.K) * 2u : 0;
+}
 
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
 // consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
@@ -57,8 +65,8 @@ hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
 // Split-K epilogue shared by the GEMV and the prefill kernels: y[M, N] =
 // fp16(sum of the S fp32 partials [S][M][N], in split order) (+ fp16 bias).
 // N % 4 == 0.
-hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int S,
-                                hipStream_t st);
+hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int ldy,
+                                int S, hipStream_t st);
 // Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256, cfg 8: 256 x 128):
 // needs K % 64 == 0.
 bool occ2_gemm_applicable(int M, int N, int K, int G);

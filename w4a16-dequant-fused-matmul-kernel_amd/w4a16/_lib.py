@@ -71,6 +71,11 @@ SIGNATURES = {
         _int,
         [ctypes.POINTER(Plan), _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
     ),
+    "w4a16_gemm_f16_strided": (
+        _int,
+        [ctypes.POINTER(Plan), _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+         _vp, _sz, _vp],
+    ),
     "w4a16_quantize_pack_f16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "w4a16_quantize_pack_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "w4a16_pack_int4": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
@@ -99,7 +104,11 @@ def load() -> ctypes.CDLL:
         except OSError as e:
             raise ImportError(f"cannot load {LIB_PATH}: {e}") from e
         for name, (res, args) in SIGNATURES.items():
-            fn = getattr(lib, name)
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as e:
+                raise ImportError(f"{LIB_PATH} lacks {name} (built from older sources); "
+                                  "rebuild it") from e
             fn.restype = res
             fn.argtypes = args
         ver = lib.w4a16_abi_version()

@@ -7,13 +7,18 @@ kernel is chosen inside ``libw4a16.so`` by shape:
 
 * M <= 8: decode GEMV -- VALU v_dot2_f32_f16, no MFMA, column blocks wide
   enough to give every CU a workgroup, split-K only when N is too narrow;
-* 9 <= M <= 64: skinny GEMM on v_mfma_f32_16x16x32_f16, 16 columns per
-  workgroup over the whole of K;
-* M > 64: prefill GEMM on MFMA, tile configuration by shape (two waves per
-  SIMD with 128 x 256 tiles for large M);
+* 3 <= M <= 64 on small weights: skinny GEMM on v_mfma_f32_16x16x32_f16, 16
+  columns per workgroup over the whole of K;
+* 4 <= M <= 64 on larger weights, and M > 64: the streamed prefill GEMM on
+  MFMA (32-, 64- or 128-row tiles, split along K where the tiles are few);
 * shapes the vector kernels do not take (N % 4 != 0 beyond the skinny range,
   G % 32 != 0, misaligned views, operands >= 2 GiB): the sequential-k SIMT
   kernel.
+
+Row-strided views (inner stride 1, row stride >= the row length) are accepted
+for ``x`` and ``out``: the reference's kernel takes strides (:71-75) though its
+wrapper asserts contiguity (:170-173); any other layout raises the same
+``AssertionError`` as the reference.
 
 Group size: the reference's Triton path needs every autotune BLOCK_K to divide
 G (:177-182), i.e. G % 64 == 0.  These kernels need G % 32 == 0, so G = 32 works
@@ -51,7 +56,7 @@ def _check_operands(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor, g
     num_groups = K // group_size
     assert scales.shape == (num_groups, N), f"scales shape {tuple(scales.shape)} != {(num_groups, N)}"
     assert zeros.shape == (num_groups, N), f"zeros shape {tuple(zeros.shape)} != {(num_groups, N)}"
-    assert x.is_contiguous(), "x must be contiguous"
+    assert _rows_ok(x), "x must be contiguous"
     assert qweight.is_contiguous(), "qweight must be contiguous"
     assert scales.is_contiguous(), "scales must be contiguous"
     assert zeros.is_contiguous(), "zeros must be contiguous"
@@ -63,6 +68,17 @@ def _check_operands(x: Tensor, qweight: Tensor, scales: Tensor, zeros: Tensor, g
     return M, K, N
 
 
+def _rows_ok(t: Tensor) -> bool:
+    """Contiguous, or row-major with unit inner stride and rows >= a row apart."""
+    return t.is_contiguous() or (t.dim() == 2 and t.stride(1) == 1
+                                 and t.stride(0) >= t.shape[1])
+
+
+def _row_stride(t: Tensor) -> int:
+    # a single row's stride is arbitrary (torch calls such a view contiguous)
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
 def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | None"):
     dev = x.device
     with rt.on_device(dev):
@@ -72,7 +88,14 @@ def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | N
             ws_bytes = int(plan.workspace_bytes)
         ws = rt.workspace(dev, ws_bytes)
         stream = rt.stream_ptr(dev)
-        if plan is None:
+        ldx, ldy = _row_stride(x), _row_stride(y)
+        if ldx != K or ldy != N:
+            code = rt.lib().w4a16_gemm_f16_strided(
+                None if plan is None else ctypes.byref(plan), x.data_ptr(), ldx,
+                qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), rt.ptr(bias),
+                y.data_ptr(), ldy, M, N, K, G, rt.ptr(ws), 0 if ws is None else ws.numel(),
+                stream)
+        elif plan is None:
             code = rt.lib().w4a16_linear_f16(
                 x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
                 rt.ptr(bias), y.data_ptr(), M, N, K, G, rt.ptr(ws),
@@ -89,7 +112,7 @@ def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | N
 def _output(x: Tensor, M: int, N: int, out: Tensor | None) -> Tensor:
     if out is None:
         return torch.empty((M, N), device=x.device, dtype=torch.float16)
-    assert out.shape == (M, N) and out.dtype == torch.float16 and out.is_contiguous()
+    assert out.shape == (M, N) and out.dtype == torch.float16 and _rows_ok(out)
     assert out.device == x.device, "out must be on the same device as x"
     return out
 
@@ -105,11 +128,11 @@ def w4a16_matmul(
     """Fused W4A16 GEMM: ``Y = X @ dequant(qweight)`` (triton_kernel.py:131-200).
 
     Args:
-        x: activations [M, K] fp16, contiguous, on a HIP device.
+        x: activations [M, K] fp16, contiguous or row-strided, on a HIP device.
         qweight: int32 [K//8, N], contiguous.
         scales, zeros: fp16 [K//G, N], contiguous.
         group_size: G, with G | K, 8 | K and G % 32 == 0.
-        out: optional preallocated fp16 [M, N] output.
+        out: optional preallocated fp16 [M, N] output (contiguous or row-strided).
     Returns:
         fp16 [M, N], fp32-accumulated.
     """
