@@ -26,7 +26,8 @@
 //     LDS-direct loads three steps ahead (each wave streams and reads back only
 //     its own columns: no barrier); each stage is its own LDS array, so the
 //     compiler's vmcnt wait before a stage's reads covers exactly the loads into
-//     that stage.  One load per half-step brings the scales and zeros of the
+//     that stage.  One load per half-step (per step when G % 64 == 0: both
+//     halves then share a group) brings the scales and zeros of the
 //     wave's 64 columns, laid out per 4-column quad as (scales 0-1, scales 2-3,
 //     zeros 0-1, zeros 2-3), so a lane reads its column constants with one
 //     ds_read_b128; the load addresses both tensors through one buffer
@@ -101,7 +102,9 @@ __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t 
   }
 }
 
-template <int kMT>
+// kSZ1: G % 64 == 0, so both half-steps of a step lie in one group and one
+// scale / zero load per step serves both (else one per half-step).
+template <int kMT, bool kSZ1>
 __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
@@ -225,7 +228,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
           uniform(in ? ((uint32_t)kt * 8u + 4u * (uint32_t)h) * (uint32_t)N * 4u : kOobOffset), 0,
           0);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < (kSZ1 ? 1 : 2); ++h) {
       const uint32_t g = (uint32_t)((kt * kBK + 32 * h) / G);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rq, (lds_void*)(q + 16 * h), 4, q_off, uniform(in ? g * (uint32_t)N * 2u : kOobOffset),
@@ -250,7 +253,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   asm("" : "+v"(q_i[1]));
   auto read_in = [&](auto sc, int h, In& in) {
     in.w = wq(sc)[wave * 128 + 64 * h + lane_i];
-    const uint4 c = sz(sc)[q_i[h]];
+    const uint4 c = sz(sc)[q_i[kSZ1 ? 0 : h]];
     in.s = make_uint2(c.x, c.y);
     in.z = make_uint2(c.z, c.w);
   };
@@ -332,9 +335,13 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
     read_in(s1, 1, in1);
     interleave();
     __builtin_amdgcn_sched_barrier(0);
-    // this wave's part of step kt+1's activations: only the four weight
-    // loads issued after it may still be in flight
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    // this wave's part of step kt+1's activations: only the weight and
+    // scale / zero loads issued after it (4, or 3 with kSZ1) may still be in
+    // flight
+    if constexpr (kSZ1)
+      asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     tile_barrier();
   };
 
@@ -412,8 +419,8 @@ int split_steps(int K, int split) {
   return ((KT + split - 1) / split + kStages - 1) / kStages * kStages;
 }
 
-template <int kMT>
-hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
+template <int kMT, bool kSZ1>
+hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t st) {
   constexpr int kBM = 16 * kMT;
   const int tiles = ((a.N + kBN - 1) / kBN) * ((a.M + kBM - 1) / kBM);
   const int KT = a.K / kBK;
@@ -427,7 +434,7 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
   const char* base = sc < zr ? sc : zr;
   const uint32_t sz_bytes = (uint32_t)((sc < zr ? zr : sc) - base) +
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
-  hipLaunchKernelGGL(stream_kernel<kMT>, dim3(tiles * nsplit), dim3(kNT), 0, st,
+  hipLaunchKernelGGL((stream_kernel<kMT, kSZ1>), dim3(tiles * nsplit), dim3(kNT), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
@@ -436,6 +443,12 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
+}
+
+template <int kMT>
+hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
+  return a.G % (2 * 32) == 0 ? launch_kernel<kMT, true>(a, split, part, st)
+                             : launch_kernel<kMT, false>(a, split, part, st);
 }
 
 }  // namespace
