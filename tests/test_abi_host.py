@@ -159,6 +159,29 @@ def test_strided_entry_validates_row_strides(lib):
                                       NULL, 0, NULL) == 0
 
 
+def test_group_reciprocal_division_is_exact():
+    """The kernels find the quantisation group of row k as
+    (umulhi(k, magic) + k) >> shift, with shift = ceil(log2 G) and
+    magic = floor(2^32 (2^shift - G) / G) + 1 (group_div in csrc/w4a16_launch.h).
+    Checked against integer division for every G up to 4096 and for large G,
+    at multiples of G +- 1 near 0 and near 2^31 and at random k < 2^31."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    rand = rng.integers(0, 2**31, size=2000, dtype=np.uint64)
+    for G in list(range(1, 4097)) + [8192, 14336, 28672, 1 << 20, 3 << 20, (1 << 31) - 1]:
+        shift = (G - 1).bit_length()
+        magic = ((1 << 32) * ((1 << shift) - G)) // G + 1
+        assert 1 <= magic < 2**32
+        mult = np.arange(0, 64, dtype=np.uint64) * np.uint64(G)
+        top = np.uint64(((2**31 - 1) // G) * G) - np.arange(0, 64, dtype=np.uint64) * np.uint64(G)
+        k = np.concatenate([mult, mult + 1, mult - 1, top, top + 1, top - 1, rand,
+                            np.array([0, 1, 2**31 - 1], dtype=np.uint64)])
+        k = k[k < 2**31]
+        q = (((k * np.uint64(magic)) >> np.uint64(32)) + k) >> np.uint64(shift)
+        assert np.array_equal(q, k // np.uint64(G)), G
+
+
 def test_quant_entry_points_reject_bad_args(lib):
     a = ctypes.c_void_p(1 << 12)
     assert lib.w4a16_quantize_pack_f16(a, a, a, a, 100, 16, 64, a, NULL) == -2

@@ -110,7 +110,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
                    uint32_t sz_bytes, const f16* __restrict__ bias, f16* __restrict__ Y,
                    float* __restrict__ part, int M, int N, int K, int G, int KTS, int ldx,
-                   int ldy) {
+                   int ldy, uint32_t gmagic, int gshift) {
   static_assert(kStages == 4, "stage arrays below are written out for four stages");
   static_assert(kMT == 2 || kMT == 4 || kMT == 8, "8-row activation loads per wave");
   constexpr int kBM = 16 * kMT;          // rows per workgroup tile
@@ -229,7 +229,7 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
           0);
 #pragma unroll
     for (int h = 0; h < (kSZ1 ? 1 : 2); ++h) {
-      const uint32_t g = (uint32_t)((kt * kBK + 32 * h) / G);
+      const uint32_t g = div_group((uint32_t)(kt * kBK + 32 * h), gmagic, gshift);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rq, (lds_void*)(q + 16 * h), 4, q_off, uniform(in ? g * (uint32_t)N * 2u : kOobOffset),
           0, 0);
@@ -434,12 +434,13 @@ hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t 
   const char* base = sc < zr ? sc : zr;
   const uint32_t sz_bytes = (uint32_t)((sc < zr ? zr : sc) - base) +
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
+  const GroupDiv gd = group_div(a.G);
   hipLaunchKernelGGL((stream_kernel<kMT, kSZ1>), dim3(tiles * nsplit), dim3(kNT), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
                      nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : KT, a.ldx,
-                     a.ldy);
+                     a.ldy, gd.magic, gd.shift);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);

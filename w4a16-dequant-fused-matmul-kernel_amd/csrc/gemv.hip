@@ -327,18 +327,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   }
 }
 
-// Reciprocal form of k / G for the kernel (see group_of).
-struct GroupDiv {
-  uint32_t magic;
-  int shift;
-};
-GroupDiv group_div(int G) {
-  int l = 0;
-  while ((1ll << l) < (long long)G) ++l;
-  const uint64_t m = ((1ull << 32) * (uint64_t)((1ll << l) - G)) / (uint64_t)G + 1;
-  return GroupDiv{(uint32_t)m, l};
-}
-
 template <int MT, int CWL, int WAVES, bool STAGE>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;

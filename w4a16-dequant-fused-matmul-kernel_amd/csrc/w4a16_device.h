@@ -167,6 +167,11 @@ __device__ __forceinline__ float fold_rows4(float v0, float v1, float v2, float 
   return s01 + s23;
 }
 
+// k / G for 0 <= k < 2^31 from the host's group_div(G) constants.
+__device__ __forceinline__ uint32_t div_group(uint32_t k, uint32_t magic, int shift) {
+  return (__umulhi(k, magic) + k) >> shift;
+}
+
 __device__ __forceinline__ f16 f32_to_f16(float x) { return (f16)x; }  // v_cvt_f16_f32, RNE
 
 // Buffer resource over [p, p + bytes): raw buffer loads outside the range return

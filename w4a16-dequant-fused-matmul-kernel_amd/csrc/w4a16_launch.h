@@ -9,6 +9,20 @@
 namespace w4a16 {
 
 // One W4A16 GEMM call: Y[M,N] = X[M,K] @ dequant(qweight, scales, zeros) (+ bias).
+// k / G without a division in the kernels: (umulhi(k, magic) + k) >> shift
+// with shift = ceil(log2 G) and magic = floor(2^32 (2^shift - G) / G) + 1,
+// exact for 0 <= k < 2^31 (magic = 1 for a power of two).
+struct GroupDiv {
+  uint32_t magic;
+  int shift;
+};
+inline GroupDiv group_div(int G) {
+  int l = 0;
+  while ((1ll << l) < (long long)G) ++l;
+  const uint64_t m = ((1ull << 32) * (uint64_t)((1ll << l) - G)) / (uint64_t)G + 1;
+  return GroupDiv{(uint32_t)m, l};
+}
+
 struct GemmArgs {
   const void* x;        // fp16 [M, K], rows ldx elements apart
   const int32_t* qw;    // int32 [K/8, N]
