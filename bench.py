@@ -251,7 +251,8 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(this build targets a single MI355X; see DESIGN.md for the sharding design)",
+              "(this build targets a single MI355X: columns would shard with no "
+              "communication, rows with one all-reduce of fp32 partial Y)",
               file=sys.stderr)
         return 2
     import torch

@@ -99,7 +99,8 @@ def test_quantize_spec_example():
     q = O.unpack_int4(qw)[:, 0]
     assert q[:4].tolist() == [8, 0, 15, 4]
     assert float(z[0, 0]) == 6.0
-    # scale = (0.5 - (-0.3)) / 15 with fp16 inputs (survey Appendix A: fp16 0x2ad4)
+    # scale = (0.5 - (-0.3)) / 15 from the fp16 inputs of the worked example
+    # (W4A16_SPEC.md:84-100): fp32(fp16(0.5) - fp16(-0.3)) / 15 rounds to fp16 0x2ad4
     assert int(s.view(np.uint16)[0, 0]) == 0x2AD4
     dq = O.dequantize_weight(qw, s, z, 4)[:4, 0].astype(np.float64)
     np.testing.assert_allclose(dq, [0.1067, -0.3200, 0.4800, -0.1067], atol=5e-4)
