@@ -5,9 +5,10 @@ Drop-in for the reference's primary backend ``w4a16_matmul``
 preconditions raised as ``AssertionError`` (:153-187), optional ``out``.  The
 kernel is chosen inside ``libw4a16.so`` by shape:
 
-* M <= 8: decode GEMV -- VALU v_dot2_f32_f16, no MFMA, column blocks wide
-  enough to give every CU a workgroup, split-K only when N is too narrow;
-* 3 <= M <= 64 on small weights: skinny GEMM on v_mfma_f32_16x16x32_f16, 16
+* M <= 2 (M <= 4 on weights wider than 16384 columns): decode GEMV -- VALU
+  v_dot2_f32_f16, no MFMA, column blocks wide enough to give every CU a
+  workgroup, split-K only when N is too narrow;
+* other M <= 64 on small weights: skinny GEMM on v_mfma_f32_16x16x32_f16, 16
   columns per workgroup over the whole of K;
 * 4 <= M <= 64 on larger weights, and M > 64: the streamed prefill GEMM on
   MFMA (32-, 64- or 128-row tiles, split along K where the tiles are few);
