@@ -224,6 +224,8 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     p = _lib.plan(M, N, K, G)
     assert _lib.KERNEL_NAMES[p.kernel] == kernel
     assert p.grid_x >= 1 and p.grid_y >= 1
+    if kernel == "skinny":
+        assert p.tile_cfg == 0   # 4 waves per workgroup (measured no slower anywhere)
 
 
 def test_planner_gemv_split_rule():

@@ -282,10 +282,12 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->tile_n = 16;
       p->grid_x = (N + 15) / 16;
       p->grid_y = 1;
-      // 8 waves per workgroup up to one column block per CU, for M <= 16 up
-      // to two (measured at M = 4 / 8, N = 6144: 9.7 / 10.8 vs 10.9 / 11.4
-      // us; at M = 32, N = 6144 the 4-wave form is faster, 20.9 vs 23.4 us)
-      p->tile_cfg = (M <= 32 && (p->grid_x <= cus || (M <= 16 && p->grid_x <= 2 * cus))) ? 1 : 0;
+      // 4 waves per workgroup: with the branch-free batch loop the 8-wave
+      // form is nowhere faster (measured on MI355X, 4 vs 8 waves: M = 3 / 8 /
+      // 16, K = 4096, N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us;
+      // M = 8 / 16, K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32,
+      // K = N = 4096: 11.5 vs 12.1; M = 8, K = 8192, N = 1024: 9.6 vs 9.9)
+      p->tile_cfg = 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
