@@ -212,6 +212,11 @@ def test_quant_entry_points_reject_bad_args(lib):
     (65, 4096, 4096, 128, "mfma"),
     (4096, 14336, 4096, 128, "mfma"),
     (16, 4096, 4096, 32, "skinny"),
+    (32, 6144, 4096, 128, "skinny"),  # 32-column blocks beat the streamed tiles to N = 8192
+    (16, 14336, 4096, 128, "skinny"),  # ... and to N = 16384 for M <= 16
+    (32, 14336, 4096, 128, "mfma"),
+    (16, 28672, 4096, 128, "mfma"),
+    (4, 8192, 28672, 128, "skinny"),   # long K: whole K per workgroup
     (16, 4098, 4096, 32, "skinny"),   # any N
     (1, 4098, 4096, 128, "skinny"),   # N % 4 != 0: the 16-column kernel takes any N
     (1, 4098, 4096, 16, "simt"),      # ... but needs G % 32 == 0
@@ -225,7 +230,11 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     assert _lib.KERNEL_NAMES[p.kernel] == kernel
     assert p.grid_x >= 1 and p.grid_y >= 1
     if kernel == "skinny":
-        assert p.tile_cfg == 0   # 4 waves per workgroup (measured no slower anywhere)
+        # 32-column blocks (cfg 2) where 16-column ones outnumber the CUs (256
+        # on MI355X, also the library's value without a device), M <= 32 and N
+        # even; else 16-column blocks with 4 waves
+        wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
+        assert (p.tile_cfg, p.tile_n) == ((2, 32) if wide else (0, 16)), (M, N)
 
 
 def test_planner_gemv_split_rule():
@@ -295,14 +304,15 @@ def test_planner_gemv_blocks_and_waves():
 
 
 def test_planner_small_batch_wide_weights_stream():
-    """4 <= M <= 64 on large enough weights takes the streamed prefill kernel
-    with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K for
-    about 448 workgroups with >= 8 k-steps per split; narrow N or small weights
-    stay on the skinny kernel (or the GEMV for M <= 3)."""
+    """4 <= M <= 64 on large enough, wide weights takes the streamed prefill
+    kernel with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K
+    for about 448 workgroups with >= 8 k-steps per split; narrow N, small
+    weights, or N <= 8192 (16384 for M <= 16) with M <= 32 stay on the skinny
+    kernel (or the GEMV for M <= 3)."""
     from w4a16 import _lib
 
     for M, N, K, cfg, s in ((16, 28672, 4096, 12, 4), (32, 28672, 4096, 12, 4),
-                            (16, 8192, 28672, 12, 14), (8, 28672, 8192, 12, 4),
+                            (8, 28672, 8192, 12, 4),
                             (32, 4096, 14336, 12, 28), (64, 28672, 8192, 13, 4),
                             (48, 14336, 4096, 13, 8), (64, 4096, 4096, 13, 8)):
         p = _lib.plan(M, N, K, 128)
@@ -314,6 +324,16 @@ def test_planner_small_batch_wide_weights_stream():
     for M, N, K in ((16, 4096, 4096), (16, 4096, 14336), (24, 4096, 4096), (16, 6144, 4096),
                     (9, 8192, 8192), (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
+    # up to N = 8192 (N = 16384 for M <= 16) the skinny kernel's 32-column
+    # blocks beat the streamed tiles, long K included
+    for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (32, 6144, 4096), (12, 14336, 4096)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (2, 32), (M, N, K)
+        assert p.grid_x == N // 32
+    # ... measured with G = 128; smaller groups keep the streamed tiles
+    for G in (32, 64):
+        p = _lib.plan(16, 8192, 28672, G)
+        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 12, G
 
 
 def test_planner_prefill_split_k():

@@ -207,17 +207,18 @@ def test_mfma_split_k(M, K, N, G):
 @pytest.mark.parametrize("M,K,N,G", [
     (9, 96, 260, 32), (16, 4096, 4096, 128), (17, 160, 7, 32), (32, 11008, 1028, 64),
     (33, 1024, 130, 32), (48, 4096, 516, 128), (64, 4096, 4100, 64), (1, 4096, 1000, 128),
-    (5, 320, 33, 32),
+    (5, 320, 33, 32), (24, 2048, 6150, 64), (4, 4096, 8194, 128),
 ])
 def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
-    with 4 and (M <= 32) 8 waves per workgroup."""
+    with 4 and (M <= 32) 8 waves per workgroup, and (M <= 32, N even) 32-column
+    blocks with two columns per lane."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in ((0, 1) if M <= 32 else (0,)):      # 4 or 8 waves per workgroup
+    for cfg in ((0, 1) + ((2,) if N % 2 == 0 else ()) if M <= 32 else (0,)):
         log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg}")
         p = plan_for(M, N, K, G, "skinny")
         p.tile_cfg = cfg

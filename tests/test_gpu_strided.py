@@ -80,13 +80,13 @@ def test_gemv_strided(M, N):
                             what=f"gemv cfg={cfg} cols={cols} split={split}")
 
 
-@pytest.mark.parametrize("M,N", [(16, 1030), (33, 2048), (64, 516)])
+@pytest.mark.parametrize("M,N", [(16, 1030), (33, 2048), (64, 516), (8, 4100)])
 def test_skinny_strided(M, N):
     from w4a16.hip_kernel import plan_for
 
     K, G = 2048, 64
     X, qw, s, z = _case(M, K, N, G, seed=M + 1)
-    for cfg in (0, 1) if M <= 32 else (0,):
+    for cfg in (0, 1, 2) if M <= 32 else (0,):
         p = plan_for(M, N, K, G, "skinny", 0)
         p.tile_cfg = cfg
         log(f"skinny strided M={M} N={N} cfg={cfg}")

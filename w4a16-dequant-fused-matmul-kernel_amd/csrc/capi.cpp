@@ -166,6 +166,28 @@ bool small_m_takes_stream(int64_t M, int64_t N, int64_t K, int64_t G) {
   return (N >= 14336 && mb >= 24) || mb >= 64;
 }
 
+// The skinny kernel's 32-column blocks (two columns per lane, N even, M <= 32)
+// where 16-column blocks would put two on some CUs: one activation stream and
+// 8-byte weight loads per 32 columns (measured on MI355X against 16-column
+// blocks, K = 4096, N = 6144: M = 4 / 8 / 16 / 32 8.3 / 8.5 / 9.4 / 13.0 vs
+// 9.2 / 10.1 / 12.4 / 19.1 us; at N = 4096, 128 blocks for 256 CUs, slower:
+// M = 4 8.2 vs 6.4).
+bool skinny_wide(int64_t M, int64_t N, int cus) {
+  return M <= 32 && N % 2 == 0 && (N + 15) / 16 > cus;
+}
+
+// ... and it beats the streamed small-M tiles up to N = 8192, and to N = 16384
+// for M <= 16 (measured on MI355X: M = 24, K = 4096, N = 6144: 11.9 vs 14.6
+// us; M = 4, K = 28672, N = 8192: 34.1 vs 38.9; M = 12, K = 4096, N = 14336:
+// 15.3 vs 17.2), not on wider weights, whose 256-column streamed tiles share
+// the activations (M = 16, K = 4096, N = 28672: 27.8 vs 23.8; M = 32,
+// N = 14336: 22.6 vs 19.6).  Measured with G = 128; smaller groups add
+// scale / zero loads to every skinny k-step and lose (M = 16, K = 28672,
+// N = 8192: G = 32 55.1 vs 48.6 us, G = 64 48.1 vs 46.1; G = 128 a tie).
+bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t G, int cus) {
+  return skinny_wide(M, N, cus) && G % 128 == 0 && (N <= 8192 || (N <= 16384 && M <= 16));
+}
+
 // k-splits for the streamed kernel on few tiles: about 448 workgroups (two
 // per CU at most), at least 8 k-steps per split.
 int stream_split_for(int64_t tiles, int64_t K) {
@@ -222,7 +244,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
-    else if (small_m_takes_stream(M, N, K, G))
+    else if (small_m_takes_stream(M, N, K, G) &&
+             !(skinny_applicable(M, G) && skinny_wide_beats_stream(M, N, G, cus)))
       kernel = W4A16_KERNEL_MFMA;
     else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G))
       kernel = W4A16_KERNEL_GEMV;
@@ -279,15 +302,16 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     case W4A16_KERNEL_SKINNY:
       if (!skinny_applicable(M, G)) return W4A16_ERR_BAD_PLAN;
       p->tile_m = (int32_t)((M + 15) / 16 * 16);
-      p->tile_n = 16;
-      p->grid_x = (N + 15) / 16;
+      p->tile_n = skinny_wide(M, N, cus) ? 32 : 16;
+      p->grid_x = (N + p->tile_n - 1) / p->tile_n;
       p->grid_y = 1;
-      // 4 waves per workgroup: with the branch-free batch loop the 8-wave
-      // form is nowhere faster (measured on MI355X, 4 vs 8 waves: M = 3 / 8 /
+      // 32-column blocks where they apply (cfg 2), else 16-column blocks
+      // with 4 waves per workgroup: with the branch-free batch loop the 8-wave
+      // form (cfg 1) is nowhere faster (measured on MI355X, 4 vs 8 waves: M = 3 / 8 /
       // 16, K = 4096, N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us;
       // M = 8 / 16, K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32,
       // K = N = 4096: 11.5 vs 12.1; M = 8, K = 8192, N = 1024: 9.6 vs 9.9)
-      p->tile_cfg = 0;
+      p->tile_cfg = p->tile_n == 32 ? 2 : 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
@@ -368,8 +392,8 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
       return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }
     case W4A16_KERNEL_SKINNY: {
-      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 1 ||
-          (p->tile_cfg == 1 && M > 32))
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 2 ||
+          (p->tile_cfg >= 1 && M > 32) || (p->tile_cfg == 2 && N % 2 != 0))
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 4) || !aligned(sc, 2) || !aligned(zr, 2))
         return W4A16_ERR_BAD_PLAN;

@@ -39,13 +39,18 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // GSTEP = k-steps per quantisation group inside an aligned 8-step batch (G/32
 // when that is 1, 2, 4 or 8; 8 for larger powers of two): scales and zeros are
 // loaded once per group.  GSTEP = 1 loads them every k-step (any G % 32 == 0).
-template <int MT, int GSTEP, int WAVES>
+// NT = columns per lane: 1 (16-column blocks) or 2 (32-column blocks, N even:
+// the lane's two adjacent columns come in one 8-byte word load and one 4-byte
+// scale / zero load each, and its activation fragment feeds both n-tiles, so a
+// CU streams X once for 32 columns instead of once per 16).
+template <int MT, int GSTEP, int WAVES, int NT>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
     int N, int K, int G, int nblk, int ldx, int ldy) {
+  static_assert(NT == 1 || NT == 2, "one or two columns per lane");
   constexpr int kWaves = WAVES;
-  __shared__ f32x4 red[kWaves][MT][64];
+  __shared__ f32x4 red[kWaves][MT][NT][64];
 
   const int nb = (int)gridDim.x;
   int lin = (int)blockIdx.x;
@@ -56,10 +61,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 15;       // column within the block
+  const int c = lane & 15;       // column (pair for NT = 2) within the block
   const int q = lane >> 4;       // octet within a 32-k step
-  const int col = cb * 16 + c;
-  const bool nv = col < N;
+  const int col = cb * (16 * NT) + NT * c;   // the lane's first column
+  const bool nv = col < N;                   // (N even for NT = 2: so is col + 1)
   const int KP = K >> 3;
   const int KS = K >> 5;         // 32-k steps
   const int NG = K / G;
@@ -89,8 +94,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   }
 
   struct Batch {
-    uint32_t w[kBatch];
-    uint32_t sz[kBatch];  // scale bits | zero bits << 16
+    uint32_t w[kBatch][NT];
+    uint32_t sz[kBatch][NT];  // scale bits | zero bits << 16
     uint4 x[kBatch][MT];
   };
   auto load_batch = [&](int s0, Batch& b) {
@@ -102,15 +107,34 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
       const bool in = ks < ke;
       {
         const uint32_t wk = uniform(in ? (uint32_t)ks * 4u * (uint32_t)N * 4u : kOobOffset);
-        b.w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
+        if constexpr (NT == 1) {
+          b.w[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
+        } else {
+          const uint2 w2 = buf_load8(rw, w_off, wk);
+          b.w[j][0] = w2.x;
+          b.w[j][1] = w2.y;
+        }
         if (j % GSTEP == 0) {
           const uint32_t gk =
               uniform(in ? (uint32_t)((ks * 32) / G) * (uint32_t)N * 2u : kOobOffset);
-          const uint32_t sv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
-          const uint32_t zv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
-          b.sz[j] = (sv & 0xFFFFu) | (zv << 16);
+          if constexpr (NT == 1) {
+            const uint32_t sv =
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
+            const uint32_t zv =
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
+            b.sz[j][0] = (sv & 0xFFFFu) | (zv << 16);
+          } else {
+            const uint32_t sv =
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off, (int)gk, 0);
+            const uint32_t zv =
+                (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rz, (int)s_off, (int)gk, 0);
+            b.sz[j][0] = (sv & 0xFFFFu) | (zv << 16);
+            b.sz[j][1] = (sv >> 16) | (zv & 0xFFFF0000u);
+          }
         } else {
-          b.sz[j] = b.sz[j - j % GSTEP];   // same group as the batch slot it copies
+#pragma unroll
+          for (int t = 0; t < NT; ++t)   // same group as the batch slot it copies
+            b.sz[j][t] = b.sz[j - j % GSTEP][t];
         }
         const uint32_t xk = uniform(in ? (uint32_t)ks * 64u : kOobOffset);
 #pragma unroll
@@ -119,23 +143,28 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     }
   };
 
-  f32x4 acc[MT];
+  f32x4 acc[MT][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{};
 
   auto process = [&](const Batch& b, int s0) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       if (s0 + j >= ke) break;   // wave-uniform
-      const ColQ cq = make_colq(b.sz[j] & 0xFFFFu, b.sz[j] >> 16);
-      f16x2 d[4];
-      dq_word_fast(b.w[j], cq, mg, d);
-      // natural k order: w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
-      const f16x8 bf = f16x8{d[0].x, d[1].x, d[2].x, d[3].x, d[0].y, d[1].y, d[2].y, d[3].y};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b.x[j][mt]),
-                                                         bf, acc[mt], 0, 0, 0);
+      for (int t = 0; t < NT; ++t) {
+        const ColQ cq = make_colq(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
+        f16x2 d[4];
+        dq_word_fast(b.w[j][t], cq, mg, d);
+        // natural k order: w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
+        const f16x8 bf = f16x8{d[0].x, d[1].x, d[2].x, d[3].x, d[0].y, d[1].y, d[2].y, d[3].y};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(f16x8, b.x[j][mt]), bf, acc[mt][t], 0, 0, 0);
+      }
     }
   };
 
@@ -155,22 +184,27 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   }
 
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[wave][mt][t][lane] = acc[mt][t];
   __syncthreads();
   // wave w finishes m-tiles w, w+4, ...: sum the 4 waves in order, round, store
   for (int mt = wave; mt < MT; mt += kWaves) {
-    f32x4 v = red[0][mt][lane];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) v += red[w][mt][lane];
-    if (nv) {
-      const f16 bv = bias ? bias[col] : (f16)0.0f;
+    for (int t = 0; t < NT; ++t) {
+      f32x4 v = red[0][mt][t][lane];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = mt * 16 + 4 * q + r;
-        if (row < M) {
-          f16 y = f32_to_f16(v[r]);
-          if (bias) y = y + bv;
-          Y[(size_t)row * ldy + col] = y;
+      for (int w = 1; w < kWaves; ++w) v += red[w][mt][t][lane];
+      if (nv) {
+        const f16 bv = bias ? bias[col + t] : (f16)0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = mt * 16 + 4 * q + r;
+          if (row < M) {
+            f16 y = f32_to_f16(v[r]);
+            if (bias) y = y + bv;
+            Y[(size_t)row * ldy + col + t] = y;
+          }
         }
       }
     }
@@ -178,13 +212,25 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 }
 
 template <int MT, int GSTEP>
-hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
+hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
+  const bool eight_waves = cfg == 1;
+  if constexpr (MT <= 2) {
+    if (cfg == 2) {   // 32-column blocks
+      const int nblk2 = (a.N + 31) / 32;
+      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 2>), dim3(nblk2), dim3(256), 0, st,
+                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
+                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
+                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
+                         a.G, nblk2, a.ldx, a.ldy);
+      return hipGetLastError();
+    }
+  }
   const int nblk = (a.N + 15) / 16;
   // 8 waves (M <= 32 only, register budget): two per SIMD, twice the weight
   // loads in flight per CU -- pays when there is about one workgroup per CU
   if constexpr (MT <= 2) {
     if (eight_waves) {
-      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 8>), dim3(nblk), dim3(512), 0, st,
+      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 8, 1>), dim3(nblk), dim3(512), 0, st,
                          static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                          static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                          static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
@@ -192,7 +238,7 @@ hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4>), dim3(nblk), dim3(256), 0, st,
+  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 1>), dim3(nblk), dim3(256), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
@@ -201,28 +247,30 @@ hipError_t launch_g(const GemmArgs& a, bool eight_waves, hipStream_t st) {
 }
 
 template <int MT>
-hipError_t launch_mt(const GemmArgs& a, bool w8, hipStream_t st) {
+hipError_t launch_mt(const GemmArgs& a, int cfg, hipStream_t st) {
   // batch slots per group when group boundaries land on fixed slots of an
   // aligned 8-step (256-k) batch: G / 32 a power of two
   const int gs = a.G / 32;
-  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, w8, st);
+  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, cfg, st);
   switch (gs) {
-    case 4: return launch_g<MT, 4>(a, w8, st);
-    case 2: return launch_g<MT, 2>(a, w8, st);
-    default: return launch_g<MT, 1>(a, w8, st);
+    case 4: return launch_g<MT, 4>(a, cfg, st);
+    case 2: return launch_g<MT, 2>(a, cfg, st);
+    default: return launch_g<MT, 1>(a, cfg, st);
   }
 }
 
 }  // namespace
 
+// cfg 0: 4 waves, 16-column blocks; 1: 8 waves (M <= 32); 2: 4 waves,
+// 32-column blocks (M <= 32, N even)
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st) {
-  if (cfg == 1 && a.M > 32) return hipErrorInvalidValue;
-  const bool w8 = cfg == 1;
+  if (cfg < 0 || cfg > 2 || (cfg >= 1 && a.M > 32) || (cfg == 2 && a.N % 2 != 0))
+    return hipErrorInvalidValue;
   switch ((a.M + 15) / 16) {
-    case 1: return launch_mt<1>(a, w8, st);
-    case 2: return launch_mt<2>(a, w8, st);
-    case 3: return launch_mt<3>(a, w8, st);
-    case 4: return launch_mt<4>(a, w8, st);
+    case 1: return launch_mt<1>(a, cfg, st);
+    case 2: return launch_mt<2>(a, cfg, st);
+    case 3: return launch_mt<3>(a, cfg, st);
+    case 4: return launch_mt<4>(a, cfg, st);
     default: return hipErrorInvalidValue;
   }
 }
