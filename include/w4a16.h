@@ -64,7 +64,8 @@ typedef struct w4a16_plan {
                               activations staged in LDS (M <= 2; larger M
                               always stages them); SKINNY: 0 / 1 = 4 / 8 waves
                               on 16-column blocks (8 for M <= 32), 2 = 4 waves
-                              on 32-column blocks (M <= 32, N even)            */
+                              on 32-column blocks (M <= 32, N even), 3 = 4
+                              waves on 64-column blocks (M <= 16, N % 4 == 0) */
   int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup   */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */

@@ -201,11 +201,12 @@ def test_quant_entry_points_reject_bad_args(lib):
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
     (3, 28672, 4096, 128, "gemv"),   # wide N: the GEMV up to M = 3
-    (4, 28672, 4096, 128, "mfma"),   # ... from M = 4 the streamed small-M tiles
+    (4, 28672, 4096, 128, "skinny"),  # ... from M = 4 the skinny kernel's 64-column blocks
     (2, 6144, 4096, 128, "gemv"),
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
     (8, 4096, 4096, 128, "skinny"),
-    (5, 28672, 4096, 128, "mfma"),
+    (5, 28672, 4096, 128, "skinny"),
+    (5, 28672, 4096, 64, "mfma"),     # G = 64: the streamed small-M tiles
     (9, 4096, 4096, 128, "skinny"),
     (64, 4096, 11008, 64, "mfma"),
     (24, 4096, 4096, 128, "skinny"),  # 8 MiB of weights: skinny up to M = 32
@@ -215,7 +216,8 @@ def test_quant_entry_points_reject_bad_args(lib):
     (32, 6144, 4096, 128, "skinny"),  # 32-column blocks beat the streamed tiles to N = 8192
     (16, 14336, 4096, 128, "skinny"),  # ... and to N = 16384 for M <= 16
     (32, 14336, 4096, 128, "mfma"),
-    (16, 28672, 4096, 128, "mfma"),
+    (16, 28672, 4096, 128, "skinny"),
+    (24, 28672, 4096, 128, "mfma"),
     (4, 8192, 28672, 128, "skinny"),   # long K: whole K per workgroup
     (16, 4098, 4096, 32, "skinny"),   # any N
     (1, 4098, 4096, 128, "skinny"),   # N % 4 != 0: the 16-column kernel takes any N
@@ -233,8 +235,10 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
         # 32-column blocks (cfg 2) where 16-column ones outnumber the CUs (256
         # on MI355X, also the library's value without a device), M <= 32 and N
         # even; else 16-column blocks with 4 waves
+        quad = M <= 16 and N % 4 == 0 and G % 128 == 0 and (N + 63) // 64 > 128
         wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
-        assert (p.tile_cfg, p.tile_n) == ((2, 32) if wide else (0, 16)), (M, N)
+        want = (3, 64) if quad else (2, 32) if wide else (0, 16)
+        assert (p.tile_cfg, p.tile_n) == want, (M, N)
 
 
 def test_planner_gemv_split_rule():
@@ -311,8 +315,7 @@ def test_planner_small_batch_wide_weights_stream():
     kernel (or the GEMV for M <= 3)."""
     from w4a16 import _lib
 
-    for M, N, K, cfg, s in ((16, 28672, 4096, 12, 4), (32, 28672, 4096, 12, 4),
-                            (8, 28672, 8192, 12, 4),
+    for M, N, K, cfg, s in ((32, 28672, 4096, 12, 4), (24, 28672, 8192, 12, 4),
                             (32, 4096, 14336, 12, 28), (64, 28672, 8192, 13, 4),
                             (48, 14336, 4096, 13, 8), (64, 4096, 4096, 13, 8)):
         p = _lib.plan(M, N, K, 128)
@@ -326,10 +329,14 @@ def test_planner_small_batch_wide_weights_stream():
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
     # up to N = 8192 (N = 16384 for M <= 16) the skinny kernel's 32-column
     # blocks beat the streamed tiles, long K included
-    for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (32, 6144, 4096), (12, 14336, 4096)):
+    for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (32, 6144, 4096), (24, 8192, 8192)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (2, 32), (M, N, K)
         assert p.grid_x == N // 32
+    # M <= 16 with more than 128 64-column blocks: 64-column skinny blocks
+    for M, N, K in ((16, 28672, 4096), (8, 28672, 8192), (4, 14336, 4096)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (3, 64), (M, N, K)
     # ... measured with G = 128; smaller groups keep the streamed tiles
     for G in (32, 64):
         p = _lib.plan(16, 8192, 28672, G)

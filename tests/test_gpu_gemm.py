@@ -211,14 +211,17 @@ def test_mfma_split_k(M, K, N, G):
 ])
 def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
-    with 4 and (M <= 32) 8 waves per workgroup, and (M <= 32, N even) 32-column
-    blocks with two columns per lane."""
+    with 4 and (M <= 32) 8 waves per workgroup, (M <= 32, N even) 32-column
+    blocks with two columns per lane and (M <= 16, N % 4 == 0) 64-column blocks
+    with four."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in ((0, 1) + ((2,) if N % 2 == 0 else ()) if M <= 32 else (0,)):
+    cfgs = ((0, 1) + ((2,) if N % 2 == 0 else ()) if M <= 32 else (0,)) + (
+        (3,) if M <= 16 and N % 4 == 0 else ())
+    for cfg in cfgs:
         log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg}")
         p = plan_for(M, N, K, G, "skinny")
         p.tile_cfg = cfg

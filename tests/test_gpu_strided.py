@@ -86,7 +86,7 @@ def test_skinny_strided(M, N):
 
     K, G = 2048, 64
     X, qw, s, z = _case(M, K, N, G, seed=M + 1)
-    for cfg in (0, 1, 2) if M <= 32 else (0,):
+    for cfg in ((0, 1, 2) if M <= 32 else (0,)) + ((3,) if M <= 16 and N % 4 == 0 else ()):
         p = plan_for(M, N, K, G, "skinny", 0)
         p.tile_cfg = cfg
         log(f"skinny strided M={M} N={N} cfg={cfg}")

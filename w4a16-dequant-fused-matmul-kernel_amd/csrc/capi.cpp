@@ -188,6 +188,18 @@ bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t G, int cus) {
   return skinny_wide(M, N, cus) && G % 128 == 0 && (N <= 8192 || (N <= 16384 && M <= 16));
 }
 
+// 64-column blocks (four columns per lane: 16-B weight loads, one activation
+// stream per 64 columns) for M <= 16, G % 128 == 0, where they still give more
+// than half the CUs a block (N > 8192 on MI355X).  Measured there against the
+// best other plan: M = 4 / 8, K = 4096, N = 28672: 20.9 / 22.4 vs 22.3 / 23.6
+// us (streamed tiles); M = 8, K = 8192, N = 28672: 35.6 vs 40.1; M = 16,
+// K = 4096, N = 14336: 14.7 vs 16.4 (32-column blocks); M = 16, K = 4096,
+// N = 28672: 23.7 vs 23.3.  Fewer blocks or smaller groups lose (K = 28672,
+// N = 8192: 52.5 vs 43.4; G = 32, K = 8192, N = 28672: 47.1 vs 43.1).
+bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
+  return M <= 16 && N % 4 == 0 && G % 128 == 0 && (N + 63) / 64 > cus / 2;
+}
+
 // k-splits for the streamed kernel on few tiles: about 448 workgroups (two
 // per CU at most), at least 8 k-steps per split.
 int stream_split_for(int64_t tiles, int64_t K) {
@@ -244,9 +256,11 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
-    else if (small_m_takes_stream(M, N, K, G) &&
-             !(skinny_applicable(M, G) && skinny_wide_beats_stream(M, N, G, cus)))
-      kernel = W4A16_KERNEL_MFMA;
+    else if (small_m_takes_stream(M, N, K, G))
+      kernel = skinny_applicable(M, G) && (skinny_quad(M, N, G, cus) ||
+                                           skinny_wide_beats_stream(M, N, G, cus))
+                   ? W4A16_KERNEL_SKINNY
+                   : W4A16_KERNEL_MFMA;
     else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G))
       kernel = W4A16_KERNEL_GEMV;
     else if (M <= kSkinnyMaxM && skinny_applicable(M, G))
@@ -302,7 +316,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     case W4A16_KERNEL_SKINNY:
       if (!skinny_applicable(M, G)) return W4A16_ERR_BAD_PLAN;
       p->tile_m = (int32_t)((M + 15) / 16 * 16);
-      p->tile_n = skinny_wide(M, N, cus) ? 32 : 16;
+      p->tile_n = skinny_quad(M, N, G, cus) ? 64 : skinny_wide(M, N, cus) ? 32 : 16;
       p->grid_x = (N + p->tile_n - 1) / p->tile_n;
       p->grid_y = 1;
       // 32-column blocks where they apply (cfg 2), else 16-column blocks
@@ -311,7 +325,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       // 16, K = 4096, N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us;
       // M = 8 / 16, K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32,
       // K = N = 4096: 11.5 vs 12.1; M = 8, K = 8192, N = 1024: 9.6 vs 9.9)
-      p->tile_cfg = p->tile_n == 32 ? 2 : 0;
+      p->tile_cfg = p->tile_n == 64 ? 3 : p->tile_n == 32 ? 2 : 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
@@ -392,8 +406,9 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
       return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }
     case W4A16_KERNEL_SKINNY: {
-      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 2 ||
-          (p->tile_cfg >= 1 && M > 32) || (p->tile_cfg == 2 && N % 2 != 0))
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 3 ||
+          (p->tile_cfg >= 1 && M > 32) || (p->tile_cfg == 2 && N % 2 != 0) ||
+          (p->tile_cfg == 3 && (M > 16 || N % 4 != 0)))
         return W4A16_ERR_BAD_PLAN;
       if (!aligned(x, 16) || !aligned(qw, 4) || !aligned(sc, 2) || !aligned(zr, 2))
         return W4A16_ERR_BAD_PLAN;

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
     int N, int K, int G, int nblk, int ldx, int ldy) {
-  static_assert(NT == 1 || NT == 2, "one or two columns per lane");
+  static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four columns per lane");
   constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][NT][64];
 
@@ -109,10 +109,16 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
         const uint32_t wk = uniform(in ? (uint32_t)ks * 4u * (uint32_t)N * 4u : kOobOffset);
         if constexpr (NT == 1) {
           b.w[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rw, (int)w_off, (int)wk, 0);
-        } else {
+        } else if constexpr (NT == 2) {
           const uint2 w2 = buf_load8(rw, w_off, wk);
           b.w[j][0] = w2.x;
           b.w[j][1] = w2.y;
+        } else {
+          const uint4 w4 = buf_load16(rw, w_off, wk);
+          b.w[j][0] = w4.x;
+          b.w[j][1] = w4.y;
+          b.w[j][2] = w4.z;
+          b.w[j][3] = w4.w;
         }
         if (j % GSTEP == 0) {
           const uint32_t gk =
@@ -123,13 +129,20 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
             const uint32_t zv =
                 (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rz, (int)s_off, (int)gk, 0);
             b.sz[j][0] = (sv & 0xFFFFu) | (zv << 16);
-          } else {
+          } else if constexpr (NT == 2) {
             const uint32_t sv =
                 (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)s_off, (int)gk, 0);
             const uint32_t zv =
                 (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rz, (int)s_off, (int)gk, 0);
             b.sz[j][0] = (sv & 0xFFFFu) | (zv << 16);
             b.sz[j][1] = (sv >> 16) | (zv & 0xFFFF0000u);
+          } else {
+            const uint2 sv = buf_load8(rs, s_off, gk);
+            const uint2 zv = buf_load8(rz, s_off, gk);
+            b.sz[j][0] = (sv.x & 0xFFFFu) | (zv.x << 16);
+            b.sz[j][1] = (sv.x >> 16) | (zv.x & 0xFFFF0000u);
+            b.sz[j][2] = (sv.y & 0xFFFFu) | (zv.y << 16);
+            b.sz[j][3] = (sv.y >> 16) | (zv.y & 0xFFFF0000u);
           }
         } else {
 #pragma unroll
@@ -225,6 +238,17 @@ hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
       return hipGetLastError();
     }
   }
+  if constexpr (MT == 1) {
+    if (cfg == 3) {   // 64-column blocks
+      const int nblk4 = (a.N + 63) / 64;
+      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 4>), dim3(nblk4), dim3(256), 0, st,
+                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
+                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
+                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
+                         a.G, nblk4, a.ldx, a.ldy);
+      return hipGetLastError();
+    }
+  }
   const int nblk = (a.N + 15) / 16;
   // 8 waves (M <= 32 only, register budget): two per SIMD, twice the weight
   // loads in flight per CU -- pays when there is about one workgroup per CU
@@ -262,9 +286,11 @@ hipError_t launch_mt(const GemmArgs& a, int cfg, hipStream_t st) {
 }  // namespace
 
 // cfg 0: 4 waves, 16-column blocks; 1: 8 waves (M <= 32); 2: 4 waves,
-// 32-column blocks (M <= 32, N even)
+// 32-column blocks (M <= 32, N even); 3: 4 waves, 64-column blocks (M <= 16,
+// N % 4 == 0)
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st) {
-  if (cfg < 0 || cfg > 2 || (cfg >= 1 && a.M > 32) || (cfg == 2 && a.N % 2 != 0))
+  if (cfg < 0 || cfg > 3 || (cfg >= 1 && a.M > 32) || (cfg == 2 && a.N % 2 != 0) ||
+      (cfg == 3 && (a.M > 16 || a.N % 4 != 0)))
     return hipErrorInvalidValue;
   switch ((a.M + 15) / 16) {
     case 1: return launch_mt<1>(a, cfg, st);
