@@ -74,6 +74,14 @@ typedef struct w4a16_plan {
 /* Version of this ABI (W4A16_ABI_VERSION). */
 int w4a16_abi_version(void);
 
+/*
+ * Identity of the sources the library was built from: the hex sha256 the build
+ * computes over them (never NULL).  No reference counterpart (the reference
+ * JIT-compiles its extension on first use, pkg/cuda_kernel.py:56-61); a loader
+ * compares it with the sources beside it and refuses a stale library.
+ */
+const char* w4a16_build_id(void);
+
 /* Static English text for a status code (never NULL). */
 const char* w4a16_status_string(int status);
 

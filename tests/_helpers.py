@@ -68,8 +68,22 @@ def oracle_cols(X: torch.Tensor, qw, s, z, G: int, cols: np.ndarray) -> np.ndarr
     return O.reference_w4a16(np_(X), np_(qw)[:, cols], np_(s)[:, cols], np_(z)[:, cols], G)
 
 
+STRATUM = 16   # narrowest column block any kernel gives a workgroup
+
+
 def sample_cols(N: int, k: int = 96, seed: int = 0) -> np.ndarray:
+    """Columns for an oracle check of a wide output (columns are independent).
+
+    Stratified: one random column inside every STRATUM-column block, so every
+    column block of every kernel (16/32/64/256 columns wide) and every tile of
+    the XCD-grouped tile orders is checked at least once, at a random lane
+    position within the block; plus `k` further random columns and the first
+    and last four.
+    """
     rng = np.random.default_rng(seed + N)
     edge = np.array([0, 1, 2, 3, N - 4, N - 3, N - 2, N - 1])
+    starts = np.arange(0, N, STRATUM)
+    widths = np.minimum(STRATUM, N - starts)
+    strat = starts + (rng.random(len(starts)) * widths).astype(np.int64)
     mid = rng.choice(N, size=min(k, N), replace=False)
-    return np.unique(np.concatenate([edge[edge >= 0], mid]))
+    return np.unique(np.concatenate([edge[edge >= 0], strat, mid]))

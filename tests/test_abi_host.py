@@ -14,6 +14,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -477,3 +478,38 @@ def test_workload_bytes_formula():
     c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
     assert c4.flops() == 2 * 4096 * 14336 * 4096
     assert c4.bytes() == 182_190_080
+
+
+def test_sampled_columns_cover_every_block():
+    """The GPU tests check wide outputs on sampled columns; the sample must hit
+    every 16-column block (and hence every 32/64/256-column block and tile) of
+    each BASELINE width, at varying lane positions within the block."""
+    from _helpers import STRATUM, sample_cols
+
+    for N in (4096, 6144, 8192, 14336, 28672, 4100, 1028):
+        cols = sample_cols(N, 128)
+        assert cols.min() >= 0 and cols.max() < N
+        assert len(np.unique(cols)) == len(cols)
+        for width in (STRATUM, 32, 64, 256):
+            hit = np.zeros((N + width - 1) // width, bool)
+            hit[cols // width] = True
+            assert hit.all(), (N, width)
+        assert len(np.unique(cols % STRATUM)) == STRATUM, N
+
+
+def test_library_built_from_these_sources(lib):
+    """The library carries the sha256 of the sources it was built from, and it
+    equals the hash of the sources in the tree."""
+    from w4a16 import _build
+
+    assert lib.w4a16_build_id().decode() == _build.source_hash()
+
+
+def test_stale_library_refused(monkeypatch):
+    """A library built from other sources than those beside it is refused."""
+    from w4a16 import _lib
+
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "_sources_hash", lambda: "0" * 64)
+    with pytest.raises(ImportError, match="other sources"):
+        _lib.load()

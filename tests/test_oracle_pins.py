@@ -381,6 +381,81 @@ def test_reference_gemm_float64_bruteforce(M, K, N, G):
             assert O.within_tolerance(Y[m, n], ref), (m, n, float(Y[m, n]), float(ref))
 
 
+def _f64_product(X: np.ndarray, W: np.ndarray) -> np.ndarray:
+    """fp16(X @ W) with the sums formed in Python floats (float64), row by
+    column, with no BLAS involved."""
+    M, K = X.shape
+    N = W.shape[1]
+    out = np.empty((M, N), np.float16)
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                acc += float(X[m, k]) * float(W[k, n])
+            out[m, n] = np.float16(acc)
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,G", [(3, 32, 5, 8), (2, 96, 11, 32), (4, 256, 7, 128)])
+def test_dequant_then_matmul_float64_bruteforce(M, K, N, G):
+    """reference.py:43-53: fp16 weights materialised, then a matmul with an fp16
+    result.  Pinned against float64 brute force over the weight dequantised by
+    hand from the unpacked codes (not by the oracle's dequantize_weight), on
+    non-square shapes, so a transposed operand or a wrong group index fails."""
+    rng = np.random.default_rng(7 * M + K + N)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    W = (rng.standard_normal((K, N)) * 0.05).astype(np.float16)
+    qw, s, z = O.quantize_weight(W, G)
+    Y = O.dequant_then_matmul(X, qw, s, z, G)
+    assert Y.shape == (M, N) and Y.dtype == np.float16
+    q = O.unpack_int4(qw)
+    wdq = np.empty((K, N), np.float16)
+    for k in range(K):
+        for n in range(N):
+            wdq[k, n] = np.float16((np.float16(q[k, n]) - z[k // G, n]) * s[k // G, n])
+    exp = _f64_product(X, wdq)
+    assert O.within_tolerance(Y, exp).all()
+    # the two baselines of reference.py agree with its oracle at fp16 output
+    assert O.within_tolerance(Y, O.reference_w4a16(X, qw, s, z, G)).all()
+    with pytest.raises(AssertionError):
+        O.dequant_then_matmul(X.astype(np.float32), qw, s, z, G)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 40, 3), (5, 64, 9), (3, 17, 6)])
+def test_fp16_matmul_float64_bruteforce(M, K, N):
+    """reference.py:56-67: plain fp16 [M, K] @ [K, N].  Pinned by float64 brute
+    force (within one fp16 ulp) and by its preconditions: fp16 operands and a
+    matching K (a transposed W of a non-square shape is refused)."""
+    rng = np.random.default_rng(M * 31 + K * 7 + N)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    W = (rng.standard_normal((K, N)) * 0.1).astype(np.float16)
+    Y = O.fp16_matmul(X, W)
+    assert Y.shape == (M, N) and Y.dtype == np.float16
+    assert O.within_tolerance(Y, _f64_product(X, W)).all()
+    with pytest.raises(AssertionError):
+        O.fp16_matmul(X, np.ascontiguousarray(W.T))
+    with pytest.raises(AssertionError):
+        O.fp16_matmul(X.astype(np.float32), W)
+
+
+def test_fp16_baselines_match_torch_cpu():
+    """The third-party boundary: the reference runs both baselines through
+    ``torch.matmul`` on fp16 tensors (reference.py:53, :67).  torch's own CPU
+    result must lie within one fp16 ulp of the oracle's."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    M, K, N, G = 6, 512, 40, 64
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    W = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    qw, s, z = O.quantize_weight(W, G)
+    wdq = O.dequantize_weight(qw, s, z, G)
+    t_dq = torch.matmul(torch.from_numpy(X), torch.from_numpy(wdq)).numpy()
+    t_fp = torch.matmul(torch.from_numpy(X), torch.from_numpy(W)).numpy()
+    assert O.within_tolerance(O.dequant_then_matmul(X, qw, s, z, G), t_dq).all()
+    assert O.within_tolerance(O.fp16_matmul(X, W), t_fp).all()
+
+
 def test_linear_forward_bias_double_rounding():
     """linear.py:90-91: y = fp16(Y) + bias in fp16 (two roundings).  Checked
     against float64 brute force with the two roundings applied explicitly."""

@@ -442,9 +442,16 @@ int run_auto(const void* x, int64_t ldx, const int32_t* qw, const void* sc, cons
 
 }  // namespace
 
+// sha256 of the sources this library was built from (set by the build).
+#ifndef W4A16_SOURCE_HASH
+#define W4A16_SOURCE_HASH "unknown"
+#endif
+
 extern "C" {
 
 int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
+const char* w4a16_build_id(void) { return W4A16_SOURCE_HASH; }
 
 const char* w4a16_status_string(int status) {
   switch (status) {

@@ -7,6 +7,7 @@ Every source under ``csrc/`` is compiled for gfx950 only, then linked into
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -22,7 +23,23 @@ SOURCES = ["gemv.hip", "gemm_mfma.hip", "gemm_lds.hip", "gemm_occ2.hip", "gemm_s
            "gemm_skinny.hip", "simt.hip",
            "quant.hip", "capi.cpp"]
 HEADERS = ["w4a16_device.h", "w4a16_launch.h"]
+PUBLIC_HEADER = os.path.join(os.path.dirname(ROOT_DIR), "include", "w4a16.h")
 ARCH = "gfx950"
+
+
+def source_hash() -> str:
+    """sha256 over the names and contents of every file the library is built
+    from (the csrc sources and headers, and the public header).  Compiled into
+    the library (w4a16_build_id) and compared by the loader, so a library
+    built from other sources is refused rather than silently run."""
+    h = hashlib.sha256()
+    files = [(n, os.path.join(CSRC, n)) for n in sorted(SOURCES + HEADERS)]
+    files.append(("include/w4a16.h", PUBLIC_HEADER))
+    for name, path in files:
+        with open(path, "rb") as f:
+            data = f.read()
+        h.update(name.encode() + b"\0" + len(data).to_bytes(8, "little") + data)
+    return h.hexdigest()
 
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU ops.
 # No fast-math: the quantiser relies on IEEE division and signed zeros.
@@ -43,9 +60,9 @@ def hipcc() -> str:
     return exe
 
 
-def _compile(src: str, verbose: bool) -> str:
+def _compile(src: str, verbose: bool, defines: list[str]) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *defines, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -62,8 +79,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     """Compile every source and link libw4a16.so; returns the library path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
+    defines = [f'-DW4A16_SOURCE_HASH="{source_hash()}"']
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, verbose, defines), SOURCES))
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:

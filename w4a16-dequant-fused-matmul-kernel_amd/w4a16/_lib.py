@@ -1,8 +1,11 @@
 """ctypes binding of ``libw4a16.so`` (declarations: ``include/w4a16.h``).
 
 The library is built in-tree by :mod:`w4a16._build`.  Loading never falls back to
-anything: a missing or stale library raises ``ImportError`` with the build
-command, so no caller can silently run without the HIP kernels.
+anything: a missing library, one lacking a declared symbol, one of another ABI
+version, or one built from other sources than those beside it (the sha256 the
+build compiles in, ``w4a16_build_id``, against the sources' own) raises
+``ImportError`` with the build command, so no caller can silently run without
+the HIP kernels or on kernels older than the sources.
 """
 from __future__ import annotations
 
@@ -61,6 +64,7 @@ _int = ctypes.c_int
 # name -> (restype, argtypes); exactly the functions include/w4a16.h declares
 SIGNATURES = {
     "w4a16_abi_version": (_int, []),
+    "w4a16_build_id": (ctypes.c_char_p, []),
     "w4a16_status_string": (ctypes.c_char_p, [_int]),
     "w4a16_gemm_plan": (_int, [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(Plan)]),
     "w4a16_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
@@ -85,6 +89,16 @@ SIGNATURES = {
 
 _LIB = None
 _LOCK = threading.Lock()
+
+
+def _sources_hash() -> str | None:
+    """sha256 of the sources beside the package (None when they are absent,
+    e.g. a library installed without its sources)."""
+    from . import _build
+
+    if not os.path.isdir(_build.CSRC):
+        return None
+    return _build.source_hash()
 
 
 def load() -> ctypes.CDLL:
@@ -114,6 +128,12 @@ def load() -> ctypes.CDLL:
         ver = lib.w4a16_abi_version()
         if ver != ABI_VERSION:
             raise ImportError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}; rebuild it")
+        want = _sources_hash()
+        got = lib.w4a16_build_id().decode()
+        if want is not None and got != want:
+            raise ImportError(
+                f"{LIB_PATH} was built from other sources (build id {got[:12]}, sources "
+                f"{want[:12]}); rebuild it with `python -m w4a16._build`")
         _LIB = lib
         return lib
 

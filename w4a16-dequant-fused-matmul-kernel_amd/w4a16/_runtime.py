@@ -48,12 +48,27 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     """A workspace of at least `nbytes` for the current stream.
 
     It holds split-K fp32 partial sums (forced GEMV splits, prefill splits),
-    which every call rewrites before reading, so its contents never matter and
-    one buffer serves every later call on the same stream.  Calls on one stream
-    are ordered, so sharing is safe; each stream has its own buffer.
+    which every call writes before it reads them within the same call, so its
+    contents never matter between calls.
+
+    * Eager calls share one buffer per (device, stream): calls on one stream
+      are ordered, and a buffer replaced by a larger one goes back to torch's
+      stream-ordered caching allocator, which hands it out again only after
+      the work already queued on that stream.
+    * A call made while the stream is being captured into a HIP graph gets a
+      buffer of its own, allocated inside the capture: it comes from the
+      graph's private memory pool, so the graph owns it for as long as the
+      graph exists, no other graph or eager call can be given it, and
+      replaying graphs on different streams at the same time cannot race on
+      it.  A later allocation in the same capture may reuse it; replays run
+      such work after this call's kernels, as in eager order.  The shared
+      eager buffer is never recorded into a graph, so growing or freeing it
+      cannot leave a graph pointing at freed memory.
     """
     if nbytes <= 0:
         return None
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            stream_ptr(device))
     with _WS_LOCK:
