@@ -5,8 +5,9 @@
  * the HIP stream as `void*` (a hipStream_t; NULL = the legacy default stream).
  * All device pointers belong to the calling thread's current HIP device and are
  * owned by the caller; the library allocates nothing and keeps no global mutable
- * state apart from a per-device cache of the CU count.  Launches are
- * asynchronous on `stream`.
+ * state apart from a per-device cache of the CU count and, for
+ * w4a16_gemm_f16_noalloc only, a static device scratch array per GPU.
+ * Launches are asynchronous on `stream`.
  *
  * Return value: 0 (W4A16_OK) on success, a negative w4a16_status for an invalid
  * argument (detected on the host, before anything is launched), or a positive
@@ -148,6 +149,33 @@ int w4a16_gemm_f16_strided(const w4a16_plan* plan, const void* x, int64_t ldx,
                            const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                            int64_t group_size, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/*
+ * Bytes of the device scratch behind w4a16_gemm_f16_noalloc: a static array
+ * that every GPU the library runs on holds until the process ends.
+ */
+#define W4A16_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/*
+ * As w4a16_gemm_f16_strided, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): no workspace argument and no allocation of any kind.  No
+ * counterpart in the reference.  The split-K partials go to the library's own
+ * static device scratch of W4A16_NOALLOC_SCRATCH_BYTES per GPU (its address is
+ * resolved with hipGetSymbolAddress on a device's first call).  An explicit
+ * `plan` whose partials exceed that size is refused with W4A16_ERR_WORKSPACE;
+ * with `plan` NULL the automatic plan is limited to the most k-splits whose
+ * partials fit (one split needs none, so every shape runs).  Every call on a
+ * GPU shares that GPU's scratch, which keeps the last call's contents
+ * (nothing needs to start zeroed: a call writes its partials before it reads
+ * them), so calls that overlap on one GPU -- different streams, or graphs
+ * replayed concurrently -- race and must be ordered by the caller.  Results
+ * equal w4a16_gemm_f16_strided's for the same plan.
+ */
+int w4a16_gemm_f16_noalloc(const w4a16_plan* plan, const void* x, int64_t ldx,
+                           const int32_t* qweight, const void* scales, const void* zeros,
+                           const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                           int64_t group_size, void* stream);
 
 /*
  * Group-wise asymmetric uint4 quantisation of fp16 W [K, N] with int4 packing,

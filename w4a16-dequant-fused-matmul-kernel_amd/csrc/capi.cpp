@@ -8,6 +8,7 @@
 
 #include <atomic>
 #include <climits>
+#include <mutex>
 
 #include "../../include/w4a16.h"
 #include "w4a16_launch.h"
@@ -422,22 +423,75 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
 }
 
 // Automatic plan, falling back to the SIMT kernel when the pointers or row
-// strides do not meet the vector kernels' alignment.
+// strides do not meet the vector kernels' alignment.  Shape and strides must
+// have been checked.
+int auto_plan(const void* x, int64_t ldx, const int32_t* qw, const void* sc, const void* zr,
+              const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t G,
+              w4a16_plan* p) {
+  if (int st = make_plan(M, N, K, G, W4A16_KERNEL_AUTO, 0, p)) return st;
+  const GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy};
+  const bool vec_aligned = aligned(x, 16) && aligned(qw, 16) && aligned(sc, 8) &&
+                           aligned(zr, 8) && aligned(y, 8) && (!bias || aligned(bias, 8)) &&
+                           strides_vec_ok(a, p->kernel, p->split_k);
+  if (p->kernel != W4A16_KERNEL_SIMT && !vec_aligned)
+    return make_plan(M, N, K, G, W4A16_KERNEL_SIMT, 0, p);
+  return W4A16_OK;
+}
+
 int run_auto(const void* x, int64_t ldx, const int32_t* qw, const void* sc, const void* zr,
              const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int64_t G,
              void* ws, size_t ws_bytes, void* stream) {
   if (int st = check_gemm_shape(M, N, K, G)) return st;
   if (int st = check_strides(M, N, K, ldx, ldy)) return st;
   w4a16_plan p;
-  if (int st = make_plan(M, N, K, G, W4A16_KERNEL_AUTO, 0, &p)) return st;
-  const GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy};
-  const bool vec_aligned = aligned(x, 16) && aligned(qw, 16) && aligned(sc, 8) &&
-                           aligned(zr, 8) && aligned(y, 8) && (!bias || aligned(bias, 8)) &&
-                           strides_vec_ok(a, p.kernel, p.split_k);
-  if (p.kernel != W4A16_KERNEL_SIMT && !vec_aligned) {
-    if (int st = make_plan(M, N, K, G, W4A16_KERNEL_SIMT, 0, &p)) return st;
-  }
+  if (int st = auto_plan(x, ldx, qw, sc, zr, bias, y, ldy, M, N, K, G, &p)) return st;
   return run_planned(&p, x, ldx, qw, sc, zr, bias, y, ldy, M, N, K, G, ws, ws_bytes, stream);
+}
+
+// Split-K partial bytes a plan's kernels write (what run_planned requires of
+// the workspace).
+size_t plan_scratch_bytes(const w4a16_plan& p, int64_t M, int64_t N, int64_t K) {
+  if (p.split_k <= 1) return 0;
+  if (p.kernel == W4A16_KERNEL_GEMV) return gemv_workspace_bytes((int)M, (int)N, (int)K, p.split_k);
+  if (p.kernel == W4A16_KERNEL_MFMA) return mfma_workspace_bytes(M, N, K, p.split_k);
+  return 0;
+}
+
+// ---- scratch of the allocation-free entry point ---------------------------
+// The split-K partials of w4a16_gemm_f16_noalloc live in this file-scope
+// device array: every GPU the library runs on holds its own copy until the
+// process ends.  In host code the name is only a stand-in for the symbol;
+// the array's device address on the current device comes from
+// hipGetSymbolAddress (scratch_on_device), and only that address is passed
+// to kernels.
+static __device__ __align__(256) unsigned char scratch[W4A16_NOALLOC_SCRATCH_BYTES];
+
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, resolved once per device
+// (with that device current) and kept.
+int scratch_on_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return W4A16_ERR_NO_DEVICE;
+  }
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return e != hipSuccess ? (int)e : W4A16_ERR_NO_DEVICE;
+      }
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return W4A16_OK;
 }
 
 }  // namespace
@@ -516,6 +570,33 @@ int w4a16_gemm_f16_strided(const w4a16_plan* plan, const void* x, int64_t ldx,
                     workspace_bytes, stream);
   return run_planned(plan, x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size,
                      workspace, workspace_bytes, stream);
+}
+
+int w4a16_gemm_f16_noalloc(const w4a16_plan* plan, const void* x, int64_t ldx,
+                           const int32_t* qweight, const void* scales, const void* zeros,
+                           const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                           int64_t group_size, void* stream) {
+  if (int st = check_gemm_shape(M, N, K, group_size)) return st;
+  if (int st = check_strides(M, N, K, ldx, ldy)) return st;
+  constexpr size_t kMax = W4A16_NOALLOC_SCRATCH_BYTES;
+  w4a16_plan p;
+  if (plan) {
+    // an explicit plan whose partials do not fit the scratch is refused
+    p = *plan;
+    if (plan_scratch_bytes(p, M, N, K) > kMax) return W4A16_ERR_WORKSPACE;
+  } else {
+    if (int st = auto_plan(x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size, &p))
+      return st;
+    // the automatic plan takes the most k-splits whose partials fit (a plan
+    // with one split needs no scratch at all)
+    for (int s = p.split_k - 1; plan_scratch_bytes(p, M, N, K) > kMax && s >= 1; --s)
+      if (int st = make_plan(M, N, K, group_size, p.kernel, s, &p)) return st;
+    if (plan_scratch_bytes(p, M, N, K) > kMax) return W4A16_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (int st = scratch_on_device(&ws)) return st;
+  return run_planned(&p, x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size, ws,
+                     kMax, stream);
 }
 
 static int quantize_common(const void* W, bool f32, int32_t* qweight, void* scales, void* zeros,

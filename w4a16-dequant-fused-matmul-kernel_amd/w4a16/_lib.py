@@ -22,6 +22,8 @@ KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
                 KERNEL_SKINNY: "skinny"}
 # MFMA tile configurations 0 .. MFMA_CONFIGS-1 (w4a16_plan.tile_cfg)
 MFMA_CONFIGS = 14
+# W4A16_NOALLOC_SCRATCH_BYTES: the static scratch of w4a16_gemm_f16_noalloc
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # enum w4a16_status
 STATUS = {
@@ -79,6 +81,11 @@ SIGNATURES = {
         _int,
         [ctypes.POINTER(Plan), _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _vp, _sz, _vp],
+    ),
+    "w4a16_gemm_f16_noalloc": (
+        _int,
+        [ctypes.POINTER(Plan), _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+         _vp],
     ),
     "w4a16_quantize_pack_f16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "w4a16_quantize_pack_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
