@@ -50,7 +50,7 @@ enum w4a16_status {
 enum w4a16_kernel {
   W4A16_KERNEL_AUTO = 0,
   W4A16_KERNEL_GEMV = 1, /* decode: VALU dot2, no MFMA, M <= 8, optional split-K    */
-  W4A16_KERNEL_MFMA = 2, /* prefill: MFMA (32x32x16 / 16x16x32), tile_cfg 0..13     */
+  W4A16_KERNEL_MFMA = 2, /* prefill: MFMA (32x32x16 / 16x16x32), tile_cfg below     */
   W4A16_KERNEL_SIMT = 3, /* sequential-k, one thread per output, any shape           */
   W4A16_KERNEL_SKINNY = 4 /* small batch: v_mfma_f32_16x16x32_f16, weights streamed   */
 };
@@ -59,14 +59,15 @@ enum w4a16_kernel {
 typedef struct w4a16_plan {
   int32_t kernel;          /* enum w4a16_kernel (never AUTO once planned)       */
   int32_t split_k;         /* GEMV, MFMA cfg 7/8/11-13: k-splits (1 = none)     */
-  int32_t tile_cfg;        /* MFMA: tile configuration 0..13 (tile_m x tile_n);
-                              GEMV: 0 / 1 / 2 = 4 / 8 / 16 waves per workgroup
-                              (16 for M <= 2), 3 / 4 / 5 = the same with the
+  int32_t tile_cfg;        /* MFMA: tiling 1, 2, 6, 7, 11, 12 or 13 (tile_m x
+                              tile_n); GEMV: 1 / 2 = 8 / 16 waves per workgroup
+                              (16 for M <= 2), 4 / 5 = the same with the
                               activations staged in LDS (M <= 2; larger M
-                              always stages them); SKINNY: 0 / 1 = 4 / 8 waves
-                              on 16-column blocks (8 for M <= 32), 2 = 4 waves
-                              on 32-column blocks (M <= 32, N even), 3 = 4
-                              waves on 64-column blocks (M <= 16, N % 4 == 0) */
+                              always stages them); SKINNY: 0 / 2 / 3 = 16 / 32 /
+                              64-column blocks of 4 waves (32: M <= 32, N even;
+                              64: M <= 16, N % 4 == 0).  Other numbers name
+                              retired forms and are refused
+                              (W4A16_ERR_BAD_PLAN)                           */
   int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup   */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */

@@ -112,6 +112,61 @@ def test_split_k_gemv_requires_workspace(lib):
     assert code == -5
 
 
+def test_retired_configurations_refused(lib):
+    """Tile / wave configurations retired from the library (measured slower on
+    every shape) are refused by number before anything is launched (fake,
+    never dereferenced pointers: no call here may reach a launch; a live GEMV
+    configuration with a split and no workspace stops at the workspace
+    check)."""
+    from w4a16 import _lib
+
+    a = ctypes.c_void_p(1 << 12)
+    M, N, K, G = 128, 1024, 4096, 128
+    for cfg in range(16):
+        if cfg in _lib.MFMA_CONFIGS:
+            continue       # valid: would launch
+        p = _lib.plan(M, N, K, G, _lib.KERNEL_MFMA, 1)
+        p.tile_cfg = cfg
+        code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, M, N, K, G,
+                                          NULL, 0, NULL)
+        assert code == -5, cfg
+    for cfg in range(8):
+        p = _lib.plan(1, N, K, G, _lib.KERNEL_GEMV, 4)
+        p.tile_cfg = cfg
+        code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, N, K, G,
+                                          NULL, 0, NULL)
+        assert code == (-4 if cfg in _lib.GEMV_CONFIGS else -5), cfg
+    for cfg in range(6):
+        p = _lib.plan(16, N, K, G, _lib.KERNEL_SKINNY, 0)
+        p.tile_cfg = cfg
+        if cfg in _lib.SKINNY_CONFIGS:
+            continue       # valid: would launch
+        code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 16, N, K, G,
+                                          NULL, 0, NULL)
+        assert code == -5, cfg
+
+
+def test_skinny_plans_check_their_load_alignment(lib):
+    """32- and 64-column skinny blocks load 2 / 4 adjacent columns per lane in
+    one load: 8 / 16-byte weights and 4 / 8-byte scales and zeros.  Pointers
+    aligned for 16-column blocks only are refused for those plans."""
+    from w4a16 import _lib
+
+    M, N, K, G = 16, 1024, 4096, 128
+    good = ctypes.c_void_p(1 << 12)
+    for cfg, qw_off, sz_off in ((2, 4, 2), (3, 8, 4), (3, 4, 2)):
+        p = _lib.plan(M, N, K, G, _lib.KERNEL_SKINNY, 0)
+        p.tile_cfg = cfg
+        qw = ctypes.c_void_p((1 << 12) + qw_off)
+        sz = ctypes.c_void_p((1 << 12) + sz_off)
+        assert lib.w4a16_gemm_f16_planned(ctypes.byref(p), good, qw, good, good, NULL, good, M, N,
+                                          K, G, NULL, 0, NULL) == -5, cfg
+        assert lib.w4a16_gemm_f16_planned(ctypes.byref(p), good, good, sz, good, NULL, good, M, N,
+                                          K, G, NULL, 0, NULL) == -5, cfg
+        assert lib.w4a16_gemm_f16_planned(ctypes.byref(p), good, good, good, sz, NULL, good, M, N,
+                                          K, G, NULL, 0, NULL) == -5, cfg
+
+
 def test_planned_rejects_mismatched_plan(lib):
     from w4a16 import _lib
 

@@ -119,15 +119,15 @@ RAGGED = [
 
 @pytest.mark.parametrize("M,K,N,G", RAGGED)
 def test_gemv_splits(M, K, N, G):
-    """Decode GEMV with every column-block width, every wave count (4, 8, and
-    16 waves per workgroup for M <= 2), the LDS-staged activations (cfg 3-5,
+    """Decode GEMV with every column-block width, both wave counts (8, and 16
+    waves per workgroup for M <= 2), the LDS-staged activations (cfg 4, 5,
     M <= 2; K = 16640 needs several staging chunks) and k-splits 1, 2, 3, 7,
     auto."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M + K)
     ref = _ref(X, qw, s, z, G)
-    for cfg in ((0, 1, 2, 3, 4, 5) if M <= 2 else (0, 1)):
+    for cfg in ((1, 2, 4, 5) if M <= 2 else (1,)):
         for cols in (16, 32, 64, 256):
             for split in (1, 2, 3, 7, 0):
                 if split > K // 8:
@@ -149,19 +149,18 @@ def test_gemv_splits(M, K, N, G):
 ])
 def test_mfma_tile_configs(M, K, N, G):
     """Prefill MFMA kernels with every tile configuration over tails in M, N, K
-    (configs 4, 9, 10 -- weight tile dequantised into LDS -- and 7, 8 -- two
-    waves per SIMD with 16x16x32 MFMAs -- where K % 64 == 0; configs 5 and 6,
-    two waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; configs 11,
-    12 and 13, activations and weights streamed into LDS with 128-, 32- and
+    (configs 1 and 2, one wave per SIMD with 32x32x16 MFMAs, any K; config 7,
+    two waves per SIMD with 16x16x32 MFMAs, where K % 64 == 0; config 6, two
+    waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; configs 11, 12
+    and 13, activations and weights streamed into LDS with 128-, 32- and
     64-row tiles, where K % 256 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 3 + N)
     ref = _ref(X, qw, s, z, G)
-    for cfg in range(_lib.MFMA_CONFIGS):
-        if ((cfg in (4, 7, 8, 9, 10) and K % 64) or (cfg in (5, 6) and K % 128)
-                or (cfg >= 11 and K % 256)):
+    for cfg in _lib.MFMA_CONFIGS:
+        if (cfg == 7 and K % 64) or (cfg == 6 and K % 128) or (cfg >= 11 and K % 256):
             continue
         p = plan_for(M, N, K, G, "mfma", 1)
         p.tile_cfg = cfg
@@ -177,7 +176,7 @@ def test_mfma_tile_configs(M, K, N, G):
     (65, 4096, 1028, 128), (200, 2048, 516, 32), (256, 11008, 772, 64), (130, 2112, 260, 96),
 ])
 def test_mfma_split_k(M, K, N, G):
-    """Prefill split-K (cfg 7, 8 and, where K % 256 == 0, 11-13): fp32 partials per
+    """Prefill split-K (cfg 7 and, where K % 256 == 0, 11-13): fp32 partials per
     k-split, summed in split order by a second kernel; every split count, fused
     bias; then a forced GEMV split-K call reuses the same cached workspace."""
     from w4a16 import w4a16_matmul
@@ -186,7 +185,7 @@ def test_mfma_split_k(M, K, N, G):
     X, qw, s, z = _build_case(M, K, N, G, seed=M + N + K)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in (7, 8, 11, 12, 13) if K % 256 == 0 else (7, 8):
+    for cfg in (7, 11, 12, 13) if K % 256 == 0 else (7,):
         for split in (2, 3, 5, K // 64):
             p = plan_for(M, N, K, G, "mfma", split)
             p.tile_cfg = cfg
@@ -211,15 +210,14 @@ def test_mfma_split_k(M, K, N, G):
 ])
 def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
-    with 4 and (M <= 32) 8 waves per workgroup, (M <= 32, N even) 32-column
-    blocks with two columns per lane and (M <= 16, N % 4 == 0) 64-column blocks
-    with four."""
+    with 16-column blocks, (M <= 32, N even) 32-column blocks with two columns
+    per lane and (M <= 16, N % 4 == 0) 64-column blocks with four."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    cfgs = ((0, 1) + ((2,) if N % 2 == 0 else ()) if M <= 32 else (0,)) + (
+    cfgs = (0,) + ((2,) if M <= 32 and N % 2 == 0 else ()) + (
         (3,) if M <= 16 and N % 4 == 0 else ())
     for cfg in cfgs:
         log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg}")
@@ -363,18 +361,18 @@ def test_gemv_auto_split_long_k(M, K, N, G):
 
 
 def test_streamed_prefill_far_apart_scales_zeros():
-    """The streamed prefill kernel (cfg 11) reads scales and zeros through one
-    buffer resource based at the lower of the two; placed more than 2 GiB
-    apart they take the register kernel of the same tiles instead.  Both give
-    results within the oracle's tolerance."""
+    """The streamed prefill kernels (cfg 11 / 12 / 13) read scales and zeros
+    through one buffer resource based at the lower of the two; placed more
+    than 2 GiB apart they take the register kernel of 128 x 256 tiles (cfg 7)
+    instead, with the plan's k-split and workspace (its own split count never
+    exceeds the plan's).  Unsplit and split plans of every row count, with a
+    fused bias, against the oracle; the bias add is bit-exact."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
-    M, K, N, G = 256, 1024, 1028, 64
+    M, K, N, G = 256, 2048, 1028, 64
     X, qw, s, z = _build_case(M, K, N, G, seed=11)
     ref = _ref(X, qw, s, z, G)
-    p = plan_for(M, N, K, G, "mfma", 1)
-    p.tile_cfg = 11
-    assert_gemm_close(w4a16_matmul_planned(X, qw, s, z, G, p), ref, "cfg 11 adjacent")
+    b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
     # scales at the start and zeros at the end of one 2.5 GiB allocation
     big = torch.empty(5 << 29, dtype=torch.uint8, device=DEV)
     nb = s.numel() * 2
@@ -383,8 +381,17 @@ def test_streamed_prefill_far_apart_scales_zeros():
     dist = abs(z_far.data_ptr() - s_far.data_ptr())
     log(f"scales/zeros {dist / 2**30:.2f} GiB apart")
     assert dist >= (1 << 31)
-    out = w4a16_matmul_planned(X, qw, s_far, z_far, G, p)
-    assert_gemm_close(out, ref, "cfg 11 scales/zeros far apart")
+    for cfg, split in ((11, 1), (11, 3), (12, 2), (13, 4), (12, 8)):
+        p = plan_for(M, N, K, G, "mfma", split)
+        p.tile_cfg = cfg
+        assert p.split_k == split
+        log(f"far-apart cfg={cfg} split={p.split_k}")
+        adj = w4a16_matmul_planned(X, qw, s, z, G, p)
+        assert_gemm_close(adj, ref, f"cfg {cfg} split {split} adjacent")
+        out = w4a16_matmul_planned(X, qw, s_far, z_far, G, p)
+        assert_gemm_close(out, ref, f"cfg {cfg} split {split} scales/zeros far apart")
+        outb = w4a16_matmul_planned(X, qw, s_far, z_far, G, p, bias=b)
+        assert torch.equal(outb, out + b)
     del big
 
 

@@ -68,7 +68,7 @@ def test_gemv_strided(M, N):
 
     K, G = 2048, 128
     X, qw, s, z = _case(M, K, N, G, seed=M)
-    cfgs = (0, 1, 2, 3, 4, 5) if M <= 2 else (0, 1)
+    cfgs = (1, 2, 4, 5) if M <= 2 else (1,)
     for cfg in cfgs:
         for cols in (16, 32, 64, 256):
             for split in (1, 4):
@@ -86,7 +86,8 @@ def test_skinny_strided(M, N):
 
     K, G = 2048, 64
     X, qw, s, z = _case(M, K, N, G, seed=M + 1)
-    for cfg in ((0, 1, 2) if M <= 32 else (0,)) + ((3,) if M <= 16 and N % 4 == 0 else ()):
+    for cfg in (0,) + ((2,) if M <= 32 and N % 2 == 0 else ()) + (
+            (3,) if M <= 16 and N % 4 == 0 else ()):
         p = plan_for(M, N, K, G, "skinny", 0)
         p.tile_cfg = cfg
         log(f"skinny strided M={M} N={N} cfg={cfg}")
@@ -101,7 +102,7 @@ def test_mfma_strided_every_config(M, K, N, G):
 
     X, qw, s, z = _case(M, K, N, G, seed=M + K)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in range(_lib.MFMA_CONFIGS):
+    for cfg in _lib.MFMA_CONFIGS:
         p = plan_for(M, N, K, G, "mfma", 1)
         p.tile_cfg = cfg
         log(f"mfma strided M={M} K={K} N={N} cfg={cfg}")

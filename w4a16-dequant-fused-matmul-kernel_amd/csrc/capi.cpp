@@ -320,12 +320,13 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->tile_n = skinny_quad(M, N, G, cus) ? 64 : skinny_wide(M, N, cus) ? 32 : 16;
       p->grid_x = (N + p->tile_n - 1) / p->tile_n;
       p->grid_y = 1;
-      // 32-column blocks where they apply (cfg 2), else 16-column blocks
-      // with 4 waves per workgroup: with the branch-free batch loop the 8-wave
-      // form (cfg 1) is nowhere faster (measured on MI355X, 4 vs 8 waves: M = 3 / 8 /
-      // 16, K = 4096, N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us;
-      // M = 8 / 16, K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32,
-      // K = N = 4096: 11.5 vs 12.1; M = 8, K = 8192, N = 1024: 9.6 vs 9.9)
+      // 64- or 32-column blocks where they apply (cfg 3 / 2), else 16-column
+      // blocks (cfg 0), 4 waves per workgroup.  (An 8-wave form on 16-column
+      // blocks, once cfg 1, was nowhere faster with the branch-free batch
+      // loop -- measured on MI355X, 4 vs 8 waves: M = 3 / 8 / 16, K = 4096,
+      // N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us; M = 8 / 16,
+      // K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32, K = N = 4096:
+      // 11.5 vs 12.1 -- and was retired.)
       p->tile_cfg = p->tile_n == 64 ? 3 : p->tile_n == 32 ? 2 : 0;
       return W4A16_OK;
     case W4A16_KERNEL_SIMT:
@@ -407,13 +408,17 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
       return to_status(launch_mfma(a, p->tile_cfg, p->split_k, part, s));
     }
     case W4A16_KERNEL_SKINNY: {
-      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || p->tile_cfg < 0 || p->tile_cfg > 3 ||
-          (p->tile_cfg >= 1 && M > 32) || (p->tile_cfg == 2 && N % 2 != 0) ||
-          (p->tile_cfg == 3 && (M > 16 || N % 4 != 0)))
+      const int c = p->tile_cfg;
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || !(c == 0 || c == 2 || c == 3) ||
+          (c == 2 && (M > 32 || N % 2 != 0)) || (c == 3 && (M > 16 || N % 4 != 0)))
         return W4A16_ERR_BAD_PLAN;
-      if (!aligned(x, 16) || !aligned(qw, 4) || !aligned(sc, 2) || !aligned(zr, 2))
+      // each lane loads 1, 2 or 4 adjacent columns' words, scales and zeros
+      // in one load: 4 / 8 / 16-byte weights, 2 / 4 / 8-byte scales and zeros
+      const uintptr_t cols = c == 3 ? 4 : c == 2 ? 2 : 1;
+      if (!aligned(x, 16) || !aligned(qw, 4 * cols) || !aligned(sc, 2 * cols) ||
+          !aligned(zr, 2 * cols))
         return W4A16_ERR_BAD_PLAN;
-      return to_status(launch_skinny(a, p->tile_cfg, s));
+      return to_status(launch_skinny(a, c, s));
     }
     case W4A16_KERNEL_SIMT:
       return to_status(launch_simt(a, s));

@@ -521,50 +521,43 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// cfg 0: 128 x 512 (4 waves along N, each 128 x 128)
-// cfg 1: 128 x 256 (2 x 2 waves, each 64 x 128)
-// cfg 2:  32 x 512 (4 waves along N, each 32 x 128)
-// cfg 3:  64 x 512 (4 waves along N, each 64 x 128)
-// cfg 4: 256 x 256 with the weight tile dequantised once into LDS (gemm_lds.hip)
-// cfg 5: 256 x 128, two waves per SIMD (2 x 2 waves, each 128 x 64)
-// cfg 6: 128 x 256, two waves per SIMD (1 x 4 waves, each 128 x 64)
+// Tile configurations the planner takes (plans name them by number):
+// cfg 1: 128 x 256 (2 x 2 waves, each 64 x 128), 32x32x16 MFMA
+// cfg 2:  32 x 512 (4 waves along N, each 32 x 128), 32x32x16 MFMA
+// cfg 6: 128 x 256, two waves per SIMD (1 x 4 waves, each 128 x 64), 32x32x16
 // cfg 7: 128 x 256, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
-// cfg 8: 256 x 128, two waves per SIMD, 16x16x32 MFMA (gemm_occ2.hip)
-// cfg 9: 256 x 224, 8 waves sharing an LDS-dequantised weight tile (gemm_ldsb.hip)
-// cfg 10: 256 x 256, as cfg 9
 // cfg 11: 128 x 256 as cfg 7, packed weights streamed into LDS four k-steps
 //         ahead (gemm_stream.hip)
 // cfg 12:  32 x 256, the cfg 11 kernel with 2 m-tiles per wave (small M)
 // cfg 13:  64 x 256, the cfg 11 kernel with 4 m-tiles per wave
+// Numbers 0, 3, 4, 5, 8, 9 and 10 belonged to tilings that measured slower
+// on every shape and were retired; a plan naming them is refused.
 MfmaTile mfma_tile(int cfg) {
   switch (cfg) {
-    case 0: return {128, 512};
     case 1: return {128, 256};
     case 2: return {32, 512};
-    case 4: return {256, 256};
-    case 5: return {256, 128};
     case 6: return {128, 256};
     case 7: return {128, 256};
-    case 8: return {256, 128};
-    case 9: return {256, 224};
-    case 10: return {256, 256};
     case 11: return {128, 256};
     case 12: return {32, 256};
     case 13: return {64, 256};
-    default: return {64, 512};
+    default: return {0, 0};
   }
 }
 
-bool mfma_cfg_splits(int cfg) { return cfg == 7 || cfg == 8 || cfg >= 11; }
+bool mfma_cfg_splits(int cfg) { return cfg == 7 || cfg >= 11; }
 
 bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
-  if (cfg < 0 || cfg >= kMfmaConfigs) return false;
-  if (cfg == 4) return lds_gemm_applicable(M, N, K, G);
-  if (cfg == 5 || cfg == 6) return K % (2 * kBK) == 0;
-  if (cfg == 7 || cfg == 8) return occ2_gemm_applicable(M, N, K, G);
-  if (cfg == 9 || cfg == 10) return ldsb_gemm_applicable(M, N, K, G);
-  if (cfg >= 11) return stream_gemm_applicable(M, N, K, G);
-  return true;
+  switch (cfg) {
+    case 1:
+    case 2: return true;
+    case 6: return K % (2 * kBK) == 0;
+    case 7: return occ2_gemm_applicable(M, N, K, G);
+    case 11:
+    case 12:
+    case 13: return stream_gemm_applicable(M, N, K, G);
+    default: return false;
+  }
 }
 
 bool operands_fit(int M, int N, int K, int G) {
@@ -578,23 +571,12 @@ bool mfma_fits(int M, int N, int K, int G) { return operands_fit(M, N, K, G); }
 hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st) {
   if (split > 1 && !mfma_cfg_splits(cfg)) return hipErrorInvalidValue;
   switch (cfg) {
-    case 0: return launch_cfg<4, 1, 4>(a, st);
     case 1: return launch_cfg<2, 2, 2>(a, st);
     case 2: return launch_cfg<1, 1, 4>(a, st);
-    case 3: return launch_cfg<2, 1, 4>(a, st);
-    case 4:
-      if (!lds_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
-      return launch_lds_gemm(a, st);
-    case 5:
-      if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
-      return launch_occ2<4, 2, 2>(a, st);
     case 6:
       if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
       return launch_occ2<4, 1, 4>(a, st);
-    case 7: return launch_occ2_gemm(a, false, split, part, st);
-    case 8: return launch_occ2_gemm(a, true, split, part, st);
-    case 9: return launch_ldsb_gemm(a, false, st);
-    case 10: return launch_ldsb_gemm(a, true, st);
+    case 7: return launch_occ2_gemm(a, split, part, st);
     case 11: return launch_stream_gemm(a, 128, split, part, st);
     case 12: return launch_stream_gemm(a, 32, split, part, st);
     case 13: return launch_stream_gemm(a, 64, split, part, st);

@@ -343,18 +343,13 @@ size_t occ2_workspace_bytes(int M, int N, int K, int split) {
   return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-// waves 1 x 4: 128 x 256 tiles; waves 2 x 2: 256 x 128 tiles.  split > 1:
-// fp32 partials in `part` (occ2_workspace_bytes), then launch_splitk_reduce.
-hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
-                            hipStream_t st) {
+// waves 1 x 4: 128 x 256 tiles.  split > 1: fp32 partials in `part`
+// (occ2_workspace_bytes), then launch_splitk_reduce.
+hipError_t launch_occ2_gemm(const GemmArgs& a, int split, float* part, hipStream_t st) {
   if (!occ2_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
   if (occ2_splits(a.K, split) > 1 && !part) return hipErrorInvalidValue;
-  const bool g64 = a.G % 64 == 0;
-  if (tall)
-    return g64 ? launch_wg<2, 2, true>(a, split, part, st)
-               : launch_wg<2, 2, false>(a, split, part, st);
-  return g64 ? launch_wg<1, 4, true>(a, split, part, st)
-             : launch_wg<1, 4, false>(a, split, part, st);
+  return a.G % 64 == 0 ? launch_wg<1, 4, true>(a, split, part, st)
+                       : launch_wg<1, 4, false>(a, split, part, st);
 }
 
 }  // namespace w4a16

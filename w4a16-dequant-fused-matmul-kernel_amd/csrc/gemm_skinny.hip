@@ -1,23 +1,30 @@
-// Skinny-M W4A16 GEMM (9 <= M <= 64) on gfx950 matrix cores
-// (v_mfma_f32_16x16x32_f16), weights streamed from HBM.
+// Skinny-M W4A16 GEMM (3 <= M <= 64 by the planner's choice; any M <= 64 by
+// plan) on gfx950 matrix cores (v_mfma_f32_16x16x32_f16), weights streamed
+// from HBM.
 //
 // Replaces the small-batch regime of the reference's fused kernel
 // (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 with BLOCK_M = 16..64).
 //
 // At these M the GEMM is still bound by the weight stream, and a prefill tiling
 // (hundreds of rows per workgroup) leaves most CUs idle.  Here:
-//   * a workgroup owns 16 columns and the whole of K, so N = 4096 already gives
-//     256 workgroups and no cross-workgroup reduction is needed;
+//   * a workgroup of 4 waves owns a block of columns and the whole of K, so no
+//     cross-workgroup reduction is needed.  Block widths (plan tile_cfg):
+//     - cfg 0: 16 columns, one per lane: one 4-byte weight load per lane and
+//       32-k step, 2-byte scale / zero loads (N = 4096 gives 256 workgroups);
+//     - cfg 2: 32 columns (M <= 32, N even), two adjacent columns per lane: one
+//       8-byte weight load, 4-byte scale / zero loads, and the lane's
+//       activation fragment feeds both n-tiles (X streamed once per 32
+//       columns);
+//     - cfg 3: 64 columns (M <= 16, N % 4 == 0), four columns per lane: one
+//       16-byte weight load, 8-byte scale / zero loads;
 //   * in v_mfma_f32_16x16x32_f16 lane l holds B[k = 8*(l/16)..+7][n = l%16]: one
-//     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA,
-//     reading 4 packed rows x 64 bytes with one dword load per lane;
-//   * the 4 waves (8 for M <= 32 when there is about one workgroup per CU:
-//     two per SIMD, twice the loads in flight) split K into contiguous runs of
-//     whole batches; each wave walks its run in
-//     batches of 8 k-steps (256 k) with two register batches used ping-pong, all
-//     loads of batch i+1 -- weights, scales, zeros and activations -- issued
-//     before batch i is consumed, unconditionally (past the range they read
-//     zeros), so the compiler's wait counts are exact;
+//     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA
+//     and n-tile, reading 4 packed rows of its block per load;
+//   * the 4 waves split K into contiguous runs of whole batches; each wave
+//     walks its run in batches of 8 k-steps (256 k) with two register batches
+//     used ping-pong, all loads of batch i+1 -- weights, scales, zeros and
+//     activations -- issued before batch i is consumed, unconditionally (past
+//     the range they read zeros), so the compiler's wait counts are exact;
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
 //     the buffer range check;
@@ -27,7 +34,9 @@
 //     (deterministic) and rounded to fp16 once; optional fp16 bias add;
 //   * workgroup -> column block is XCD-aware (consecutive blocks share an XCD).
 // Requirements (checked by the caller): G % 32 == 0, K % G == 0, 16-byte
-// aligned x, and x, qweight, scales, zeros each below 2 GiB.  Any N.
+// aligned x, qweight aligned to the weight load (4 / 8 / 16 bytes for cfg
+// 0 / 2 / 3) and scales / zeros to theirs (2 / 4 / 8 bytes), and x, qweight,
+// scales, zeros each below 2 GiB.  Any N (cfg 2: even, cfg 3: N % 4 == 0).
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -226,7 +235,6 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 
 template <int MT, int GSTEP>
 hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
-  const bool eight_waves = cfg == 1;
   if constexpr (MT <= 2) {
     if (cfg == 2) {   // 32-column blocks
       const int nblk2 = (a.N + 31) / 32;
@@ -250,18 +258,6 @@ hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
     }
   }
   const int nblk = (a.N + 15) / 16;
-  // 8 waves (M <= 32 only, register budget): two per SIMD, twice the weight
-  // loads in flight per CU -- pays when there is about one workgroup per CU
-  if constexpr (MT <= 2) {
-    if (eight_waves) {
-      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 8, 1>), dim3(nblk), dim3(512), 0, st,
-                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                         a.G, nblk, a.ldx, a.ldy);
-      return hipGetLastError();
-    }
-  }
   hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 1>), dim3(nblk), dim3(256), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
@@ -285,11 +281,11 @@ hipError_t launch_mt(const GemmArgs& a, int cfg, hipStream_t st) {
 
 }  // namespace
 
-// cfg 0: 4 waves, 16-column blocks; 1: 8 waves (M <= 32); 2: 4 waves,
-// 32-column blocks (M <= 32, N even); 3: 4 waves, 64-column blocks (M <= 16,
-// N % 4 == 0)
+// cfg 0: 16-column blocks; 2: 32-column blocks (M <= 32, N even); 3:
+// 64-column blocks (M <= 16, N % 4 == 0); 4 waves each.  cfg 1 (8 waves on
+// 16-column blocks) measured slower on every shape and was retired.
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st) {
-  if (cfg < 0 || cfg > 3 || (cfg >= 1 && a.M > 32) || (cfg == 2 && a.N % 2 != 0) ||
+  if (!(cfg == 0 || cfg == 2 || cfg == 3) || (cfg == 2 && (a.M > 32 || a.N % 2 != 0)) ||
       (cfg == 3 && (a.M > 16 || a.N % 4 != 0)))
     return hipErrorInvalidValue;
   switch ((a.M + 15) / 16) {

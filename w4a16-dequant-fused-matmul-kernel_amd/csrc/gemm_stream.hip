@@ -476,7 +476,7 @@ hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* par
   const uintptr_t sc = reinterpret_cast<uintptr_t>(a.sc), zr = reinterpret_cast<uintptr_t>(a.zr);
   const uint64_t dist = sc < zr ? zr - sc : sc - zr;
   const uint64_t bytes = (uint64_t)(a.K / a.G) * (uint64_t)a.N * 2u;
-  if (dist + bytes >= (1ull << 31)) return launch_occ2_gemm(a, false, split, part, st);
+  if (dist + bytes >= (1ull << 31)) return launch_occ2_gemm(a, split, part, st);
   switch (rows) {
     case 128: return launch_wg<8>(a, split, part, st);
     case 64: return launch_wg<4>(a, split, part, st);

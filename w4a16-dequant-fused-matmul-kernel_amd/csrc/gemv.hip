@@ -8,7 +8,7 @@
 //     in a wave, CWL lanes cover one packed row (one dwordx4 = 4 columns per
 //     lane) and the wave's 64/CWL row-lanes sit on different packed rows;
 //   * each row-lane owns a contiguous run of packed rows, cut into batches of BR
-//     rows (8 with 4 waves, 4 with 8 waves) aligned to absolute multiples of BR.
+//     rows (4 with 8 waves, 2 with 16 waves) aligned to absolute multiples of BR.
 //     With G % 32 == 0 every 4-row half (32 k) lies in one quantisation group,
 //     so a batch needs one scale/zero load per half;
 //   * every load of batch i+1 is issued before batch i is consumed, in the order
@@ -26,10 +26,10 @@
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
 //     so that neighbouring row segments share that XCD's L2 lines;
-//   * optional split-K (forced through a plan; the automatic plan does not split:
-//     at decode sizes the extra pass costs more than the parallelism gains):
-//     each workgroup writes fp32 partials and a second kernel sums the splits
-//     in split order (deterministic).
+//   * split-K where the column blocks cannot fill the CUs and K is long (the
+//     planner's rule; a plan can also force it): each workgroup writes fp32
+//     partials and a second kernel sums the splits in split order
+//     (deterministic).
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -43,7 +43,7 @@ template <int WAVES>
 struct GemvShape {
   static constexpr int kThreads = 64 * WAVES;
   // packed rows per batch: fewer rows per lane as the wave count grows
-  static constexpr int kBatch = WAVES >= 16 ? 2 : WAVES >= 8 ? 4 : 8;
+  static constexpr int kBatch = WAVES >= 16 ? 2 : 4;
 };
 
 template <int MT, int CWL, int WAVES, bool STAGE>
@@ -356,34 +356,30 @@ hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_
   }
 }
 
-// cfg % 3 picks 4, 8 or 16 waves; cfg >= 3 stages the activations in LDS for
-// M <= 2 (larger M always stages them).  16 waves only for M <= 2 (the
-// reduction buffer grows with waves x M).
+// cfg 1 / 2: 8 / 16 waves; cfg 4 / 5: the same with the activations staged in
+// LDS for M <= 2 (larger M always stages them).  16 waves only for M <= 2
+// (the reduction buffer grows with waves x M).  cfg 0 / 3 (4 waves) measured
+// slower everywhere and were retired.
 template <int MT>
 hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {
   if constexpr (MT <= 2) {
     switch (cfg) {
-      case 0: return launch_w<MT, 4, false>(a, cols, split, ws, st);
       case 1: return launch_w<MT, 8, false>(a, cols, split, ws, st);
       case 2: return launch_w<MT, 16, false>(a, cols, split, ws, st);
-      case 3: return launch_w<MT, 4, true>(a, cols, split, ws, st);
       case 4: return launch_w<MT, 8, true>(a, cols, split, ws, st);
       case 5: return launch_w<MT, 16, true>(a, cols, split, ws, st);
       default: return hipErrorInvalidValue;
     }
   } else {
-    switch (cfg) {
-      case 0: return launch_w<MT, 4, false>(a, cols, split, ws, st);
-      case 1: return launch_w<MT, 8, false>(a, cols, split, ws, st);
-      default: return hipErrorInvalidValue;
-    }
+    if (cfg != 1) return hipErrorInvalidValue;
+    return launch_w<MT, 8, false>(a, cols, split, ws, st);
   }
 }
 
 }  // namespace
 
 bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 || cols == 256; }
-bool gemv_cfg_valid(int cfg, int M) { return cfg >= 0 && cfg < kGemvConfigs && (cfg < 2 || M <= 2); }
+bool gemv_cfg_valid(int cfg, int M) { return cfg == 1 || (M <= 2 && (cfg == 2 || cfg == 4 || cfg == 5)); }
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;

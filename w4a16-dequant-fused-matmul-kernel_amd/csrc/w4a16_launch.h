@@ -43,10 +43,10 @@ inline uint64_t x_extent_bytes(const GemmArgs& a) {
 
 // Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
 // consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
-// picks 4 (cfg 0), 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup, and
-// cfg 3..5 the same with the activations staged in LDS (M <= 2; larger M
-// always stages them); with split > 1, `ws` holds the fp32 partials of
-// gemv_workspace_bytes().
+// picks 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup, and cfg 4 / 5
+// the same with the activations staged in LDS (M <= 2; larger M always
+// stages them); cfg 0 and 3 (4 waves) were retired.  With split > 1, `ws`
+// holds the fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
 constexpr int kGemvConfigs = 6;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
@@ -60,31 +60,32 @@ int gemv_rows_per_split(int K, int split);
 hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws,
                        hipStream_t st);
 
-// Prefill GEMM on MFMA (v_mfma_f32_32x32x16_f16).  `cfg` picks the tile shape.
+// Prefill GEMM on MFMA.  `cfg` picks the tiling (mfma_tile): 1, 2 (one wave
+// per SIMD, 32x32x16), 6 (two waves per SIMD, 32x32x16), 7 (two waves per
+// SIMD, 16x16x32, gemm_occ2.hip), 11 / 12 / 13 (128- / 32- / 64-row tiles with
+// activations and packed weights streamed into LDS, gemm_stream.hip).  Other
+// numbers are refused (retired tilings).
 struct MfmaTile {
   int bm, bn;
 };
 constexpr int kMfmaConfigs = 14;
 MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
-// Whether tile configuration `cfg` can run this shape (some need K % 64 or 128).
+// Whether tile configuration `cfg` exists and can run this shape (some need
+// K % 64, 128 or 256).
 bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G);
 // Configurations with a split-K form (fp32 partials, occ2_workspace_bytes()).
 bool mfma_cfg_splits(int cfg);
-// split > 1 (cfg 7 and 8 only): fp32 partials in `part`, occ2_workspace_bytes().
+// split > 1 (cfg 7, 11-13 only): fp32 partials in `part`, occ2_workspace_bytes().
 hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st);
-// The 256 x 256 LDS-staged-weight kernel (mfma cfg 4): needs K % 64 == 0.
-bool lds_gemm_applicable(int M, int N, int K, int G);
-hipError_t launch_lds_gemm(const GemmArgs& a, hipStream_t st);
 // Split-K epilogue shared by the GEMV and the prefill kernels: y[M, N] =
 // fp16(sum of the S fp32 partials [S][M][N], in split order) (+ fp16 bias).
 // N % 4 == 0.
 hipError_t launch_splitk_reduce(const float* part, const void* bias, void* y, int M, int N, int ldy,
                                 int S, hipStream_t st);
-// Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256, cfg 8: 256 x 128):
-// needs K % 64 == 0.
+// Two-waves-per-SIMD 16x16x32 kernel (mfma cfg 7: 128 x 256): needs K % 64 == 0.
 bool occ2_gemm_applicable(int M, int N, int K, int G);
-// Split-K of cfg 7/8: the number of non-empty k-splits for a requested count,
+// Split-K of cfg 7: the number of non-empty k-splits for a requested count,
 // and the fp32 partial buffer they need (0 when not split).
 int occ2_splits(int K, int split);
 size_t occ2_workspace_bytes(int M, int N, int K, int split);
@@ -98,19 +99,19 @@ int stream_splits(int K, int split);
 // rows = 128, 64 or 32 (tile rows of cfg 11, 13, 12).
 hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* part,
                               hipStream_t st);
-hipError_t launch_occ2_gemm(const GemmArgs& a, bool tall, int split, float* part,
-                            hipStream_t st);
-// Eight-wave kernel with the weight tile dequantised into LDS (mfma cfg 9:
-// 256 x 224, cfg 10: 256 x 256): needs K % 64 == 0.
-bool ldsb_gemm_applicable(int M, int N, int K, int G);
-hipError_t launch_ldsb_gemm(const GemmArgs& a, bool wide, hipStream_t st);
+hipError_t launch_occ2_gemm(const GemmArgs& a, int split, float* part, hipStream_t st);
 
 // Buffer-addressed kernels need every operand below 2 GiB.
 bool operands_fit(int M, int N, int K, int G);
 
-// Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM.
+// Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM,
+// 4 waves per workgroup over the whole of K.  cfg 0: 16-column blocks (one
+// column per lane, 4-byte weight loads, 2-byte scale / zero loads); cfg 2:
+// 32-column blocks (M <= 32, N even: two columns per lane, 8-byte weight
+// loads, 4-byte scale / zero loads); cfg 3: 64-column blocks (M <= 16,
+// N % 4 == 0: four columns per lane, 16-byte weight loads, 8-byte scale /
+// zero loads).  cfg 1 (8 waves) was retired.
 constexpr int kSkinnyMaxM = 64;
-// cfg 0: 4 waves per workgroup; cfg 1: 8 waves (M <= 32).
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st);
 
 // Sequential-k SIMT kernel: any N, any G dividing K, no alignment needs.

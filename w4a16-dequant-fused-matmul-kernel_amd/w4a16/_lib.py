@@ -20,8 +20,11 @@ ABI_VERSION = 1
 KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT, KERNEL_SKINNY = 0, 1, 2, 3, 4
 KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
                 KERNEL_SKINNY: "skinny"}
-# MFMA tile configurations 0 .. MFMA_CONFIGS-1 (w4a16_plan.tile_cfg)
-MFMA_CONFIGS = 14
+# plan tile_cfg numbers each family has (others are refused: retired tilings)
+MFMA_CONFIGS = (1, 2, 6, 7, 11, 12, 13)
+MFMA_SPLIT_CONFIGS = (7, 11, 12, 13)
+GEMV_CONFIGS = (1, 2, 4, 5)          # 8 / 16 waves, + LDS-staged activations (M <= 2)
+SKINNY_CONFIGS = (0, 2, 3)           # 16 / 32 / 64-column blocks
 # W4A16_NOALLOC_SCRATCH_BYTES: the static scratch of w4a16_gemm_f16_noalloc
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
