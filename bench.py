@@ -1,22 +1,38 @@
 """Benchmark of the W4A16 fused dequant-GEMM on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--sweep]
+    python bench.py --reference-table [--reference-json PATH]
 
 Prints ONE JSON line.  Headline (``value``): HBM GB/s of the decode GEMV at
 BASELINE config C2 (M=1, K=N=4096, G=128) -- algorithmic bytes per call
 (2MK + 4(K/8)N + 4(K/G)N + 2MN, reference bench_gemm.py:61-67) over the average
-kernel time.  Timing:
+time per call.  Timing of the K steps:
 
-* weights cold: the call cycles over enough copies of (qweight, scales, zeros)
-  that they total > 512 MiB, so the 256 MiB Infinity Cache cannot hold them;
-* the K timed calls are captured once into a HIP graph and replayed, bracketed
-  by HIP events recorded on the stream the kernels run on, so host launch
-  overhead is not in the figure; ``ms_per_step`` = event time / K;
-* ``secondary``: TFLOP/s of the prefill MFMA GEMM at C4 M=4096 (2MNK flops);
+* weights cold: the calls cycle over enough copies of (qweight, scales, zeros)
+  that they total > 512 MiB, and right before the timed calls one untimed call
+  reads every copy in order, so the copy each timed call reads was last read
+  (copies) calls -- more than 512 MiB of other weights -- earlier: the 256 MiB
+  Infinity Cache cannot hold it, at any K;
+* the W warm-up calls, the rotation and the K timed calls are eager launches
+  on one stream, all queued behind a bounded spin kernel (torch.cuda._sleep)
+  so the host has issued every one before the GPU starts: the GPU runs them
+  back to back, busy up to the timed calls, and the figure holds neither the
+  host's launch cost (~12 us per Python call) nor a graph launch.  HIP events
+  on that stream bracket exactly the K calls; ``ms_per_step`` = event time / K;
+* ``secondary``: TFLOP/s of the prefill MFMA GEMM at C4 M=4096 (2MNK flops),
+  its calls timed as one HIP-graph replay (SECONDARY_GRAPH says why);
 * ``cpu_baseline``: the CPU oracle's dequantise-then-matmul path
   (``oracle/w4a16_oracle.reference_w4a16``, a numpy port of the reference's
-  reference.py:18-40) on the same C2 inputs, single-threaded, timed on this
-  host over a bounded number of calls.
+  reference.py:18-40) on the same C2 inputs, on every host core the process may
+  use (columns split over threads: GEMM columns are independent), over a
+  bounded number of calls.
+
+``--reference-table`` instead reproduces the reference's own benchmark
+(w4a16-kernel/benchmarks/bench_gemm.py): its method (warm weights, eager
+calls, 25 warm-up calls, median of 100 calls each bracketed by events and a
+synchronize), its result keys (fp16_ms, dequant_matmul_ms, w4a16_ms, ...,
+speedup_vs_fp16, speedup_vs_dequant) and its markdown table, over its
+DEFAULT_SHAPES and the BASELINE configurations' shapes.
 """
 from __future__ import annotations
 
@@ -35,6 +51,13 @@ for _p in (ROOT, PKG_DIR):
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2516.6      # MI355X dense fp16 MFMA
 COLD_BYTES = 512 << 20
+SPIN_CYCLES_PER_US = 2500      # the spin kernel counts shader clocks (<= 2.4 GHz)
+# The prefill line runs as one graph replay: its kernels run ~6 % faster inside a
+# graph than as separate eager dispatches (kernel trace, C4 M=4096: median 400.6
+# vs 421.7 us), and at ~0.4 ms per call the replay's launch (~9 us) is 0.5 % of
+# 50 calls.  The decode headline runs eager: there the graph's launch would be
+# 0.45 us of a ~5 us call at K = 20.
+SECONDARY_GRAPH = True
 
 
 def _args():
@@ -47,7 +70,12 @@ def _args():
     ap.add_argument("--sweep", action="store_true",
                     help="also time every C2-C5 case (stderr table, --sweep-json file)")
     ap.add_argument("--sweep-json", default=None)
-    ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
+    ap.add_argument("--graph", action="store_true",
+                    help="time one HIP-graph replay of the K calls instead of eager calls "
+                         "(includes the graph's launch latency)")
+    ap.add_argument("--reference-table", action="store_true",
+                    help="the reference's bench_gemm.py method, keys and markdown table")
+    ap.add_argument("--reference-json", default=None, help="write the --reference-table rows here")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the workload for rocprofv3 --pmc: a 256 MiB copy (calibration), "
                          "8 cold C2 decode calls, 3 C4 M=4096 prefill calls; no timing")
@@ -58,37 +86,66 @@ def _args():
     return ap.parse_args()
 
 
-def _time_calls(fns, steps: int, warmup: int, graph: bool):
-    """Average ms per call of `fns` (cycled), HIP events on the launch stream."""
+def _time_calls(fns, steps: int, warmup: int, graph: bool) -> dict:
+    """Average ms per call of `fns` (call i runs fns[i % len(fns)]), HIP events
+    on the stream the kernels run on.
+
+    In order on one stream: W warm-up calls, one call on every element of
+    `fns` in order (the rotation that leaves the timed calls' weights cold),
+    then the K timed calls between two events.  All of it is queued behind one
+    spin kernel, sized from the host's measured launch rate, so the GPU runs
+    warm-up, rotation and timed calls back to back -- busy (and clocked up)
+    right to the start event -- and none waits on the host; if the GPU reached
+    the start event before the host had queued everything, the whole sequence
+    runs again behind a longer spin.  Eager (default): the K calls are K
+    launches.  Graph: they are one graph, replayed once untimed beforehand."""
     import torch
 
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        for i in range(max(warmup, len(fns))):
-            fns[i % len(fns)]()
+        fns[0]()                             # first call: plan, workspace, code load
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for f in fns:                        # untimed: the host's launch rate
+            f()
+        host_us = (time.perf_counter() - t0) / len(fns) * 1e6
     stream.synchronize()
+    g = None
     if graph:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
             for i in range(steps):
                 fns[i % len(fns)]()
         with torch.cuda.stream(stream):
-            g.replay()                      # one untimed replay
+            g.replay()                      # untimed: uploads the graph
         stream.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        if graph:
-            g.replay()
-        else:
-            for i in range(steps):
+    n_queued = warmup + len(fns) + (1 if graph else steps)
+    for attempt in range(4):
+        spin_us = (200 + 2 * host_us * n_queued) * 4 ** attempt
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(int(SPIN_CYCLES_PER_US * spin_us))
+            for i in range(warmup):
                 fns[i % len(fns)]()
-        end.record(stream)
-    end.synchronize()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+            for f in fns:                        # rotation: every copy, in order
+                f()
+            start.record(stream)
+            if graph:
+                g.replay()
+            else:
+                for i in range(steps):
+                    fns[i % len(fns)]()
+            end.record(stream)
+            # the GPU must not have reached the start event before every call
+            # was queued, or the timed calls would have waited on the host
+            queued = not start.query()
+        end.synchronize()
+        torch.cuda.synchronize()
+        if queued:
+            break
+    return {"ms": start.elapsed_time(end) / steps, "queued_before_start": queued,
+            "host_us_per_call": host_us, "spin_us": spin_us}
 
 
 def _prepare(case, copies_for_cold: bool):
@@ -105,52 +162,214 @@ def _prepare(case, copies_for_cold: bool):
         ncopy = max(2, -(-COLD_BYTES // per_copy) + 1)
     layers = [(qw, s, z)] + [(qw.clone(), s.clone(), z.clone()) for _ in range(ncopy - 1)]
     y = torch.empty(case.M, case.N, dtype=torch.float16, device="cuda")
-    return X, W, Xd, layers, y, ncopy
+    return X, W, Xd, layers, y, ncopy, per_copy
 
 
-def bench_case(case, steps: int, warmup: int, graph: bool = True, cold: bool = True) -> dict:
+def bench_case(case, steps: int, warmup: int, graph: bool = False, cold: bool = True) -> dict:
     from w4a16 import w4a16_matmul
     from w4a16.hip_kernel import plan_for
 
-    X, W, Xd, layers, y, ncopy = _prepare(case, cold)
+    X, W, Xd, layers, y, ncopy, per_copy = _prepare(case, cold)
     fns = [(lambda l=l: w4a16_matmul(Xd, l[0], l[1], l[2], case.G, out=y)) for l in layers]
-    ms = _time_calls(fns, steps, warmup, graph)
+    t = _time_calls(fns, steps, warmup, graph)
+    ms = t["ms"]
     p = plan_for(case.M, case.N, case.K, case.G).as_dict()
     us = ms * 1e3
     gbs = case.bytes() / (ms * 1e-3) / 1e9
     tflops = case.flops() / (ms * 1e-3) / 1e12
     return {"case": case.name, "M": case.M, "K": case.K, "N": case.N, "G": case.G,
-            "us": us, "GB/s": gbs, "TFLOP/s": tflops, "weight_copies": ncopy,
-            "kernel": p["kernel_name"], "split_k": p["split_k"], "tile": [p["tile_m"], p["tile_n"]],
-            "grid": [p["grid_x"], p["grid_y"]], "bytes": case.bytes(), "flops": case.flops()}
+            "steps": steps, "us": us, "GB/s": gbs, "TFLOP/s": tflops, "weight_copies": ncopy,
+            "copy_mib": per_copy / 2**20, "queued_before_start": t["queued_before_start"],
+            "graph": graph, "host_us_per_call": round(t["host_us_per_call"], 1),
+            "kernel": p["kernel_name"], "split_k": p["split_k"], "tile_cfg": p["tile_cfg"],
+            "tile": [p["tile_m"], p["tile_n"]], "grid": [p["grid_x"], p["grid_y"]],
+            "bytes": case.bytes(), "flops": case.flops()}
+
+
+def _cold_note(r: dict) -> str:
+    if r["weight_copies"] <= 1:
+        return "warm: one copy of the weights"
+    n = r["weight_copies"]
+    return (f"cold: {n} rotating copies ({n * r['copy_mib']:.0f} MiB); each timed call's copy "
+            f"was last read {n} calls ({(n - 1) * r['copy_mib']:.0f} MiB of other weights) earlier")
+
+
+def _host_cpus() -> tuple[int, int, str]:
+    """(threads to use, CPUs in this process's affinity mask, CPU model).  The
+    thread count is the affinity mask, capped by OMP_NUM_THREADS where the
+    host sets it (the GPU box's CPU share)."""
+    n_aff = len(os.sched_getaffinity(0))
+    n = n_aff
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+        if cap > 0:
+            n = min(n, cap)
+    except ValueError:
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(1, n), n_aff, model
 
 
 def cpu_baseline(case, budget_s: float = 12.0, max_calls: int = 40) -> dict:
-    """The oracle's dequantise-then-matmul path on the host, one thread."""
+    """The oracle's dequantise-then-matmul path on the host's cores: the N
+    columns split into one contiguous chunk per thread (columns of a GEMM are
+    independent), each chunk through oracle.reference_w4a16 with a
+    single-threaded BLAS."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import w4a16_oracle as O
     from w4a16 import workloads as wl
 
+    threads, n_aff, model = _host_cpus()
     X, W = wl.make_inputs(case)
     qw, s, z = O.quantize_weight(W.numpy(), case.G)
     Xn = X.numpy()
+    bounds = np.linspace(0, case.N, threads + 1).astype(int)
+    chunks = [(np.ascontiguousarray(qw[:, a:b]), np.ascontiguousarray(s[:, a:b]),
+               np.ascontiguousarray(z[:, a:b])) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
+
+    def run(pool):
+        parts = list(pool.map(lambda c: O.reference_w4a16(Xn, c[0], c[1], c[2], case.G), chunks))
+        return np.concatenate(parts, axis=1)
+
     times = []
-    with threadpool_limits(limits=1):
-        O.reference_w4a16(Xn, qw, s, z, case.G)       # warm-up
+    with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=len(chunks)) as pool:
+        y = run(pool)                                  # warm-up
+        ref = O.reference_w4a16(Xn, qw, s, z, case.G)
+        assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)) or \
+            O.within_tolerance(y, ref).all()
         t_end = time.perf_counter() + budget_s
         while len(times) < max_calls and time.perf_counter() < t_end:
             t0 = time.perf_counter()
-            O.reference_w4a16(Xn, qw, s, z, case.G)
+            run(pool)
             times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    return {"value": case.bytes() / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": case.bytes() / med / 1e9, "unit": "GB/s", "cores": len(chunks),
+            "kind": "port",
             "sample": f"{len(times)} calls of oracle reference_w4a16 on the {case.name} inputs "
-                      f"(numpy, 1 thread), median {med * 1e3:.2f} ms/call",
-            "ms_per_call": med * 1e3}
+                      f"(numpy; N split over {len(chunks)} threads, BLAS 1 thread each), "
+                      f"median {med * 1e3:.2f} ms/call",
+            "ms_per_call": med * 1e3, "cpu_model": model, "host_cpus": n_aff}
 
 
+# --------------------------------------------------------------------------- #
+# the reference's benchmark (bench_gemm.py), reproduced                         #
+# --------------------------------------------------------------------------- #
+# bench_gemm.py:31-40
+REF_DEFAULT_SHAPES = [(1, 4096, 4096), (1, 4096, 11008), (1, 11008, 4096), (64, 4096, 4096),
+                      (256, 4096, 4096), (256, 4096, 11008), (256, 11008, 4096)]
+
+
+def _ref_time_ms(fn, warmup: int = 25, iters: int = 100) -> float:
+    """bench_gemm.py:43-58: median of `iters` calls, each bracketed by events on
+    the current stream and a synchronize."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for _ in range(iters):
+        start.record()
+        fn()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def reference_row(M: int, K: int, N: int, G: int = 128, source: str = "bench_gemm") -> dict:
+    """bench_gemm.py:70-99 for one shape: X, W ~ N(0, 1) fp16 on the GPU, W
+    quantised (HIP kernel); fp16_matmul (hipBLASLt), dequant_then_matmul (HIP
+    dequant + hipBLASLt) and the fused w4a16_matmul, each timed the
+    reference's way; the same result keys."""
+    import torch
+    from w4a16 import dequant_then_matmul, fp16_matmul, quantize_weight, w4a16_matmul
+
+    g = torch.Generator(device="cuda").manual_seed(M * 131 + K * 7 + N)
+    X = torch.randn(M, K, dtype=torch.float16, device="cuda", generator=g)
+    W = torch.randn(K, N, dtype=torch.float16, device="cuda", generator=g)
+    qw, s, z = quantize_weight(W, G)
+    t_fp16 = _ref_time_ms(lambda: fp16_matmul(X, W))
+    t_dq = _ref_time_ms(lambda: dequant_then_matmul(X, qw, s, z, G))
+    t_w4 = _ref_time_ms(lambda: w4a16_matmul(X, qw, s, z, G))
+    flops = 2.0 * M * N * K
+    ng = K // G
+    b_w4 = M * K * 2 + (K // 8) * N * 4 + 2 * ng * N * 2 + M * N * 2
+    b_fp16 = M * K * 2 + K * N * 2 + M * N * 2
+    del W
+    return {"M": M, "K": K, "N": N, "group_size": G, "source": source,
+            "fp16_ms": t_fp16, "dequant_matmul_ms": t_dq, "w4a16_ms": t_w4,
+            "w4a16_tflops": flops / (t_w4 * 1e-3) / 1e12,
+            "fp16_tflops": flops / (t_fp16 * 1e-3) / 1e12,
+            "w4a16_gbps": b_w4 / (t_w4 * 1e-3) / 1e9,
+            "fp16_gbps": b_fp16 / (t_fp16 * 1e-3) / 1e9,
+            "speedup_vs_fp16": t_fp16 / t_w4,
+            "speedup_vs_dequant": t_dq / t_w4}
+
+
+def to_markdown_table(results: list[dict]) -> str:
+    """The reference's table (bench_gemm.py:102-117)."""
+    header = (
+        "| M | K | N | w4a16 (ms) | fp16 (ms) | dequant+mm (ms) | "
+        "w4a16 TFLOPS | w4a16 GB/s | speedup vs fp16 | speedup vs dequant |\n"
+        "|---|---|---|-----------|-----------|-----------------|"
+        "--------------|------------|-----------------|--------------------|\n")
+    rows = [f"| {r['M']} | {r['K']} | {r['N']} | {r['w4a16_ms']:.3f} | {r['fp16_ms']:.3f} | "
+            f"{r['dequant_matmul_ms']:.3f} | {r['w4a16_tflops']:.1f} | {r['w4a16_gbps']:.0f} | "
+            f"{r['speedup_vs_fp16']:.2f}x | {r['speedup_vs_dequant']:.2f}x |" for r in results]
+    return header + "\n".join(rows) + "\n"
+
+
+def reference_table(json_path: str | None) -> dict:
+    from w4a16 import workloads as wl
+
+    shapes = [(M, K, N, 128, "bench_gemm DEFAULT_SHAPES") for (M, K, N) in REF_DEFAULT_SHAPES]
+    seen = {(M, K, N) for (M, K, N, _, _) in shapes}
+    for c in wl.cases("C2", "C3", "C4", "C5"):
+        if c.G == 128 and (c.M, c.K, c.N) not in seen:
+            seen.add((c.M, c.K, c.N))
+            shapes.append((c.M, c.K, c.N, 128, c.config))
+    rows = []
+    for M, K, N, G, src in shapes:
+        r = reference_row(M, K, N, G, src)
+        rows.append(r)
+        print(f"M={M:<5} K={K:<6} N={N:<6} | w4a16 {r['w4a16_ms']:.4f}ms "
+              f"({r['w4a16_tflops']:.1f} TF, {r['w4a16_gbps']:.0f} GB/s) | "
+              f"fp16 {r['fp16_ms']:.4f}ms | dq {r['dequant_matmul_ms']:.4f}ms | "
+              f"vs fp16 {r['speedup_vs_fp16']:.2f}x, vs dequant {r['speedup_vs_dequant']:.2f}x",
+              file=sys.stderr, flush=True)
+    print("\n" + to_markdown_table(rows), file=sys.stderr, flush=True)
+    if json_path:
+        with open(json_path, "w") as f:
+            json.dump(rows, f, indent=1)
+    return {"metric": "reference bench_gemm.py schema (warm weights, eager, median of 100)",
+            "device": _device_name(), "rows": rows}
+
+
+def _device_name() -> str:
+    import torch
+
+    return torch.cuda.get_device_name(0)
+
+
+# --------------------------------------------------------------------------- #
+# HBM traffic from rocprofv3 counters                                           #
+# --------------------------------------------------------------------------- #
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -167,7 +386,7 @@ def traffic_probe() -> None:
     torch.cuda.synchronize()
     print("copy 256 MiB x3", flush=True)
     c2 = wl.CONFIGS["C2"][0]
-    X, W, Xd, layers, y, _ = _prepare(c2, True)
+    X, W, Xd, layers, y, _, _ = _prepare(c2, True)
     for i in range(8):
         l = layers[i % len(layers)]
         w4a16_matmul(Xd, l[0], l[1], l[2], c2.G, out=y)
@@ -175,7 +394,7 @@ def traffic_probe() -> None:
     print("C2 x8", flush=True)
     del layers
     c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
-    X, W, Xd, layers, y, _ = _prepare(c4, False)
+    X, W, Xd, layers, y, _, _ = _prepare(c4, False)
     for _ in range(3):
         w4a16_matmul(Xd, layers[0][0], layers[0][1], layers[0][2], c4.G, out=y)
     torch.cuda.synchronize()
@@ -243,9 +462,6 @@ def _traffic_for(workload: str):
 
 def main() -> int:
     args = _args()
-    if args.traffic_probe:
-        traffic_probe()
-        return 0
     if args.traffic_from:
         print(json.dumps(traffic_from(*args.traffic_from), indent=1))
         return 0
@@ -260,9 +476,17 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         return 2
+    if args.traffic_probe:
+        traffic_probe()
+        return 0
+    if args.reference_table:
+        print(json.dumps(reference_table(args.reference_json)), flush=True)
+        return 0
     from w4a16 import workloads as wl
 
-    graph = not args.eager
+    graph = args.graph
+    timing = ("HIP graph of the K calls, one replay, HIP events" if graph else
+              "K eager calls queued behind a spin kernel, HIP events on their stream")
     c2 = wl.CONFIGS["C2"][0]
     head = bench_case(c2, args.steps, args.warmup, graph=graph, cold=True)
     ms = head["us"] / 1e3
@@ -282,8 +506,9 @@ def main() -> int:
         "config": {"workload": "C2 decode GEMV M=1 K=4096 N=4096 G=128",
                    "global_batch": 1, "parallelism": "none (1 GPU)",
                    "kernel": head["kernel"], "split_k": head["split_k"],
-                   "weights": f"cold: {head['weight_copies']} rotating copies",
-                   "timing": "HIP graph of K calls, HIP events" if graph else "eager, HIP events"},
+                   "tile_cfg": head["tile_cfg"], "weights": _cold_note(head), "timing": timing,
+                   "queued_before_start": head["queued_before_start"],
+                   "device": _device_name()},
         "roofline": {"bound": "hbm", "achieved": round(head["GB/s"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4),
                      "traffic": _traffic_for("C2")},
@@ -291,13 +516,14 @@ def main() -> int:
     if not args.no_secondary:
         c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
         # steady state: 10 untimed calls (the clock settles under the MFMA
-        # load after the light decode phase), then 50 timed calls (~25 ms)
-        sec = bench_case(c4, max(50, args.steps // 4), max(10, args.warmup // 2), graph=graph,
-                         cold=False)
+        # load after the light decode phase), then 50 timed calls (~20 ms)
+        sec = bench_case(c4, max(50, args.steps // 4), max(10, args.warmup // 2),
+                         graph=SECONDARY_GRAPH, cold=False)
         line["secondary"] = {
             "metric": "TFLOP/s, C4 prefill M=4096 K=4096 N=14336 G=128",
             "value": round(sec["TFLOP/s"], 2), "unit": "TFLOP/s", "us": round(sec["us"], 2),
-            "kernel": sec["kernel"], "tile": sec["tile"],
+            "kernel": sec["kernel"], "tile_cfg": sec["tile_cfg"], "tile": sec["tile"],
+            "timing": f"{sec['steps']} calls in one HIP graph replay, HIP events",
             "roofline": {"bound": "mfma", "achieved": round(sec["TFLOP/s"], 2),
                          "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
@@ -308,12 +534,11 @@ def main() -> int:
     if args.sweep:
         rows = []
         for case in wl.cases("C2", "C3", "C4", "C5"):
-            r = bench_case(case, max(20, args.steps // 4), 5, graph=graph,
-                           cold=case.M < 64)
+            r = bench_case(case, max(20, args.steps // 4), 5, graph=graph, cold=case.M < 64)
             rows.append(r)
-            print(f"{r['case']:<32} {r['kernel']:>5} split={r['split_k']:<3} "
-                  f"{r['us']:9.2f} us {r['GB/s']:8.1f} GB/s {r['TFLOP/s']:8.2f} TFLOP/s",
-                  file=sys.stderr, flush=True)
+            print(f"{r['case']:<32} {r['kernel']:>6} cfg={r['tile_cfg']:<2} "
+                  f"split={r['split_k']:<3} {r['us']:9.2f} us {r['GB/s']:8.1f} GB/s "
+                  f"{r['TFLOP/s']:8.2f} TFLOP/s", file=sys.stderr, flush=True)
         if args.sweep_json:
             with open(args.sweep_json, "w") as f:
                 json.dump(rows, f, indent=1)
