@@ -3,33 +3,35 @@
 // Replaces the decode regime of the reference's fused kernel
 // (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 at M = 1..16, BLOCK_M >= 16).
 //
-// Layout of the work:
+// Layout of the work (both kernels):
 //   * a workgroup (WAVES waves) owns a block of CW = 4*CWL consecutive columns;
 //     in a wave, CWL lanes cover one packed row (one dwordx4 = 4 columns per
 //     lane) and the wave's 64/CWL row-lanes sit on different packed rows;
-//   * each row-lane owns a contiguous run of packed rows, cut into batches of BR
-//     rows (4 with 8 waves, 2 with 16 waves) aligned to absolute multiples of BR.
-//     With G % 32 == 0 every 4-row half (32 k) lies in one quantisation group,
-//     so a batch needs one scale/zero load per half;
-//   * every load of batch i+1 is issued before batch i is consumed, in the order
-//     scales, activations, weights, so the in-order vmcnt counter releases the
-//     first weight row as soon as it lands.  Weights are read with the
-//     non-temporal hint: each byte is used once;
-//   * activations: for M <= 2 each lane reads its rows' activations directly
-//     (the whole X is a few KiB and stays in L2), with no barrier before the
-//     first weight arrives; for larger M, X is staged once per chunk in LDS,
-//     permuted to the dequantiser's pair order;
 //   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
 //     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
-//   * reduction over row-lanes: a fixed xor-shuffle tree inside the wave, then the
-//     waves in order through LDS -- deterministic;
+//     weights are read with the non-temporal hint: each byte is used once;
+//   * reduction over row-lanes: DPP row rotations and a permlane
+//     transpose-reduce inside the wave, then the waves in order through LDS --
+//     deterministic (gemv_reduce_store);
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
-//     so that neighbouring row segments share that XCD's L2 lines;
+//     so that neighbouring row segments share that XCD's L2 lines (measured on
+//     MI355X: ~1 us per C2 call against the identity order, where both halves of
+//     a 128-byte line are fetched by two XCDs);
 //   * split-K where the column blocks cannot fill the CUs and K is long (the
 //     planner's rule; a plan can also force it): each workgroup writes fp32
 //     partials and a second kernel sums the splits in split order
 //     (deterministic).
+// gemv_direct_kernel (M <= 2, activations read directly: the whole X is a few
+// KiB and stays in L2, and no barrier stands before the first dot product):
+// the rows are dealt to the row-lanes in sweeps, so each batch is one
+// contiguous run of rows and a lane's first rows are the first to arrive.
+// gemv_kernel (M > 2, or M <= 2 with X staged in LDS): each row-lane owns a
+// contiguous run of packed rows, cut into batches of BR rows (4 with 8 waves,
+// 2 with 16) aligned to absolute multiples of BR, so a 4-row half (32 k, G %
+// 32 == 0) lies in one group and a batch needs one scale / zero load per
+// half; every load of batch i+1 is issued before batch i is consumed; X is
+// staged once per chunk in LDS, permuted to the dequantiser's pair order.
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
 
@@ -46,6 +48,79 @@ struct GemvShape {
   static constexpr int kBatch = WAVES >= 16 ? 2 : 4;
 };
 
+// Sum the lanes' partial dot products over the workgroup's row-lanes in a
+// fixed order and write y (S == 1, fp16 RNE, optional fp16 bias add) or this
+// k-split's fp32 partials.  Inside each 16-lane DPP row the lanes with equal
+// column quad are combined by row rotations, then a transpose-reduce over the
+// wave's four 16-lane rows leaves column slot c of the lane's quad in row c
+// (register-to-register, fixed order); the per-wave sums go through LDS once
+// and thread t < CW adds the WAVES partial sets of its column in wave order.
+template <int MT, int CWL, int WAVES>
+__device__ __forceinline__ void gemv_reduce_store(float (&acc)[MT][4],
+                                                  float (&red)[WAVES][MT][4 * CWL], int tid,
+                                                  int cb, int sk, int S, int N, int ldy,
+                                                  const f16* __restrict__ bias, f16* __restrict__ Y,
+                                                  float* __restrict__ part) {
+  constexpr int CW = 4 * CWL;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int cq = lane % CWL;
+  if constexpr (CWL <= 16) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[c] = acc[m][c];
+        if constexpr (CWL <= 4) v[c] += dpp_row_ror<4>(v[c]);
+        if constexpr (CWL <= 8) v[c] += dpp_row_ror<8>(v[c]);
+      }
+      const float r = fold_rows4(v[0], v[1], v[2], v[3]);
+      if ((lane & 15) < CWL) red[wave][m][4 * cq + (lane >> 4)] = r;
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      *reinterpret_cast<float4*>(&red[wave][m][4 * cq]) =
+          make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+  }
+  __syncthreads();
+
+  const int t = tid;
+  const int col = cb * CW + t;
+  const bool cv = (t < CW) && (col < N);
+  float v[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float sum = 0.0f;
+    if (t < CW) {
+      sum = red[0][m][t];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) sum += red[w][m][t];
+    }
+    v[m] = sum;
+  }
+
+  if (S == 1) {
+    if (cv) {
+      const f16 b = bias ? bias[col] : (f16)0.0f;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        f16 y = f32_to_f16(v[m]);
+        if (bias) y = y + b;
+        Y[(size_t)m * ldy + col] = y;
+      }
+    }
+    return;
+  }
+
+  // split-K: fp32 partials [split][M][N]; a second kernel sums the splits
+  if (cv) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) part[((size_t)sk * MT + m) * N + col] = v[m];
+  }
+}
+
 template <int MT, int CWL, int WAVES, bool STAGE>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
@@ -56,14 +131,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
   constexpr int H = BR / RH;               // halves per batch
-  // activations read directly from global (M <= 2 unless STAGE) or staged in LDS
-  constexpr bool XD = MT <= 2 && !STAGE;
+  // M <= 2 without staging runs gemv_direct_kernel; here X is staged in LDS
+  static_assert(MT > 2 || STAGE, "M <= 2 with direct activations is gemv_direct_kernel");
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
   constexpr int CW = 4 * CWL;              // columns per workgroup
-  constexpr int CHUNK = XD ? BR : kXsEntries / MT / BR * BR;   // packed rows of X per stage
+  constexpr int CHUNK = kXsEntries / MT / BR * BR;   // packed rows of X per stage
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
-  __shared__ uint4 xs[XD ? 1 : MT * CHUNK];
+  __shared__ uint4 xs[MT * CHUNK];
   __shared__ float red[WAVES][MT][CW];
 
   // 16-column blocks: every kernel argument in one batch of scalar loads up
@@ -121,7 +196,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 
   struct Batch {
     uint2 s[H], z[H];
-    uint4 x[XD ? MT * BR : 1];
     uint4 w[BR];
   };
   // Rows r0..r0+BR-1 of this lane's run [.., le).  Row u rides in the SGPR
@@ -136,15 +210,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       const uint32_t so = (nv && r0 < le) ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
       b.s[h] = buf_load8(rs, so, 0u);
       b.z[h] = buf_load8(rz, so, 0u);
-    }
-    if constexpr (XD) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int u = 0; u < BR; ++u)
-          b.x[m * BR + u] = buf_load16(
-              rx, r0 < le ? ((uint32_t)m * (uint32_t)ldx + (uint32_t)r0 * 8u) * 2u : kOobOffset,
-              uniform((uint32_t)u * 16u));
     }
     // One path for full and partial batches (a lane-dependent branch here would
     // move the row offset out of the SGPR and serialise the loads).
@@ -172,11 +237,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          uint4 xp;
-          if constexpr (XD)
-            xp = perm_pairs(b.x[m * BR + u]);
-          else
-            xp = xs[m * CHUNK + (r - c0)];
+          const uint4 xp = xs[m * CHUNK + (r - c0)];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             float a = acc[m][c];
@@ -191,8 +252,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     }
   };
 
-  for (int c0 = rb; c0 < re; c0 += (XD ? re - rb : CHUNK)) {
-    const int c1 = XD ? re : min(re, c0 + CHUNK);
+  for (int c0 = rb; c0 < re; c0 += CHUNK) {
+    const int c1 = min(re, c0 + CHUNK);
     const int nr = c1 - c0;
     // this row-lane's rows in the chunk: BR-row aligned run
     const int per = ((nr + RL - 1) / RL + BR - 1) / BR * BR;
@@ -200,9 +261,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const int le = min(c1, lb + per);
 
     Batch ba, bb;
-    if constexpr (XD) {
-      load_batch(lb, le, ba);
-    } else {
+    {
       // Stage X rows [c0, c1) into LDS; its loads go out before the first
       // weight batch, so the barrier waits only for them.
       if (c0 != rb) __syncthreads();   // previous chunk's readers are done
@@ -264,67 +323,203 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     }
   }
 
-  // Reduce over row-lanes in a fixed order.  Inside each 16-lane DPP row the
-  // lanes with equal cq are combined by row rotations, then a transpose-reduce
-  // over the wave's four 16-lane rows leaves column slot c of the lane's quad in
-  // row c (register-to-register, fixed order); the per-wave sums go through LDS
-  // once and thread t < CW adds the WAVES partial sets of its column in wave
-  // order.
-  constexpr int PS = WAVES;   // partial sets per workgroup
-  if constexpr (CWL <= 16) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      float v[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        v[c] = acc[m][c];
-        if constexpr (CWL <= 4) v[c] += dpp_row_ror<4>(v[c]);
-        if constexpr (CWL <= 8) v[c] += dpp_row_ror<8>(v[c]);
-      }
-      const float r = fold_rows4(v[0], v[1], v[2], v[3]);
-      if ((lane & 15) < CWL) red[wave][m][4 * cq + (lane >> 4)] = r;
-    }
-  } else {
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-      *reinterpret_cast<float4*>(&red[wave][m][4 * cq]) =
-          make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
-  }
-  __syncthreads();
+  gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
+}
 
-  const int t = tid;
-  const int col = cb * CW + t;
-  const bool cv = (t < CW) && (col < N);
-  float v[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    float s = 0.0f;
-    if (t < CW) {
-      s = red[0][m][t];
-#pragma unroll
-      for (int w = 1; w < PS; ++w) s += red[w][m][t];
-    }
-    v[m] = s;
-  }
+// M <= 2 with the activations read directly (no LDS staging): the rows of a
+// workgroup's k-range [rb, re) are dealt to its RL row-lanes in sweeps -- slot
+// j of row-lane rl is packed row rb + j * RL + rl -- and a batch is BR
+// consecutive slots.  So every batch is one contiguous run of BR * RL rows
+// read by the whole workgroup at once, and the rows a lane processes first are
+// the ones the memory system returns first: the dequant and dot products of
+// the first slots overlap the arrival of the later ones instead of waiting
+// for the lane's whole run (measured on MI355X, C2: 4.81-4.85 -> 4.48-4.57 us
+// with 16 waves and two slots per lane).  Each slot has its own group, so its
+// scale and zero loads are its own.  Slots past `re` load nothing (out-of-range
+// offsets read zeros: a zero activation makes their products exactly zero),
+// so every lane runs the same loads and the same trip count without a branch.
+// Arguments of gemv_direct_kernel: everything the loads need comes first (one
+// batch of scalar loads), the epilogue's arguments follow; the grid size is an
+// argument rather than a read of the dispatch's hidden arguments.
+struct DirectArgs {
+  const f16* X;
+  const uint32_t* QW;
+  const uint16_t* SC;
+  const uint16_t* ZR;
+  int N, K, ldx, rows_per_wg;
+  int nblk, nb;               // column blocks, workgroups (nblk * splits)
+  uint32_t gmagic, bmagic;    // k / G and block / nblk by reciprocal (group_div)
+  int gshift, bshift;
+  // epilogue
+  int S, ldy;
+  const f16* bias;
+  f16* Y;
+  float* part;
+};
 
-  if (S == 1) {
-    if (cv) {
-      const f16 b = bias ? bias[col] : (f16)0.0f;
+// M <= 2 with the activations read directly (no LDS staging): the rows of a
+// workgroup's k-range [rb, re) are dealt to its RL row-lanes in sweeps -- slot
+// j of row-lane rl is packed row rb + j * RL + rl -- and a batch is BR
+// consecutive slots.  So every batch is one contiguous run of BR * RL rows
+// read by the whole workgroup at once, and the rows a lane processes first are
+// the ones the memory system returns first: the dequant and dot products of
+// the first slots overlap the arrival of the later ones instead of waiting
+// for the lane's whole run.  Each slot has its own group, so its scale and
+// zero loads are its own.  Slots past `re` load nothing (out-of-range offsets
+// read zeros: a zero activation makes their products exactly zero), so every
+// lane runs the same loads and the same trip count without a branch.
+//
+// The time to the first weight load is on the critical path of a few-us call
+// (every wave waits for its own), so the set-up is kept short: one batch of
+// argument loads, the column block and k-split from the block index by
+// reciprocal instead of division and without branches, and each slot's
+// loads issued together, weight first (the long pole: cold HBM, most of the
+// bytes).  Measured on MI355X, C2 (16 waves, two slots per lane, one batch),
+// medians of 7 interleaved runs: 4.81-4.85 us with contiguous runs per lane,
+// 4.68-4.70 with sweeps.
+template <int MT, int CWL, int WAVES, bool ONE_BATCH>
+__global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArgs args) {
+  static_assert(MT <= 2, "direct activations are for M <= 2");
+  constexpr int BR = GemvShape<WAVES>::kBatch;
+  constexpr int RW = 64 / CWL;             // row-lanes per wave
+  constexpr int RL = WAVES * RW;           // row-lanes per workgroup
+  constexpr int CW = 4 * CWL;              // columns per workgroup
+  __shared__ float red[WAVES][MT][CW];
+
+  const f16* __restrict__ X = args.X;
+  const uint32_t* __restrict__ QW = args.QW;
+  const uint16_t* __restrict__ SC = args.SC;
+  const uint16_t* __restrict__ ZR = args.ZR;
+  const int N = args.N, K = args.K, ldx = args.ldx, rows_per_wg = args.rows_per_wg;
+  const int nblk = args.nblk, nb = args.nb;
+  const uint32_t gmagic = args.gmagic, bmagic = args.bmagic;
+  const int gshift = args.gshift, bshift = args.bshift;
+  const int S = args.S, ldy = args.ldy;
+  const f16* __restrict__ bias = args.bias;
+  f16* __restrict__ Y = args.Y;
+  float* __restrict__ part = args.part;
+  // every argument in one batch of scalar loads, before anything else: left
+  // to itself the compiler split them into dependent rounds (one more
+  // kernel-argument round trip in front of the first weight load) or loaded
+  // the output pointer after the reduction's barrier
+  asm volatile("" ::"s"(X), "s"(QW), "s"(SC), "s"(ZR), "s"(N), "s"(K), "s"(ldx),
+               "s"(rows_per_wg), "s"(nblk), "s"(nb), "s"(gmagic), "s"(bmagic), "s"(gshift),
+               "s"(bshift), "s"(S), "s"(ldy), "s"(bias), "s"(Y), "s"(part));
+
+  // XCD-aware block order (gemv_kernel), then block -> (k-split, column block)
+  const int b0 = (int)blockIdx.x;
+  const int lin = (nb & 7) == 0 ? (b0 & 7) * (nb >> 3) + (b0 >> 3) : b0;
+  const int sk = (int)((__umulhi((uint32_t)lin, bmagic) + (uint32_t)lin) >> bshift);
+  const int cb = lin - sk * nblk;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cq = lane % CWL;
+  const int rl = wave * RW + lane / CWL;
+  const int n = cb * CW + 4 * cq;
+  const bool nv = n < N;
+  const int KP = K >> 3;
+  auto group_of = [&](int k) {
+    return (int)((__umulhi((uint32_t)k, gmagic) + (uint32_t)k) >> gshift);
+  };
+  const int NG = group_of(K);
+  const int rb = sk * rows_per_wg;
+  const int re = min(KP, rb + rows_per_wg);
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, ((uint32_t)(MT - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(QW, (uint32_t)KP * (uint32_t)N * 4u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
+  const uint32_t row_bytes = (uint32_t)N * 4u;
+  // this lane's row and column at slot 0; slot j adds j * RL rows (in the SGPR)
+  const uint32_t w_voff = ((uint32_t)(rb + rl) * (uint32_t)N + (uint32_t)n) * 4u;
+
+  struct Batch {
+    uint2 s[BR], z[BR];
+    uint4 x[MT * BR];
+    uint4 w[BR];
+  };
+  // Slots b * BR .. b * BR + BR - 1: offsets first, then the loads in the
+  // order they are consumed, each slot's weight first.
+  auto load_batch = [&](int b, Batch& bt) {
+    uint32_t wo[BR], so[BR], xo[BR];
+#pragma unroll
+    for (int i = 0; i < BR; ++i) {
+      const int r = rb + (b * BR + i) * RL + rl;
+      const bool v = nv && r < re;
+      wo[i] = v ? w_voff : kOobOffset;
+      so[i] = v ? ((uint32_t)group_of(r * 8) * (uint32_t)N + (uint32_t)n) * 2u : kOobOffset;
+      xo[i] = v ? (uint32_t)r * 16u : kOobOffset;
+    }
+#pragma unroll
+    for (int i = 0; i < BR; ++i) {
+      bt.w[i] = buf_load16<kNonTemporal>(rw, wo[i],
+                                         uniform((uint32_t)((b * BR + i) * RL) * row_bytes));
+      bt.s[i] = buf_load8(rs, so[i], 0u);
+      bt.z[i] = buf_load8(rz, so[i], 0u);
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        bt.x[m * BR + i] = buf_load16(rx, xo[i], uniform((uint32_t)m * (uint32_t)ldx * 2u));
+      __builtin_amdgcn_sched_barrier(0);   // keep the slots in order
+    }
+  };
+
+  Batch ba, bb;
+  load_batch(0, ba);
+
+  const MagicRegs mg = make_magic();
+  float acc[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
+
+  auto process = [&](const Batch& bt) {
+#pragma unroll
+    for (int i = 0; i < BR; ++i) {
+      const ColQ2 p01 = make_colq2(bt.s[i].x, bt.z[i].x), p23 = make_colq2(bt.s[i].y, bt.z[i].y);
+      const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
+      f16x2 d[4][4];
+      dq_word_fast(bt.w[i].x, cq4[0], mg, d[0]);
+      dq_word_fast(bt.w[i].y, cq4[1], mg, d[1]);
+      dq_word_fast(bt.w[i].z, cq4[2], mg, d[2]);
+      dq_word_fast(bt.w[i].w, cq4[3], mg, d[3]);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        f16 y = f32_to_f16(v[m]);
-        if (bias) y = y + b;
-        Y[(size_t)m * ldy + col] = y;
+        const uint4 xp = perm_pairs(bt.x[m * BR + i]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float a = acc[m][c];
+          a = __builtin_amdgcn_fdot2(d[c][0], as_h2(xp.x), a, false);
+          a = __builtin_amdgcn_fdot2(d[c][1], as_h2(xp.y), a, false);
+          a = __builtin_amdgcn_fdot2(d[c][2], as_h2(xp.z), a, false);
+          a = __builtin_amdgcn_fdot2(d[c][3], as_h2(xp.w), a, false);
+          acc[m][c] = a;
+        }
       }
     }
-    return;
+  };
+
+  // ONE_BATCH (the host's choice when every split has at most one batch, e.g.
+  // C2): straight-line code, so the compiler's waits release slot 0 while the
+  // later slots are still in flight (behind a branch shared with the loop it
+  // waited for all of them).  Otherwise two register batches used ping-pong;
+  // the batch count is the same for every lane, so the branches are uniform.
+  if constexpr (ONE_BATCH) {
+    process(ba);
+  } else {
+    const int nbat = (re - rb + BR * RL - 1) / (BR * RL);
+    for (int b = 0; b < nbat; b += 2) {
+      load_batch(b + 1, bb);
+      process(ba);
+      if (b + 1 >= nbat) break;
+      load_batch(b + 2, ba);
+      process(bb);
+    }
   }
 
-  // split-K: fp32 partials [split][M][N]; a second kernel sums the splits
-  if (cv) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) part[((size_t)sk * MT + m) * N + col] = v[m];
-  }
+  gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
 }
 
 template <int MT, int CWL, int WAVES, bool STAGE>
@@ -334,12 +529,40 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   const int rows = gemv_rows_per_split(a.K, split);
   float* part = split > 1 ? static_cast<float*>(ws) : nullptr;
   const GroupDiv gd = group_div(a.G);
-  hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE>), dim3(nblk * split),
-                     dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
-                     reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
-                     static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                     static_cast<f16*>(a.y), part, a.N, a.K, a.ldx, a.ldy, gd.magic, gd.shift, rows,
-                     split, nblk);
+  if constexpr (MT <= 2 && !STAGE) {
+    // every split's rows fit one batch of BR slots per row-lane
+    constexpr int kRowsPerBatch = GemvShape<WAVES>::kBatch * WAVES * (64 / CWL);
+    auto kern = rows <= kRowsPerBatch ? gemv_direct_kernel<MT, CWL, WAVES, true>
+                                      : gemv_direct_kernel<MT, CWL, WAVES, false>;
+    const GroupDiv bd = group_div(nblk);
+    DirectArgs da{};
+    da.X = static_cast<const f16*>(a.x);
+    da.QW = reinterpret_cast<const uint32_t*>(a.qw);
+    da.SC = static_cast<const uint16_t*>(a.sc);
+    da.ZR = static_cast<const uint16_t*>(a.zr);
+    da.N = a.N;
+    da.K = a.K;
+    da.ldx = a.ldx;
+    da.rows_per_wg = rows;
+    da.nblk = nblk;
+    da.nb = nblk * split;
+    da.gmagic = gd.magic;
+    da.bmagic = bd.magic;
+    da.gshift = gd.shift;
+    da.bshift = bd.shift;
+    da.S = split;
+    da.ldy = a.ldy;
+    da.bias = static_cast<const f16*>(a.bias);
+    da.Y = static_cast<f16*>(a.y);
+    da.part = part;
+    hipLaunchKernelGGL(kern, dim3(nblk * split), dim3(GemvShape<WAVES>::kThreads), 0, st, da);
+  } else
+    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE>), dim3(nblk * split),
+                       dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
+                       reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
+                       static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
+                       static_cast<f16*>(a.y), part, a.N, a.K, a.ldx, a.ldy, gd.magic, gd.shift,
+                       rows, split, nblk);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, split, st);
