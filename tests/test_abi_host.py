@@ -331,12 +331,12 @@ def test_planner_gemv_split_rule():
 
 
 def test_planner_gemv_blocks_and_waves():
-    """Decode block, wave and activation-staging rules (measured on MI355X): 16
-    waves for M <= 2 on 16/32-column blocks with short rows per split, else 8;
-    32-column blocks where 16-column ones would leave every CU between one and
-    two blocks (K < 8192 only); activations staged in LDS (cfg + 3) for M <= 2
-    on 64-column blocks and for M = 1 on long 16-column rows, one chunk, no
-    split."""
+    """Decode block, wave and activation-staging rules (measured on MI355X): on
+    16/32-column blocks the activations are read directly with 16 waves at
+    M = 1 for any K and at M = 2 up to 8192 rows per split, else 8; 32-column
+    blocks where 16-column ones would leave every CU between one and two blocks
+    (K < 8192 only); activations staged in LDS (cfg 4: 8 waves) for M <= 2 on
+    64-column blocks, one chunk, no split."""
     from w4a16 import _lib
 
     p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
@@ -349,15 +349,17 @@ def test_planner_gemv_blocks_and_waves():
     assert p.tile_n == 16
     p = _lib.plan(2, 4096, 14336, 128)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
-    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, staged
-    assert p.tile_cfg == 5
+    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, direct
+    assert p.tile_cfg == 2
     p = _lib.plan(1, 28672, 4096, 128)           # 64-column blocks: 8 waves, staged
     assert (p.tile_n, p.tile_cfg) == (64, 4)
     p = _lib.plan(2, 28672, 8192, 128)
     assert (p.tile_n, p.tile_cfg) == (64, 4)
     p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 8192, 28672, 128)
+    p = _lib.plan(1, 8192, 28672, 128)           # C5 down-proj: 16 waves, direct
+    assert (p.tile_n, p.tile_cfg) == (32, 2)
+    p = _lib.plan(2, 8192, 28672, 128)           # ... 8 waves at M = 2
     assert (p.tile_n, p.tile_cfg) == (32, 1)
     p = _lib.plan(2, 1024, 8192, 128)            # split 4: 2048 rows per split
     assert p.split_k == 4 and p.tile_cfg == 2

@@ -81,26 +81,23 @@ int gemv_cols_auto(int64_t N, int64_t K, int cus) {
   return 16;
 }
 
-// GEMV waves per workgroup (measured on MI355X): 16 waves (two packed rows per
-// lane) for M <= 2 with 16- or 32-column blocks and short rows per split
-// (K / split <= 8192, or 16384 at M = 1): C2 5.14 -> 5.02 us, M = 2 5.88 ->
-// 5.49 us; 8 waves for wider blocks and longer K (K = 28672, N = 8192: 29.7 us
-// against 33.4).
-//
-// Activations staged in LDS (cfg + 3, M <= 2): one load and one permute per
-// element instead of one per lane sharing a row, at the cost of a barrier in
-// front of the first dot product.  Measured on MI355X: faster on 64-column
-// blocks (16 lanes per row; M = 2, K = 4096, N = 28672: 23.1 -> 19.6 us;
-// M = 2, K = 8192, N = 28672: 40.2 -> 33.7 us) and for M = 1 on long rows of
-// 16-column blocks (K = 14336, N = 4096: 13.6 -> 12.8 us); slower at short K
-// (C2: 4.84 -> 5.72 us), on 32-column blocks at K = 28672 (two staging chunks)
-// and with splits.
+// GEMV waves per workgroup and activation staging (measured on MI355X with
+// the sweep-ordered direct kernel for M <= 2, medians of 3 runs of 60 calls):
+//   * 64-column blocks stage the activations in LDS (cfg 4: 8 waves): 16
+//     lanes share a row, and one load and one permute per element beat one
+//     per lane (M = 1, K = 4096, N = 28672: 16.2 us against 18.6 direct; M = 1,
+//     K = 8192, N = 28672: 27.9 against 32.3; M = 2 likewise);
+//   * 16- and 32-column blocks read them directly with 16 waves (cfg 2) at
+//     M = 1 for any K (K = 28672, N = 8192: 27.2 us against 30.8 with 8 waves
+//     and 28.7 staged; K = 14336, N = 4096: 11.7 against 11.9 staged; C2 4.7)
+//     and at M = 2 up to K / split = 8192, with 8 waves (cfg 1) beyond;
+//   * M > 2 always stages them (gemv_kernel, cfg 1).
 int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   const int64_t ks = K / (split > 0 ? split : 1);
-  const int waves = (M <= 2 && cols <= 32 && ks <= (M == 1 ? 16384 : 8192)) ? 2 : kGemvDefaultConfig;
-  const bool stage = M <= 2 && (split <= 1) && ks <= 16384 &&
-                     (cols >= 64 || (M == 1 && cols == 16 && ks >= 12288));
-  return stage ? waves + 3 : waves;
+  if (M > 2) return kGemvDefaultConfig;
+  const bool stage = split <= 1 && ks <= 16384 && cols >= 64;
+  if (stage) return kGemvDefaultConfig + 3;
+  return (M == 1 || ks <= 8192) ? 2 : kGemvDefaultConfig;
 }
 
 // GEMV k-split by shape (measured on MI355X, M = 1..8, fp32 partials plus the
