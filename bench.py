@@ -77,12 +77,17 @@ def _args():
                     help="the reference's bench_gemm.py method, keys and markdown table")
     ap.add_argument("--reference-json", default=None, help="write the --reference-table rows here")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="run the workload for rocprofv3 --pmc: a 256 MiB copy (calibration), "
-                         "8 cold C2 decode calls, 3 C4 M=4096 prefill calls; no timing")
+                    help="run the workloads for rocprofv3 --pmc: a 256 MiB copy "
+                         "(calibration), then cold C2 decode calls, C3 small-batch calls "
+                         "(skinny and 32-row streamed kernels) and C4 M=4096 prefill "
+                         "calls (PROBE); no timing")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic.json from the counter_collection.csv files "
                          "of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "--traffic-probe")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="markdown table of every counter in rocprofv3 --pmc runs of "
+                         "--traffic-probe, per workload and kernel")
     return ap.parse_args()
 
 
@@ -372,9 +377,19 @@ def _device_name() -> str:
 # --------------------------------------------------------------------------- #
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 
+# --traffic-probe's workloads, in order: (key, config, M, K, N, calls, cold)
+PROBE = [("C2", "C2", 1, 4096, 4096, 8, True),
+         ("C3_M8_K4096_N4096", "C3", 8, 4096, 4096, 4, True),
+         ("C3_M16_K4096_N28672", "C3", 16, 4096, 28672, 4, True),
+         ("C3_M32_K4096_N28672", "C3", 32, 4096, 28672, 4, True),
+         ("C4_M4096", "C4", 4096, 4096, 14336, 3, False)]
+
 
 def traffic_probe() -> None:
-    """Kernels for the HBM-traffic counters (FETCH_SIZE / WRITE_SIZE)."""
+    """Kernels for the counter runs (FETCH_SIZE / WRITE_SIZE / SQ_*): a 256 MiB
+    device copy three times (calibration), then each PROBE workload's calls
+    with the default plans, each group preceded by one short spin kernel that
+    marks where it starts."""
     import torch
     from w4a16 import w4a16_matmul
     from w4a16 import workloads as wl
@@ -384,69 +399,128 @@ def traffic_probe() -> None:
     for _ in range(3):
         b.copy_(a)                                   # calibration: 256 MiB read + written
     torch.cuda.synchronize()
+    del a, b
     print("copy 256 MiB x3", flush=True)
-    c2 = wl.CONFIGS["C2"][0]
-    X, W, Xd, layers, y, _, _ = _prepare(c2, True)
-    for i in range(8):
-        l = layers[i % len(layers)]
-        w4a16_matmul(Xd, l[0], l[1], l[2], c2.G, out=y)
-    torch.cuda.synchronize()
-    print("C2 x8", flush=True)
-    del layers
-    c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
-    X, W, Xd, layers, y, _, _ = _prepare(c4, False)
-    for _ in range(3):
-        w4a16_matmul(Xd, layers[0][0], layers[0][1], layers[0][2], c4.G, out=y)
-    torch.cuda.synchronize()
-    print("C4 M=4096 x3", flush=True)
+    for key, cfg, M, K, N, calls, cold in PROBE:
+        case = [c for c in wl.CONFIGS[cfg] if (c.M, c.K, c.N) == (M, K, N)][0]
+        X, W, Xd, layers, y, _, _ = _prepare(case, cold)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(1000)                      # group marker
+        for i in range(calls):
+            l = layers[i % len(layers)]
+            w4a16_matmul(Xd, l[0], l[1], l[2], case.G, out=y)
+        torch.cuda.synchronize()
+        del layers
+        print(f"{key} x{calls}", flush=True)
 
 
-def _counter_rows(path: str, counter: str):
-    """(dispatch id, kernel name, value) per dispatch from a rocprofv3 counter CSV."""
+def _counter_groups(path: str):
+    """{counter: {workload: {kernel: [value per dispatch]}}} from a rocprofv3
+    counter CSV of --traffic-probe, plus the calibration copies' values."""
     import csv
 
-    rows = {}
+    disp = {}
     with open(path) as f:
         for r in csv.DictReader(f):
-            if r["Counter_Name"] != counter:
-                continue
             d = int(r["Dispatch_Id"])
-            name, v = r["Kernel_Name"], float(r["Counter_Value"])
-            rows[d] = (name, rows.get(d, (name, 0.0))[1] + v)
-    return [(d, n, v) for d, (n, v) in sorted(rows.items())]
+            e = disp.setdefault(d, {"name": r["Kernel_Name"], "c": {}})
+            e["c"][r["Counter_Name"]] = e["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    out, calib = {}, {}
+    gi = -1
+    for d in sorted(disp):
+        name, cs = disp[d]["name"], disp[d]["c"]
+        if "copy" in name.lower() and gi < 0:
+            for k, v in cs.items():
+                calib.setdefault(k, []).append(v)
+            continue
+        if "spin_kernel" in name:
+            gi += 1
+            continue
+        if gi < 0 or gi >= len(PROBE) or "w4a16" not in name or any(
+                t in name for t in ("quantize", "pack", "dequant")):
+            continue
+        for k, v in cs.items():
+            out.setdefault(k, {}).setdefault(PROBE[gi][0], {}).setdefault(name, []).append(v)
+    return out, calib
 
 
 def traffic_from(fetch_csv: str, write_csv: str) -> dict:
-    """HBM bytes per launch of the C2 and C4 GEMM kernels from --traffic-probe's
-    counters.  FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; each is scaled by
-    what it reads for the calibration copy (the probe's first three copy
-    dispatches, 256 MiB read and 256 MiB written each)."""
+    """HBM bytes per launch of each PROBE workload's kernels from
+    --traffic-probe's counters.  FETCH_SIZE / WRITE_SIZE are in KiB per
+    dispatch; each is scaled by what it reads for the calibration copy (the
+    probe's first three copy dispatches, 256 MiB read and 256 MiB written
+    each).  A workload's figure is its main kernel's (most dispatched, then
+    longest name); a split-K reduction pass is listed beside it."""
     out = {"calibration": {"copy_bytes": 256 << 20}, "kernels": {}}
-    per = {}
     for key, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"),
                                ("write", write_csv, "WRITE_SIZE")):
-        rows = _counter_rows(path, counter)
-        copies = [v for _, n, v in rows if "copy" in n.lower()][:3]
+        groups, calib = _counter_groups(path)
+        copies = calib.get(counter, [])[:3]
         if len(copies) < 3:
             raise SystemExit(f"{path}: calibration copies not found")
         raw = sum(copies) / len(copies)
         scale = (256 << 10) / raw
         out["calibration"][f"{key}_size_kib_raw"] = raw
         out["calibration"][f"{key}_scale"] = scale
-        gemm = [(n, v) for _, n, v in rows if "w4a16" in n
-                and not any(t in n for t in ("quantize", "pack", "dequant"))]
-        if len(gemm) != 11:
-            raise SystemExit(f"{path}: expected 8 C2 + 3 C4 GEMM dispatches, got {len(gemm)}")
-        per[key] = {"C2": (gemm[0][0], gemm[:8]), "C4_M4096": (gemm[8][0], gemm[8:])}
-        for wkey, (name, ds) in per[key].items():
-            e = out["kernels"].setdefault(wkey, {"kernel": name})
-            e[f"{key}_kib_raw"] = sum(v for _, v in ds) / len(ds)
-            e[f"{key}_bytes"] = e[f"{key}_kib_raw"] * 1024 * scale
+        for wkey, kernels in groups.get(counter, {}).items():
+            e = out["kernels"].setdefault(wkey, {"launches": {}})
+            for name, vals in kernels.items():
+                k = e["launches"].setdefault(name, {"dispatches": len(vals)})
+                k[f"{key}_kib_raw"] = sum(vals) / len(vals)
+                k[f"{key}_bytes"] = k[f"{key}_kib_raw"] * 1024 * scale
     for e in out["kernels"].values():
-        e["bytes_per_launch"] = int(round(e["fetch_bytes"] + e["write_bytes"]))
+        for k in e["launches"].values():
+            k["bytes_per_launch"] = int(round(k.get("fetch_bytes", 0) + k.get("write_bytes", 0)))
+        main = max(e["launches"], key=lambda n: ("reduce" not in n, e["launches"][n]["dispatches"]))
+        e["kernel"] = main
+        e["bytes_per_launch"] = e["launches"][main]["bytes_per_launch"]
     with open(TRAFFIC_JSON, "w") as f:
         json.dump(out, f, indent=1)
     return out
+
+
+def _kernel_short(mangled: str) -> str:
+    """`name<args>` of a kernel in this library's anonymous namespace from its
+    mangled name (template arguments that are integer or bool literals only) or
+    from the profiler's demangled one; the profiler leaves names with _Float16
+    (DF16_) parameters mangled."""
+    import re
+
+    m = re.match(r"_ZN5w4a1612_GLOBAL__N_1(\d+)", mangled)
+    if not m:                                    # already demangled by the profiler
+        short = mangled.replace("w4a16::(anonymous namespace)::", "")
+        return short.split("(")[0].replace("void ", "")
+    n = int(m.group(1))
+    at = m.end()
+    name, rest = mangled[at:at + n], mangled[at + n:]
+    if rest.startswith("I"):
+        args = re.findall(r"L([ib])(\d+)E", rest[:rest.find("EE") + 2])
+        name += "<" + ", ".join(("true" if v == "1" else "false") if t == "b" else v
+                                for t, v in args) + ">"
+    return name
+
+
+def pmc_summary(paths) -> str:
+    """Markdown table: per PROBE workload and kernel, each counter's average per
+    dispatch over the --traffic-probe calls, from rocprofv3 --pmc CSVs."""
+    rows = {}
+    counters = []
+    for p in paths:
+        groups, _ = _counter_groups(p)
+        for c, wl_ in groups.items():
+            if c not in counters:
+                counters.append(c)
+            for wkey, kernels in wl_.items():
+                for name, vals in kernels.items():
+                    rows.setdefault((wkey, name), {})[c] = sum(vals) / len(vals)
+    order = {k[0]: i for i, k in enumerate(PROBE)}
+    lines = ["| workload | kernel | " + " | ".join(counters) + " |",
+             "|---|---|" + "---|" * len(counters)]
+    for (wkey, name), cs in sorted(rows.items(), key=lambda kv: (order.get(kv[0][0], 99), kv[0][1])):
+        short = _kernel_short(name)
+        lines.append(f"| {wkey} | `{short}` | " +
+                     " | ".join(f"{cs[c]:,.0f}" if c in cs else "" for c in counters) + " |")
+    return "\n".join(lines)
 
 
 def _traffic_for(workload: str):
@@ -464,6 +538,9 @@ def main() -> int:
     args = _args()
     if args.traffic_from:
         print(json.dumps(traffic_from(*args.traffic_from), indent=1))
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -534,7 +611,10 @@ def main() -> int:
     if args.sweep:
         rows = []
         for case in wl.cases("C2", "C3", "C4", "C5"):
-            r = bench_case(case, max(20, args.steps // 4), 5, graph=graph, cold=case.M < 64)
+            # prefill-sized calls (M >= 64) as one graph replay, like the
+            # secondary line; decode-sized calls eager behind the spin
+            r = bench_case(case, max(20, args.steps // 4), 5, graph=graph or case.M >= 64,
+                           cold=case.M < 64)
             rows.append(r)
             print(f"{r['case']:<32} {r['kernel']:>6} cfg={r['tile_cfg']:<2} "
                   f"split={r['split_k']:<3} {r['us']:9.2f} us {r['GB/s']:8.1f} GB/s "

@@ -64,8 +64,9 @@ typedef struct w4a16_plan {
                               (16 for M <= 2), 4 / 5 = the same with the
                               activations staged in LDS (M <= 2; larger M
                               always stages them); SKINNY: 0 / 2 / 3 = 16 / 32 /
-                              64-column blocks of 4 waves (32: M <= 32, N even;
-                              64: M <= 16, N % 4 == 0).  Other numbers name
+                              64-column blocks (32: M <= 32, N even; 64:
+                              M <= 16, N % 4 == 0), 4 to 16 waves by K.
+                              Other numbers name
                               retired forms and are refused
                               (W4A16_ERR_BAD_PLAN)                           */
   int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup   */

@@ -256,8 +256,10 @@ def test_quant_entry_points_reject_bad_args(lib):
 
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
-    (3, 28672, 4096, 128, "gemv"),   # wide N: the GEMV up to M = 3
-    (4, 28672, 4096, 128, "skinny"),  # ... from M = 4 the skinny kernel's 64-column blocks
+    (3, 28672, 4096, 128, "skinny"),  # wide N, K <= 4096: 64-column skinny blocks from M = 3
+    (3, 28672, 8192, 128, "gemv"),    # ... longer K (the skinny loop): the GEMV up to M = 4
+    (3, 28672, 4096, 64, "gemv"),     # ... and without 64-column blocks (G % 128 != 0)
+    (4, 28672, 4096, 128, "skinny"),
     (2, 6144, 4096, 128, "gemv"),
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
     (8, 4096, 4096, 128, "skinny"),

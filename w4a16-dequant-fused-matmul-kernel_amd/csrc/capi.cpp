@@ -130,16 +130,20 @@ struct MfmaChoice {
   int cfg, split;
 };
 
+bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
+
 // Decode batches 3 <= M <= 8: the MFMA skinny kernel does the M dot products
 // per dequantised pair on the matrix cores where the GEMV spends M v_dot2 on
 // each; measured on MI355X it wins from M = 3 up to N = 16384 (M = 8,
 // K = N = 4096: 7.7 vs 12.1 us; M = 3, K = 14336, N = 4096: 17.2 vs 20.8 us;
 // M = 4, K = 4096, N = 6144: 9.7 vs 11.5 us) and from M = 5 on wider weights
-// (M = 5, K = 4096, N = 28672: 29.7 vs 32.6 us), while at M <= 2, and at M <= 4
-// on N = 28672, the GEMV is faster (M = 4, K = 8192, N = 28672: 47 vs 75 us).
-bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G) {
-  (void)K;
-  return M >= 3 && M <= kGemvMaxM && skinny_applicable(M, G) && (N <= 16384 || M >= 5);
+// (M = 5, K = 4096, N = 28672: 29.7 vs 32.6 us).  At M <= 4 on wider weights
+// the GEMV is faster where the skinny kernel loops over K (M = 4, K = 8192,
+// N = 28672: 47 vs 75 us), not where its 64-column blocks take K in one batch
+// per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us).
+bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  return M >= 3 && M <= kGemvMaxM && skinny_applicable(M, G) &&
+         (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, G, cus)));
 }
 
 // Small batches (4 <= M <= 64) on large enough weights: the streamed prefill
@@ -259,7 +263,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
                                            skinny_wide_beats_stream(M, N, G, cus))
                    ? W4A16_KERNEL_SKINNY
                    : W4A16_KERNEL_MFMA;
-    else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G))
+    else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G, cus))
       kernel = W4A16_KERNEL_GEMV;
     else if (M <= kSkinnyMaxM && skinny_applicable(M, G))
       kernel = W4A16_KERNEL_SKINNY;
@@ -318,9 +322,9 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->grid_x = (N + p->tile_n - 1) / p->tile_n;
       p->grid_y = 1;
       // 64- or 32-column blocks where they apply (cfg 3 / 2), else 16-column
-      // blocks (cfg 0), 4 waves per workgroup.  (An 8-wave form on 16-column
-      // blocks, once cfg 1, was nowhere faster with the branch-free batch
-      // loop -- measured on MI355X, 4 vs 8 waves: M = 3 / 8 / 16, K = 4096,
+      // blocks (cfg 0); the kernel's wave count follows K.  (An 8-wave form
+      // of the two-batch loop on 16-column blocks, once cfg 1, was nowhere
+      // faster -- measured on MI355X, 4 vs 8 waves: M = 3 / 8 / 16, K = 4096,
       // N = 6144: 8.9 / 10.0 / 12.3 vs 9.3 / 10.5 / 13.0 us; M = 8 / 16,
       // K = 14336, N = 4096: 15.4 / 19.3 vs 16.2 / 19.9; M = 32, K = N = 4096:
       // 11.5 vs 12.1 -- and was retired.)

@@ -7,8 +7,9 @@
 //
 // At these M the GEMM is still bound by the weight stream, and a prefill tiling
 // (hundreds of rows per workgroup) leaves most CUs idle.  Here:
-//   * a workgroup of 4 waves owns a block of columns and the whole of K, so no
-//     cross-workgroup reduction is needed.  Block widths (plan tile_cfg):
+//   * a workgroup of 4, 8 or 16 waves owns a block of columns and the whole of
+//     K, so no cross-workgroup reduction is needed.  Block widths (plan
+//     tile_cfg):
 //     - cfg 0: 16 columns, one per lane: one 4-byte weight load per lane and
 //       32-k step, 2-byte scale / zero loads (N = 4096 gives 256 workgroups);
 //     - cfg 2: 32 columns (M <= 32, N even), two adjacent columns per lane: one
@@ -20,8 +21,10 @@
 //   * in v_mfma_f32_16x16x32_f16 lane l holds B[k = 8*(l/16)..+7][n = l%16]: one
 //     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA
 //     and n-tile, reading 4 packed rows of its block per load;
-//   * the 4 waves split K into contiguous runs of whole batches; each wave
-//     walks its run in batches of 8 k-steps (256 k) with two register batches
+//   * the waves split K into contiguous runs of whole batches of 8 k-steps
+//     (256 k).  Up to K = 4096 there are enough waves (K / 256, at least 4)
+//     for one batch each, and each wave issues all its loads before its first
+//     product; longer K has 4 waves walk their runs with two register batches
 //     used ping-pong, all loads of batch i+1 -- weights, scales, zeros and
 //     activations -- issued before batch i is consumed, unconditionally (past
 //     the range they read zeros), so the compiler's wait counts are exact;
@@ -30,7 +33,7 @@
 //     the buffer range check;
 //   * dequant is the packed-fp16 magic-number form, then the pairs are put back
 //     in natural k order (4 v_perm per word) so activations need no permutation;
-//   * the 4 waves' 16x16 fp32 tiles are summed in LDS in wave order
+//   * the waves' 16x16 fp32 tiles are summed in LDS in wave order
 //     (deterministic) and rounded to fp16 once; optional fp16 bias add;
 //   * workgroup -> column block is XCD-aware (consecutive blocks share an XCD).
 // Requirements (checked by the caller): G % 32 == 0, K % G == 0, 16-byte
@@ -52,7 +55,7 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // the lane's two adjacent columns come in one 8-byte word load and one 4-byte
 // scale / zero load each, and its activation fragment feeds both n-tiles, so a
 // CU streams X once for 32 columns instead of once per 16).
-template <int MT, int GSTEP, int WAVES, int NT>
+template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
@@ -160,7 +163,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
         }
         const uint32_t xk = uniform(in ? (uint32_t)ks * 64u : kOobOffset);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
+        for (int mt = 0; mt < MT; ++mt) {
+          b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
+        }
       }
     }
   };
@@ -174,7 +179,14 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   auto process = [&](const Batch& b, int s0) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      if (s0 + j >= ke) break;   // wave-uniform
+      // Steps past the range loaded zero activations and zero scales / zeros
+      // (ke is a multiple of the group's step count, so a past step's group
+      // slot is past too): their products are exactly 0.  Single-batch code
+      // runs them branch-free: behind per-step range branches the compiler
+      // sank the later steps' loads below the earlier steps' math, a round
+      // trip each.  The two-batch loop skips them (measured faster there: C5
+      // M = 16, K = 28672 took 47.4 us branch-free against 40.4).
+      if (!ONE_BATCH && s0 + j >= ke) break;   // wave-uniform
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const ColQ cq = make_colq(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
@@ -196,13 +208,19 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   // the compiler's vmcnt waits count exactly; with loads under the branches
   // its waits at the joins covered the next batch too (C3 M = 4..32 measured
   // 2-11 % slower that way).
-  Batch bt[2];
-  load_batch(kb, bt[0]);
-  for (int s0 = kb; s0 < ke; s0 += 2 * kBatch) {
-    load_batch(s0 + kBatch, bt[1]);
-    process(bt[0], s0);
-    load_batch(s0 + 2 * kBatch, bt[0]);
-    if (s0 + kBatch < ke) process(bt[1], s0 + kBatch);
+  if constexpr (ONE_BATCH) {
+    Batch b1;
+    load_batch(kb, b1);
+    process(b1, kb);
+  } else {
+    Batch bt[2];
+    load_batch(kb, bt[0]);
+    for (int s0 = kb; s0 < ke; s0 += 2 * kBatch) {
+      load_batch(s0 + kBatch, bt[1]);
+      process(bt[0], s0);
+      load_batch(s0 + 2 * kBatch, bt[0]);
+      if (s0 + kBatch < ke) process(bt[1], s0 + kBatch);
+    }
   }
 
 #pragma unroll
@@ -210,10 +228,11 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[wave][mt][t][lane] = acc[mt][t];
   __syncthreads();
-  // wave w finishes m-tiles w, w+4, ...: sum the 4 waves in order, round, store
-  for (int mt = wave; mt < MT; mt += kWaves) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
+  // wave w finishes tiles w, w + WAVES, ...: sum the waves in order, round, store
+  for (int i = wave; i < MT * NT; i += kWaves) {
+    const int mt = i / NT;
+    {
+      const int t = i % NT;
       f32x4 v = red[0][mt][t][lane];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) v += red[w][mt][t][lane];
@@ -233,37 +252,43 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   }
 }
 
-template <int MT, int GSTEP>
-hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
-  if constexpr (MT <= 2) {
-    if (cfg == 2) {   // 32-column blocks
-      const int nblk2 = (a.N + 31) / 32;
-      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 2>), dim3(nblk2), dim3(256), 0, st,
-                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                         a.G, nblk2, a.ldx, a.ldy);
-      return hipGetLastError();
-    }
-  }
-  if constexpr (MT == 1) {
-    if (cfg == 3) {   // 64-column blocks
-      const int nblk4 = (a.N + 63) / 64;
-      hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 4>), dim3(nblk4), dim3(256), 0, st,
-                         static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                         static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                         static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                         a.G, nblk4, a.ldx, a.ldy);
-      return hipGetLastError();
-    }
-  }
-  const int nblk = (a.N + 15) / 16;
-  hipLaunchKernelGGL((skinny_kernel<MT, GSTEP, 4, 1>), dim3(nblk), dim3(256), 0, st,
+// Waves per workgroup: as many as give each wave exactly one batch (K <= 1024:
+// 4, K <= 2048: 8, K <= 4096: 16), so every load is issued before the first
+// product, in one round trip to memory; longer K walks 4 waves' runs in the
+// two-batch loop (16 waves' loop registers spill; 8 or 16 waves in the loop
+// measured no faster at K = 8192..28672).  Measured on MI355X, cold weights,
+// against 4 waves in the loop: K = N = 4096 M = 4 / 8 / 16: 6.40 / 6.78 /
+// 7.85 us -> 5.74 / 6.29 / 7.49; M = 16, N = 28672 (64 columns): 22.6 ->
+// 21.1; M = 8, K = 2048, N = 4096: 4.99 -> 4.55 with 8 waves.
+template <int MT, int GSTEP, int NT>
+hipError_t launch_nt(const GemmArgs& a, hipStream_t st) {
+  const int nblk = (a.N + 16 * NT - 1) / (16 * NT);
+  const int ks = a.K >> 5;
+  // 16 waves hold 128 registers each: 64 rows with a scale / zero load per
+  // step would spill there, and take the loop instead
+  constexpr int k16 = MT == 4 && GSTEP == 1 ? 0 : 16;
+  auto k = ks <= 4 * kBatch     ? skinny_kernel<MT, GSTEP, 4, NT, true>
+           : ks <= 8 * kBatch   ? skinny_kernel<MT, GSTEP, 8, NT, true>
+           : ks <= k16 * kBatch ? skinny_kernel<MT, GSTEP, (k16 ? k16 : 4), NT, true>
+                                : skinny_kernel<MT, GSTEP, 4, NT, false>;
+  const int waves = ks <= 4 * kBatch ? 4 : ks <= 8 * kBatch ? 8 : ks <= k16 * kBatch ? k16 : 4;
+  hipLaunchKernelGGL(k, dim3(nblk), dim3(64 * waves), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
                      a.G, nblk, a.ldx, a.ldy);
   return hipGetLastError();
+}
+
+template <int MT, int GSTEP>
+hipError_t launch_g(const GemmArgs& a, int cfg, hipStream_t st) {
+  if constexpr (MT <= 2) {
+    if (cfg == 2) return launch_nt<MT, GSTEP, 2>(a, st);   // 32-column blocks
+  }
+  if constexpr (MT == 1) {
+    if (cfg == 3) return launch_nt<MT, GSTEP, 4>(a, st);   // 64-column blocks
+  }
+  return launch_nt<MT, GSTEP, 1>(a, st);                    // 16-column blocks
 }
 
 template <int MT>
@@ -282,8 +307,9 @@ hipError_t launch_mt(const GemmArgs& a, int cfg, hipStream_t st) {
 }  // namespace
 
 // cfg 0: 16-column blocks; 2: 32-column blocks (M <= 32, N even); 3:
-// 64-column blocks (M <= 16, N % 4 == 0); 4 waves each.  cfg 1 (8 waves on
-// 16-column blocks) measured slower on every shape and was retired.
+// 64-column blocks (M <= 16, N % 4 == 0); the wave count follows K (launch_nt).
+// cfg 1 (8 waves in the two-batch loop on 16-column blocks) measured slower on
+// every shape and was retired.
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st) {
   if (!(cfg == 0 || cfg == 2 || cfg == 3) || (cfg == 2 && (a.M > 32 || a.N % 2 != 0)) ||
       (cfg == 3 && (a.M > 16 || a.N % 4 != 0)))

@@ -105,12 +105,13 @@ hipError_t launch_occ2_gemm(const GemmArgs& a, int split, float* part, hipStream
 bool operands_fit(int M, int N, int K, int G);
 
 // Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM,
-// 4 waves per workgroup over the whole of K.  cfg 0: 16-column blocks (one
+// one workgroup per column block over the whole of K (4 waves, 8 or 16 when
+// that gives each wave one 256-k batch: K <= 2048 / 4096).  cfg 0: 16-column blocks (one
 // column per lane, 4-byte weight loads, 2-byte scale / zero loads); cfg 2:
 // 32-column blocks (M <= 32, N even: two columns per lane, 8-byte weight
 // loads, 4-byte scale / zero loads); cfg 3: 64-column blocks (M <= 16,
 // N % 4 == 0: four columns per lane, 16-byte weight loads, 8-byte scale /
-// zero loads).  cfg 1 (8 waves) was retired.
+// zero loads).  cfg 1 (8 waves in the loop) was retired.
 constexpr int kSkinnyMaxM = 64;
 hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st);
 
