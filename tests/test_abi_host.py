@@ -311,10 +311,10 @@ def test_planner_gemv_split_rule():
         p = _lib.plan(1, N, 4096, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv"
         assert p.split_k == 1 and p.workspace_bytes == 0
-        assert p.tile_n in (16, 32, 64, 256)
+        assert p.tile_n in (16, 32, 64, 128, 256)
         assert p.tile_cfg in (1, 2, 4, 5)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
-    assert _lib.plan(1, 28672, 4096, 128).tile_n == 64
+    assert _lib.plan(1, 28672, 4096, 128).tile_n == 128
     for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 2048, 28672)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
@@ -337,8 +337,9 @@ def test_planner_gemv_blocks_and_waves():
     16/32-column blocks the activations are read directly with 16 waves at
     M = 1 for any K and at M = 2 up to 8192 rows per split, else 8; 32-column
     blocks where 16-column ones would leave every CU between one and two blocks
-    (K < 8192 only); activations staged in LDS (cfg 4: 8 waves) for M <= 2 on
-    64-column blocks, one chunk, no split."""
+    (K < 8192 only); activations staged in LDS for M <= 2 on 64-column blocks
+    (cfg 4: 8 waves) and on 128-column blocks where those give 7/8 of the CUs
+    one each (cfg 5: 16 waves), one chunk, no split."""
     from w4a16 import _lib
 
     p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
@@ -353,10 +354,14 @@ def test_planner_gemv_blocks_and_waves():
     assert p.tile_cfg == 1
     p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, direct
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 28672, 4096, 128)           # 64-column blocks: 8 waves, staged
+    p = _lib.plan(1, 16384, 4096, 128)           # 64-column blocks: 8 waves, staged
     assert (p.tile_n, p.tile_cfg) == (64, 4)
+    p = _lib.plan(1, 28672, 4096, 128)           # 224 blocks of 128: 16 waves, staged
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 5, 1)
     p = _lib.plan(2, 28672, 8192, 128)
-    assert (p.tile_n, p.tile_cfg) == (64, 4)
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 5, 1)
+    p = _lib.plan(3, 28672, 8192, 128)           # M > 2 keeps 64-column blocks
+    assert (p.tile_n, p.tile_cfg) == (64, 1)
     p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
     assert p.tile_cfg == 2
     p = _lib.plan(1, 8192, 28672, 128)           # C5 down-proj: 16 waves, direct

@@ -70,7 +70,13 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 // blocks would leave the CUs between one and two blocks each, 32-column blocks
 // (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
 // 7.5 us at M = 2).
-int gemv_cols_auto(int64_t N, int64_t K, int cus) {
+int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
+  // M <= 2: 128-column blocks where they give at least 7/8 of the CUs one
+  // each (N = 28672 on MI355X: 224), a workgroup per CU reading 512-byte row
+  // segments (measured on MI355X, 16 waves with staged activations against
+  // 64-column blocks of 8: M = 1, K = 4096, N = 28672 15.4 vs 16.4 us; K = 8192
+  // 26.5 vs 28.6; G = 32 26.9 vs 29.6; M = 2, K = 8192 31.5 vs 32.2)
+  if (M <= 2 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
     if ((N + c - 1) / c >= cus) {
@@ -95,6 +101,7 @@ int gemv_cols_auto(int64_t N, int64_t K, int cus) {
 int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   const int64_t ks = K / (split > 0 ? split : 1);
   if (M > 2) return kGemvDefaultConfig;
+  if (cols == 128) return kGemvDefaultConfig + 4;   // 16 waves, staged
   const bool stage = split <= 1 && ks <= 16384 && cols >= 64;
   if (stage) return kGemvDefaultConfig + 3;
   return (M == 1 || ks <= 8192) ? 2 : kGemvDefaultConfig;
@@ -104,12 +111,12 @@ int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
 // split-order reduction kernel): with K >= 8192 and fewer column blocks than
 // CUs, four splits win 12-50 % (K = 14336, N = 1024: 11.7 -> 7.3 us;
 // K = 28672, N = 1024: 20.5 -> 10.0 us); at K = 4096 the extra pass costs more
-// than the extra workgroups recover (4.6 -> 5.4 us); at one block per CU it is
-// neutral to 3 % slower; 3 or 6 splits, whose row ranges cut quantisation
-// groups, lose to 4.
+// than the extra workgroups recover (4.6 -> 5.4 us); at (nearly) one block per
+// CU it is neutral to 3 % slower; 3 or 6 splits, whose row ranges cut
+// quantisation groups, lose to 4.
 int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
   const int64_t nblk = (N + cols - 1) / cols;
-  return (K / 8 >= 1024 && nblk < cus) ? 4 : 1;
+  return (K / 8 >= 1024 && nblk < cus * 7 / 8) ? 4 : 1;
 }
 
 // Prefill tile configuration by shape (measured on MI355X, C4/C5 shapes):
@@ -277,7 +284,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   switch (kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
-      const int cols = gemv_cols_auto(N, K, cus);
+      const int cols = gemv_cols_auto(M, N, K, cus);
       int S = split > 0 ? split : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;

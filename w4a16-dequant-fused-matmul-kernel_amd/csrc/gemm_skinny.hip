@@ -31,8 +31,10 @@
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
 //     the buffer range check;
-//   * dequant is the packed-fp16 magic-number form, then the pairs are put back
-//     in natural k order (4 v_perm per word) so activations need no permutation;
+//   * dequant is the packed-fp16 magic-number form; its pairs come out in the
+//     order (w0 w4, w1 w5, w2 w6, w3 w7), and the MFMA's k order is matched by
+//     permuting the activation fragment (one m-tile, or more n-tiles than
+//     m-tiles) or else the words back to natural order;
 //   * the waves' 16x16 fp32 tiles are summed in LDS in wave order
 //     (deterministic) and rounded to fp16 once; optional fp16 bias add;
 //   * workgroup -> column block is XCD-aware (consecutive blocks share an XCD).
@@ -187,17 +189,31 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
       // trip each.  The two-batch loop skips them (measured faster there: C5
       // M = 16, K = 28672 took 47.4 us branch-free against 40.4).
       if (!ONE_BATCH && s0 + j >= ke) break;   // wave-uniform
+      // Dequantised words come out in pair order (w0 w4, w1 w5, ...).  The
+      // MFMA sums over k in whatever order both operands share, so either the
+      // activation fragments (4 v_perm per m-tile) or the words (4 per word
+      // and n-tile) are permuted, whichever is fewer: measured on MI355X,
+      // 64-column blocks M = 1 / 4 / 16, K = 4096, N = 28672: 17.7 / 18.8 /
+      // 21.2 -> 16.5 / 17.3 / 20.8 us with the activations permuted; M = 32 on
+      // 32-column blocks (two m-tiles, two n-tiles) 11.9 vs 12.3 us the other way.
+      constexpr bool kXPerm = MT == 1 || NT > MT;
+      uint4 xa[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xa[mt] = kXPerm ? perm_pairs(b.x[j][mt]) : b.x[j][mt];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const ColQ cq = make_colq(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
         f16x2 d[4];
         dq_word_fast(b.w[j][t], cq, mg, d);
-        // natural k order: w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
-        const f16x8 bf = f16x8{d[0].x, d[1].x, d[2].x, d[3].x, d[0].y, d[1].y, d[2].y, d[3].y};
+        // kXPerm: the words in pair order (w0 w4 w1 w5 w2 w6 w3 w7), the
+        // activations permuted to match; else natural k order:
+        // w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
+        const f16x8 bf = kXPerm ? f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y}
+                                : f16x8{d[0].x, d[1].x, d[2].x, d[3].x, d[0].y, d[1].y, d[2].y, d[3].y};
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(f16x8, b.x[j][mt]), bf, acc[mt][t], 0, 0, 0);
+              __builtin_bit_cast(f16x8, xa[mt]), bf, acc[mt][t], 0, 0, 0);
       }
     }
   };

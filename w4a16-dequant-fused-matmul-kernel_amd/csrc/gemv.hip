@@ -40,6 +40,9 @@ namespace {
 
 constexpr int kXsEntries = 2048;          // LDS activation slots (16 B each): 32 KiB
 constexpr int kNonTemporal = 2;           // buffer-load cache policy: nt
+#ifndef W4A16_GEMV_DEPTH3
+#define W4A16_GEMV_DEPTH3 0
+#endif
 
 template <int WAVES>
 struct GemvShape {
@@ -77,6 +80,19 @@ __device__ __forceinline__ void gemv_reduce_store(float (&acc)[MT][4],
       }
       const float r = fold_rows4(v[0], v[1], v[2], v[3]);
       if ((lane & 15) < CWL) red[wave][m][4 * cq + (lane >> 4)] = r;
+    }
+  } else if constexpr (CWL == 32) {
+    // the wave's two halves hold the same 32 column quads (two row-lanes):
+    // after the swaps the lower half holds columns 0 and 2 of each quad summed
+    // over both halves, the upper half columns 1 and 3
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float v0 = acc[m][0], v1 = acc[m][1], v2 = acc[m][2], v3 = acc[m][3];
+      permlane32_swap(v0, v1);
+      permlane32_swap(v2, v3);
+      const int hi = lane >> 5;
+      red[wave][m][4 * cq + hi] = v0 + v1;
+      red[wave][m][4 * cq + 2 + hi] = v2 + v3;
     }
   } else {
 #pragma unroll
@@ -281,6 +297,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       // path and the waits below count exactly; the scheduling barrier keeps
       // the activation permutes, and their waits, behind the weight loads.
       load_batch(lb, le, ba);
+#if W4A16_GEMV_DEPTH3
+      if constexpr (MT <= 2) load_batch(lb + BR, le, bb);
+#endif
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
@@ -304,6 +323,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       if (nbat == 1) {
         process(ba, lb, le, c0);
       } else {
+#if W4A16_GEMV_DEPTH3
+        Batch bc;
+        for (int i = 0; i < nbat; i += 3) {
+          const int r0 = lb + i * BR;
+          load_batch(r0 + 2 * BR, le, bc);
+          process(ba, r0, le, c0);
+          if (i + 1 >= nbat) break;
+          load_batch(r0 + 3 * BR, le, ba);
+          process(bb, r0 + BR, le, c0);
+          if (i + 2 >= nbat) break;
+          load_batch(r0 + 4 * BR, le, bb);
+          process(bc, r0 + 2 * BR, le, c0);
+        }
+#else
         for (int i = 0; i < nbat; i += 2) {
           const int r0 = lb + i * BR;
           load_batch(r0 + BR, le, bb);
@@ -311,6 +344,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
           load_batch(r0 + 2 * BR, le, ba);
           process(bb, r0 + BR, le, c0);
         }
+#endif
       }
     } else {
       for (int r0 = lb; r0 < le; r0 += 2 * BR) {
@@ -510,6 +544,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
     process(ba);
   } else {
     const int nbat = (re - rb + BR * RL - 1) / (BR * RL);
+#if W4A16_GEMV_DEPTH3
+    Batch bc;
+    load_batch(1, bb);
+    for (int b = 0; b < nbat; b += 3) {
+      load_batch(b + 2, bc);
+      process(ba);
+      if (b + 1 >= nbat) break;
+      load_batch(b + 3, ba);
+      process(bb);
+      if (b + 2 >= nbat) break;
+      load_batch(b + 4, bb);
+      process(bc);
+    }
+#else
     for (int b = 0; b < nbat; b += 2) {
       load_batch(b + 1, bb);
       process(ba);
@@ -517,6 +565,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
       load_batch(b + 2, ba);
       process(bb);
     }
+#endif
   }
 
   gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
@@ -574,6 +623,7 @@ hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_
     case 16: return launch_cwl<MT, 4, WAVES, STAGE>(a, split, ws, st);
     case 32: return launch_cwl<MT, 8, WAVES, STAGE>(a, split, ws, st);
     case 64: return launch_cwl<MT, 16, WAVES, STAGE>(a, split, ws, st);
+    case 128: return launch_cwl<MT, 32, WAVES, STAGE>(a, split, ws, st);
     case 256: return launch_cwl<MT, 64, WAVES, STAGE>(a, split, ws, st);
     default: return hipErrorInvalidValue;
   }
@@ -601,7 +651,9 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, 
 
 }  // namespace
 
-bool gemv_cols_valid(int cols) { return cols == 16 || cols == 32 || cols == 64 || cols == 256; }
+bool gemv_cols_valid(int cols) {
+  return cols == 16 || cols == 32 || cols == 64 || cols == 128 || cols == 256;
+}
 bool gemv_cfg_valid(int cfg, int M) { return cfg == 1 || (M <= 2 && (cfg == 2 || cfg == 4 || cfg == 5)); }
 
 int gemv_rows_per_split(int K, int split) {
