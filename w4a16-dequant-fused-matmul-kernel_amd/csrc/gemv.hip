@@ -4,15 +4,21 @@
 // (w4a16-kernel/src/w4a16/triton_kernel.py:62-128 at M = 1..16, BLOCK_M >= 16).
 //
 // Layout of the work (both kernels):
-//   * a workgroup (WAVES waves) owns a block of CW = 4*CWL consecutive columns;
-//     in a wave, CWL lanes cover one packed row (one dwordx4 = 4 columns per
-//     lane) and the wave's 64/CWL row-lanes sit on different packed rows;
+//   * a workgroup (WAVES waves) owns a block of CW = 4*CWL consecutive columns
+//     (16, 32, 64, 128 or 256); in a wave, CWL lanes cover one packed row (one
+//     dwordx4 = 4 columns per lane) and the wave's 64/CWL row-lanes sit on
+//     different packed rows;
 //   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
 //     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
 //     weights are read with the non-temporal hint: each byte is used once;
 //   * reduction over row-lanes: DPP row rotations and a permlane
-//     transpose-reduce inside the wave, then the waves in order through LDS --
-//     deterministic (gemv_reduce_store);
+//     transpose-reduce inside the wave (two permlane32 swaps for 128-column
+//     blocks), then the waves in order through LDS -- deterministic
+//     (gemv_reduce_store);
+//   * at most two register batches per lane are in flight: a third (loads two
+//     batches ahead) measured 3-23 % slower on every multi-batch shape, its
+//     registers costing a workgroup per CU (M = 1, K = 4096, N = 28672 16.4 ->
+//     20.2 us on 64-column blocks, 15.5 -> 16.2 on 128-column blocks);
 //   * workgroup -> column block is XCD-aware: the hardware deals workgroups to the
 //     8 XCDs round-robin, and consecutive column blocks are given to the same XCD
 //     so that neighbouring row segments share that XCD's L2 lines (measured on
@@ -40,9 +46,6 @@ namespace {
 
 constexpr int kXsEntries = 2048;          // LDS activation slots (16 B each): 32 KiB
 constexpr int kNonTemporal = 2;           // buffer-load cache policy: nt
-#ifndef W4A16_GEMV_DEPTH3
-#define W4A16_GEMV_DEPTH3 0
-#endif
 
 template <int WAVES>
 struct GemvShape {
@@ -297,9 +300,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       // path and the waits below count exactly; the scheduling barrier keeps
       // the activation permutes, and their waits, behind the weight loads.
       load_batch(lb, le, ba);
-#if W4A16_GEMV_DEPTH3
-      if constexpr (MT <= 2) load_batch(lb + BR, le, bb);
-#endif
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
@@ -323,20 +323,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       if (nbat == 1) {
         process(ba, lb, le, c0);
       } else {
-#if W4A16_GEMV_DEPTH3
-        Batch bc;
-        for (int i = 0; i < nbat; i += 3) {
-          const int r0 = lb + i * BR;
-          load_batch(r0 + 2 * BR, le, bc);
-          process(ba, r0, le, c0);
-          if (i + 1 >= nbat) break;
-          load_batch(r0 + 3 * BR, le, ba);
-          process(bb, r0 + BR, le, c0);
-          if (i + 2 >= nbat) break;
-          load_batch(r0 + 4 * BR, le, bb);
-          process(bc, r0 + 2 * BR, le, c0);
-        }
-#else
         for (int i = 0; i < nbat; i += 2) {
           const int r0 = lb + i * BR;
           load_batch(r0 + BR, le, bb);
@@ -344,7 +330,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
           load_batch(r0 + 2 * BR, le, ba);
           process(bb, r0 + BR, le, c0);
         }
-#endif
       }
     } else {
       for (int r0 = lb; r0 < le; r0 += 2 * BR) {
@@ -544,20 +529,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
     process(ba);
   } else {
     const int nbat = (re - rb + BR * RL - 1) / (BR * RL);
-#if W4A16_GEMV_DEPTH3
-    Batch bc;
-    load_batch(1, bb);
-    for (int b = 0; b < nbat; b += 3) {
-      load_batch(b + 2, bc);
-      process(ba);
-      if (b + 1 >= nbat) break;
-      load_batch(b + 3, ba);
-      process(bb);
-      if (b + 2 >= nbat) break;
-      load_batch(b + 4, bb);
-      process(bc);
-    }
-#else
     for (int b = 0; b < nbat; b += 2) {
       load_batch(b + 1, bb);
       process(ba);
@@ -565,7 +536,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
       load_batch(b + 2, ba);
       process(bb);
     }
-#endif
   }
 
   gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
