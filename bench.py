@@ -85,6 +85,9 @@ def _args():
                     help="write profiles/traffic.json from the counter_collection.csv files "
                          "of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "--traffic-probe")
+    ap.add_argument("--floor-probe", action="store_true",
+                    help="time the decode GEMV's weight-access shapes loads-only "
+                         "(csrc/floor_probe.hip) beside the GEMV itself; markdown table")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="markdown table of every counter in rocprofv3 --pmc runs of "
                          "--traffic-probe, per workload and kernel")
@@ -340,6 +343,89 @@ def to_markdown_table(results: list[dict]) -> str:
     return header + "\n".join(rows) + "\n"
 
 
+# --floor-probe: the decode GEMV's weight-access shapes with the dequant and
+# dot products taken out (csrc/floor_probe.hip).  (label, config, K, N)
+FLOOR_SHAPES = [("C2", "C2", 4096, 4096), ("C3 N=28672", "C3", 4096, 28672),
+                ("C5 K=8192", "C5", 8192, 28672), ("C5 K=28672", "C5", 28672, 8192)]
+# rows: (column-block bytes, waves, rows per lane per batch); linear: (workgroups,
+# waves, loads per lane in flight)
+FLOOR_ROWS = [(64, 16, 2), (64, 8, 4), (128, 16, 2), (256, 8, 4), (256, 16, 2), (512, 8, 4),
+              (512, 16, 2)]
+FLOOR_LINEAR = [(256, 8, 4), (512, 8, 4), (1024, 4, 8)]
+
+
+def floor_probe(steps: int) -> str:
+    """Markdown table: µs per call and GB/s of packed-weight bytes for the
+    loads-only probe's row shapes (a GEMV column block of 64 / 128 / 256 / 512
+    bytes, i.e. 16 / 32 / 64 / 128 columns) and linear reads of the same bytes, cold like
+    the bench (rotating copies), beside the GEMV's default plan on the M = 1,
+    G = 128 case of each shape (its GB/s also counts scales, zeros, x, y)."""
+    import ctypes
+
+    import torch
+    from w4a16 import _build
+    from w4a16 import workloads as wl
+
+    lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    lib.w4a16_probe_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
+    lib.w4a16_probe_linear.argtypes = [vp, ctypes.c_uint32, i32, i32, i32, vp, vp]
+    lib.w4a16_probe_rows_out_words.restype = ctypes.c_int64
+    lib.w4a16_probe_rows_out_words.argtypes = [i32, i32, i32]
+    lib.w4a16_probe_linear_out_words.restype = ctypes.c_int64
+    lib.w4a16_probe_linear_out_words.argtypes = [i32, i32]
+    rows = ["| shape | packed weights | access | µs | GB/s |", "|---|---|---|---|---|"]
+    for label, cfg, K, N in FLOOR_SHAPES:
+        KP, row_bytes = K // 8, N * 4
+        nbytes = KP * row_bytes
+        ncopy = max(2, -(-COLD_BYTES // nbytes) + 1)
+        bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+                for _ in range(ncopy)]
+
+        def timed(launch) -> float:
+            fns = [(lambda b=b: launch(b)) for b in bufs]
+            return _time_calls(fns, steps, 10, False)["ms"] * 1e3
+
+        shapes = []
+        for cwb, waves, br in FLOOR_ROWS:
+            if row_bytes % cwb:
+                continue
+            out = torch.empty(lib.w4a16_probe_rows_out_words(row_bytes, cwb, waves),
+                              dtype=torch.int32, device="cuda")
+
+            def launch(b, cwb=cwb, waves=waves, br=br, out=out):
+                rc = lib.w4a16_probe_rows(b.data_ptr(), KP, row_bytes, cwb, waves, br,
+                                          out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                if rc:
+                    raise RuntimeError(f"w4a16_probe_rows: {rc}")
+            shapes.append((f"rows: {cwb // 4}-column blocks ({row_bytes // cwb} workgroups), "
+                           f"{waves} waves, {br} rows/lane/batch", launch))
+        for nwg, waves, br in FLOOR_LINEAR:
+            out = torch.empty(lib.w4a16_probe_linear_out_words(nwg, waves), dtype=torch.int32,
+                              device="cuda")
+
+            def launch(b, nwg=nwg, waves=waves, br=br, out=out):
+                rc = lib.w4a16_probe_linear(b.data_ptr(), nbytes, nwg, waves, br, out.data_ptr(),
+                                            torch.cuda.current_stream().cuda_stream)
+                if rc:
+                    raise RuntimeError(f"w4a16_probe_linear: {rc}")
+            shapes.append((f"linear: {nwg} workgroups of {waves} waves, {br} loads/lane", launch))
+        for what, launch in shapes:
+            us = timed(launch)
+            rows.append(f"| {label} | {nbytes / 2**20:.1f} MiB | {what} | {us:.2f} | "
+                        f"{nbytes / us / 1e3:.0f} |")
+            print(rows[-1], file=sys.stderr, flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+        case = [c for c in wl.CONFIGS[cfg] if (c.M, c.K, c.N, c.G) == (1, K, N, 128)][0]
+        r = bench_case(case, steps, 10, cold=True)
+        rows.append(f"| {label} | {nbytes / 2**20:.1f} MiB | GEMV as planned ({r['kernel']} "
+                    f"{r['tile'][1]}-column blocks, cfg {r['tile_cfg']}), with dequant and dot "
+                    f"products | {r['us']:.2f} | {r['GB/s']:.0f} (all bytes) |")
+        print(rows[-1], file=sys.stderr, flush=True)
+    return "\n".join(rows)
+
+
 def reference_table(json_path: str | None) -> dict:
     from w4a16 import workloads as wl
 
@@ -558,6 +644,9 @@ def main() -> int:
         return 0
     if args.reference_table:
         print(json.dumps(reference_table(args.reference_json)), flush=True)
+        return 0
+    if args.floor_probe:
+        print(floor_probe(max(20, args.steps // 4)), flush=True)
         return 0
     from w4a16 import workloads as wl
 

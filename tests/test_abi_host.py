@@ -577,3 +577,25 @@ def test_stale_library_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_sources_hash", lambda: "0" * 64)
     with pytest.raises(ImportError, match="other sources"):
         _lib.load()
+
+
+def test_floor_probe_library_exports():
+    """bench.py --floor-probe's loads-only library is built beside libw4a16.so,
+    exports its entry points, sizes its output and refuses shapes it has no
+    kernel for before any launch (no GPU call here)."""
+    import ctypes
+
+    from w4a16 import _build
+
+    lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
+    for name in ("w4a16_probe_rows", "w4a16_probe_linear", "w4a16_probe_rows_out_words",
+                 "w4a16_probe_linear_out_words"):
+        assert hasattr(lib, name), name
+    lib.w4a16_probe_rows_out_words.restype = ctypes.c_int64
+    assert lib.w4a16_probe_rows_out_words(114688, 512, 8) == 224 * 512
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    lib.w4a16_probe_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
+    lib.w4a16_probe_linear.argtypes = [vp, ctypes.c_uint32, i32, i32, i32, vp, vp]
+    assert lib.w4a16_probe_rows(None, 512, 16384, 48, 8, 4, None, None) == -1   # 16384 % 48
+    assert lib.w4a16_probe_rows(None, 1 << 20, 16384, 64, 8, 4, None, None) == -1  # >= 2 GiB
+    assert lib.w4a16_probe_linear(None, 1000, 3, 8, 4, None, None) == -1       # 1000 % 48

@@ -2,8 +2,11 @@
 
     python -m w4a16._build            # from the package directory's parent
 
-Every source under ``csrc/`` is compiled for gfx950 only, then linked into
-``w4a16/libw4a16.so`` next to this file, where :mod:`w4a16._lib` loads it.
+The library's sources under ``csrc/`` are compiled for gfx950 only, then linked
+into ``w4a16/libw4a16.so`` next to this file, where :mod:`w4a16._lib` loads it.
+``csrc/floor_probe.hip`` (bench.py's loads-only probe of the decode GEMV's
+access shapes) is linked on its own into ``w4a16/libw4a16_floor_probe.so``;
+nothing in the library uses it.
 """
 from __future__ import annotations
 
@@ -19,6 +22,8 @@ ROOT_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT_DIR, "csrc")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libw4a16.so")
+PROBE_SOURCE = "floor_probe.hip"
+PROBE_LIB_PATH = os.path.join(PKG_DIR, "libw4a16_floor_probe.so")
 SOURCES = ["gemv.hip", "gemm_mfma.hip", "gemm_occ2.hip", "gemm_stream.hip", "gemm_skinny.hip",
            "simt.hip", "quant.hip", "capi.cpp"]
 HEADERS = ["w4a16_device.h", "w4a16_launch.h"]
@@ -74,21 +79,29 @@ def _compile(src: str, verbose: bool, defines: list[str]) -> str:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every source and link libw4a16.so; returns the library path."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
-    defines = [f'-DW4A16_SOURCE_HASH="{source_hash()}"']
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose, defines), SOURCES))
-    tmp = LIB_PATH + ".tmp"
+def _link(objs: list[str], path: str, verbose: bool) -> None:
+    tmp = path + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every source and link libw4a16.so (and the floor probe's
+    library); returns the library path."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    jobs = jobs or min(len(SOURCES) + 1, os.cpu_count() or 1, 8)
+    defines = [f'-DW4A16_SOURCE_HASH="{source_hash()}"']
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        probe = ex.submit(_compile, PROBE_SOURCE, verbose, [])
+        objs = list(ex.map(lambda s: _compile(s, verbose, defines), SOURCES))
+        probe_obj = probe.result()
+    _link(objs, LIB_PATH, verbose)
+    _link([probe_obj], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 
