@@ -157,7 +157,21 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int CW = 4 * CWL;              // columns per workgroup
   constexpr int CHUNK = kXsEntries / MT / BR * BR;   // packed rows of X per stage
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
-  __shared__ uint4 xs[MT * CHUNK];
+  // M <= 2 on 64-column and wider blocks: every row of a lane's run is
+  // processed without a range check.  The run's end `le` is a multiple of the
+  // batch (K % 32 == 0, splits and chunks in whole batches), so a batch is
+  // wholly inside or wholly past it, and a batch past it loads zero words,
+  // scales and zeros (out-of-range offsets): its weights dequantise to exactly
+  // 0, and its activation index is clamped to a zero row (so 0 * x never
+  // meets an inf or NaN of another row).  The per-row branch had put every
+  // row's dequant under an exec mask and the next batch's loads between them:
+  // measured on MI355X without it, M = 1, K = 8192, N = 28672 on 128-column
+  // blocks 27.0 -> 25.6 us, K = 4096 16.0 -> 15.4, M = 2 30.2 -> 29.2, N = 16384
+  // on 64-column blocks 10.4 -> 9.8; on 16-column blocks (never staged by the
+  // planner) it measured slower.  XS: per m, CHUNK staged rows and that zero row.
+  constexpr bool kBranchFree = MT <= 2 && CWL >= 16;
+  constexpr int XS = kBranchFree ? CHUNK + 1 : CHUNK;
+  __shared__ uint4 xs[MT * XS];
   __shared__ float red[WAVES][MT][CW];
 
   // 16-column blocks: every kernel argument in one batch of scalar loads up
@@ -248,7 +262,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       for (int uu = 0; uu < RH; ++uu) {
         const int u = h * RH + uu;
         const int r = r0 + u;
-        if (r >= le) break;
+        if (!kBranchFree && r >= le) break;
         f16x2 d[4][4];
         dq_word_fast(b.w[u].x, cq4[0], mg, d[0]);
         dq_word_fast(b.w[u].y, cq4[1], mg, d[1]);
@@ -256,7 +270,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const uint4 xp = xs[m * CHUNK + (r - c0)];
+          const uint4 xp = xs[m * XS + (kBranchFree ? min(r - c0, CHUNK) : r - c0)];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             float a = acc[m][c];
@@ -304,14 +318,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
         const int idx = tid + i * kThreads;
-        if (idx < MT * CHUNK) xs[idx] = perm_pairs(xv[i]);
+        if (idx < MT * CHUNK) xs[(idx / CHUNK) * XS + idx % CHUNK] = perm_pairs(xv[i]);
+      }
+      if constexpr (XS > CHUNK) {
+        if (tid < MT) xs[tid * XS + CHUNK] = make_uint4(0u, 0u, 0u, 0u);
       }
       __syncthreads();
     }
 
     // Two register batches used ping-pong.  M <= 2: the trip count is the same
     // for every lane (`per` rows; past its own run a lane's loads read nothing
-    // and process() skips its rows), and the loads are unconditional, so every
+    // and process() skips its rows or, branch-free, adds their zeros), and the
+    // loads are unconditional, so every
     // path has the same loads in flight and the compiler's waits count
     // exactly (with lane-dependent branches around the loads, its waits at the
     // joins covered the next batch too: 2-10 % slower on multi-batch runs); a
