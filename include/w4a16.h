@@ -49,7 +49,7 @@ enum w4a16_status {
 /* Kernel families a plan can name. */
 enum w4a16_kernel {
   W4A16_KERNEL_AUTO = 0,
-  W4A16_KERNEL_GEMV = 1, /* decode: VALU dot2, no MFMA, M <= 8, optional split-K    */
+  W4A16_KERNEL_GEMV = 1, /* decode, M <= 8: VALU dequant, dot2 or MFMA dot, split-K */
   W4A16_KERNEL_MFMA = 2, /* prefill: MFMA (32x32x16 / 16x16x32), tile_cfg below     */
   W4A16_KERNEL_SIMT = 3, /* sequential-k, one thread per output, any shape           */
   W4A16_KERNEL_SKINNY = 4 /* small batch: v_mfma_f32_16x16x32_f16, weights streamed   */
@@ -63,7 +63,10 @@ typedef struct w4a16_plan {
                               tile_n); GEMV: 1 / 2 = 8 / 16 waves per workgroup
                               (16 for M <= 2), 4 / 5 = the same with the
                               activations staged in LDS (M <= 2; larger M
-                              always stages them); SKINNY: 0 / 2 / 3 = 16 / 32 /
+                              always stages them), 6 / 7 = 16 / 8 waves
+                              staged with the dot products on the matrix
+                              cores (M <= 2, 64-column blocks only); SKINNY:
+                              0 / 2 / 3 = 16 / 32 /
                               64-column blocks (32: M <= 32, N even; 64:
                               M <= 16, N % 4 == 0), 4 to 16 waves by K.
                               Other numbers name

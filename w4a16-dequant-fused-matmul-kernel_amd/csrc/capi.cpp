@@ -71,12 +71,13 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 // (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
 // 7.5 us at M = 2).
 int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
-  // M <= 2: 128-column blocks where they give at least 7/8 of the CUs one
+  // M = 1: 128-column blocks where they give at least 7/8 of the CUs one
   // each (N = 28672 on MI355X: 224), a workgroup per CU reading 512-byte row
   // segments (measured on MI355X, 16 waves with staged activations against
-  // 64-column blocks of 8: M = 1, K = 4096, N = 28672 15.4 vs 16.4 us; K = 8192
-  // 26.5 vs 28.6; G = 32 26.9 vs 29.6; M = 2, K = 8192 31.5 vs 32.2)
-  if (M <= 2 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
+  // 64-column blocks of 8: K = 4096, N = 28672 15.4 vs 16.4 us; K = 8192 26.5
+  // vs 28.6; G = 32 26.9 vs 29.6).  M = 2 keeps 64-column blocks, whose dot
+  // products go to the matrix cores (gemv_waves_cfg: 26.8 us there).
+  if (M == 1 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
     if ((N + c - 1) / c >= cus) {
@@ -89,10 +90,12 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
 
 // GEMV waves per workgroup and activation staging (measured on MI355X with
 // the sweep-ordered direct kernel for M <= 2, medians of 3 runs of 60 calls):
-//   * 64-column blocks stage the activations in LDS (cfg 4: 8 waves): 16
-//     lanes share a row, and one load and one permute per element beat one
-//     per lane (M = 1, K = 4096, N = 28672: 16.2 us against 18.6 direct; M = 1,
-//     K = 8192, N = 28672: 27.9 against 32.3; M = 2 likewise);
+//   * 64-column blocks stage the activations in LDS: 16 lanes share a row,
+//     and one load and one permute per element beat one per lane (M = 1, K =
+//     4096, N = 28672: 16.2 us against 18.6 direct; M = 1, K = 8192, N = 28672:
+//     27.9 against 32.3; M = 2 likewise), with the dot products on the matrix
+//     cores (cfg 7, 8 waves; gemv.hip); 256-column blocks the same with dot2
+//     (cfg 4), 128-column blocks with 16 waves (cfg 5);
 //   * 16- and 32-column blocks read them directly with 16 waves (cfg 2) at
 //     M = 1 for any K (K = 28672, N = 8192: 27.2 us against 30.8 with 8 waves
 //     and 28.7 staged; K = 14336, N = 4096: 11.7 against 11.9 staged; C2 4.7)
@@ -103,6 +106,8 @@ int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   if (M > 2) return kGemvDefaultConfig;
   if (cols == 128) return kGemvDefaultConfig + 4;   // 16 waves, staged
   const bool stage = split <= 1 && ks <= 16384 && cols >= 64;
+  // 64-column blocks: the dot products on the matrix cores (cfg 7, 8 waves)
+  if (stage && cols == 64) return kGemvDefaultConfig + 6;
   if (stage) return kGemvDefaultConfig + 3;
   return (M == 1 || ks <= 8192) ? 2 : kGemvDefaultConfig;
 }
@@ -388,7 +393,8 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
   switch (p->kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G) || !fits(M, N, K, G) || p->split_k < 1 ||
-          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n) || !gemv_cfg_valid(p->tile_cfg, (int)M))
+          p->split_k > K / 8 || !gemv_cols_valid(p->tile_n) ||
+          !gemv_cfg_valid(p->tile_cfg, (int)M, p->tile_n))
         return W4A16_ERR_BAD_PLAN;
       const int64_t nblk = (N + p->tile_n - 1) / p->tile_n;
       if (nblk * p->split_k > INT32_MAX) return W4A16_ERR_BAD_PLAN;

@@ -9,7 +9,9 @@
 //     dwordx4 = 4 columns per lane) and the wave's 64/CWL row-lanes sit on
 //     different packed rows;
 //   * dequant is the packed-fp16 magic-number form (w4a16_device.h); the dot
-//     product is v_dot2_f32_f16 with fp32 accumulation; no MFMA is used;
+//     product is v_dot2_f32_f16 with fp32 accumulation, or (staged kernel,
+//     64-column blocks, M <= 2, cfg 6 / 7) v_mfma_f32_16x16x32_f16 with the
+//     activations broadcast over its m-rows;
 //     weights are read with the non-temporal hint: each byte is used once;
 //   * reduction over row-lanes: DPP row rotations and a permlane
 //     transpose-reduce inside the wave (two permlane32 swaps for 128-column
@@ -62,6 +64,12 @@ struct GemvShape {
 // (register-to-register, fixed order); the per-wave sums go through LDS once
 // and thread t < CW adds the WAVES partial sets of its column in wave order.
 template <int MT, int CWL, int WAVES>
+__device__ __forceinline__ void gemv_sum_waves_store(float (&red)[WAVES][MT][4 * CWL], int tid,
+                                                     int cb, int sk, int S, int N, int ldy,
+                                                     const f16* __restrict__ bias,
+                                                     f16* __restrict__ Y, float* __restrict__ part);
+
+template <int MT, int CWL, int WAVES>
 __device__ __forceinline__ void gemv_reduce_store(float (&acc)[MT][4],
                                                   float (&red)[WAVES][MT][4 * CWL], int tid,
                                                   int cb, int sk, int S, int N, int ldy,
@@ -104,7 +112,18 @@ __device__ __forceinline__ void gemv_reduce_store(float (&acc)[MT][4],
           make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
   }
   __syncthreads();
+  gemv_sum_waves_store<MT, CWL, WAVES>(red, tid, cb, sk, S, N, ldy, bias, Y, part);
+}
 
+// Second half of the reduction (after the barrier): thread t < CW adds the
+// WAVES partial sets of column t in wave order and writes y (S == 1: fp16 RNE,
+// optional fp16 bias) or this k-split's fp32 partials.
+template <int MT, int CWL, int WAVES>
+__device__ __forceinline__ void gemv_sum_waves_store(float (&red)[WAVES][MT][4 * CWL], int tid,
+                                                     int cb, int sk, int S, int N, int ldy,
+                                                     const f16* __restrict__ bias,
+                                                     f16* __restrict__ Y, float* __restrict__ part) {
+  constexpr int CW = 4 * CWL;
   const int t = tid;
   const int col = cb * CW + t;
   const bool cv = (t < CW) && (col < N);
@@ -140,7 +159,7 @@ __device__ __forceinline__ void gemv_reduce_store(float (&acc)[MT][4],
   }
 }
 
-template <int MT, int CWL, int WAVES, bool STAGE>
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
@@ -152,6 +171,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int H = BR / RH;               // halves per batch
   // M <= 2 without staging runs gemv_direct_kernel; here X is staged in LDS
   static_assert(MT > 2 || STAGE, "M <= 2 with direct activations is gemv_direct_kernel");
+  // MF: the dot products on the matrix cores (v_mfma_f32_16x16x32_f16).  With
+  // 16 lanes per packed row (64-column blocks) a wave's lanes are 16 column
+  // quads x 4 row-lanes, which is the MFMA's B layout (lane l: n = l % 16,
+  // k-octet l / 16) with word t of the quad as n-tile t; each lane's
+  // activation octet (its own row, from LDS) is the A operand, the same in all
+  // 16 m-rows for M = 1 (row 1 in m-row 1 for M = 2), so the MFMA sums over
+  // the wave's four row-lanes and leaves y in every m-row.  Rows past a lane's
+  // run add zeros (kBranchFree), so every lane can take part in every MFMA.
+  // Measured on MI355X (cfg 7: 8 waves; 144 registers, one workgroup per CU)
+  // against the dot2 form of the same blocks: M = 2, K = 8192, N = 28672 32.9
+  // -> 26.8 us; M = 1, K = 4096, N = 16384 9.9 -> 9.5; K = 8192, N = 16384
+  // 15.5 -> 15.0.  Capped at 128 registers (two workgroups per CU) it spilled
+  // and ran 15-20 % slower.
+  static_assert(!MF || (CWL == 16 && MT <= 2), "MFMA dot products: 64-column blocks, M <= 2");
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
   constexpr int CW = 4 * CWL;              // columns per workgroup
@@ -226,6 +259,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
+  f32x4 macc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) macc[c] = f32x4{};
+  // MF, M = 2: m-row 1 of the A operand (lanes with lane % 16 == 1) is x row 1
+  const int xrow = (MF && MT == 2 && (lane & 15) == 1) ? 1 : 0;
 
   struct Batch {
     uint2 s[H], z[H];
@@ -268,6 +306,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         dq_word_fast(b.w[u].y, cq4[1], mg, d[1]);
         dq_word_fast(b.w[u].z, cq4[2], mg, d[2]);
         dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
+        if constexpr (MF) {
+          // both operands in pair order: (w0 w4 w1 w5 w2 w6 w3 w7) against the
+          // activations permuted the same way when they were staged
+          const uint4 xp = xs[xrow * XS + min(r - c0, CHUNK)];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            macc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(f16x8, xp),
+                f16x8{d[c][0].x, d[c][0].y, d[c][1].x, d[c][1].y, d[c][2].x, d[c][2].y,
+                      d[c][3].x, d[c][3].y},
+                macc[c], 0, 0, 0);
+          continue;
+        }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const uint4 xp = xs[m * XS + (kBranchFree ? min(r - c0, CHUNK) : r - c0)];
@@ -360,7 +411,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     }
   }
 
-  gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
+  if constexpr (MF) {
+    // lanes 0..15 hold column quad `lane` (all m-rows alike, m-row m = y row m
+    // in component m): one partial set per wave into LDS, then the waves in order
+    if (lane < 16) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = macc[c][m];
+    }
+    __syncthreads();
+    gemv_sum_waves_store<MT, CWL, WAVES>(red, tid, cb, sk, S, N, ldy, bias, Y, part);
+  } else {
+    gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
+  }
 }
 
 // M <= 2 with the activations read directly (no LDS staging): the rows of a
@@ -559,7 +623,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
   gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
 }
 
-template <int MT, int CWL, int WAVES, bool STAGE>
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL;
   const int nblk = (a.N + CW - 1) / CW;
@@ -594,7 +658,7 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
     da.part = part;
     hipLaunchKernelGGL(kern, dim3(nblk * split), dim3(GemvShape<WAVES>::kThreads), 0, st, da);
   } else
-    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE>), dim3(nblk * split),
+    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF>), dim3(nblk * split),
                        dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                        reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                        static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
@@ -618,9 +682,10 @@ hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_
 }
 
 // cfg 1 / 2: 8 / 16 waves; cfg 4 / 5: the same with the activations staged in
-// LDS for M <= 2 (larger M always stages them).  16 waves only for M <= 2
-// (the reduction buffer grows with waves x M).  cfg 0 / 3 (4 waves) measured
-// slower everywhere and were retired.
+// LDS for M <= 2 (larger M always stages them); cfg 6 / 7: 16 / 8 waves,
+// staged, with the dot products on the matrix cores (M <= 2, 64-column blocks
+// only).  16 waves only for M <= 2 (the reduction buffer grows with waves x
+// M).  cfg 0 / 3 (4 waves) measured slower everywhere and were retired.
 template <int MT>
 hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {
   if constexpr (MT <= 2) {
@@ -629,6 +694,12 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, 
       case 2: return launch_w<MT, 16, false>(a, cols, split, ws, st);
       case 4: return launch_w<MT, 8, true>(a, cols, split, ws, st);
       case 5: return launch_w<MT, 16, true>(a, cols, split, ws, st);
+      case 6:
+        if (cols != 64) return hipErrorInvalidValue;
+        return launch_cwl<MT, 16, 16, true, true>(a, split, ws, st);
+      case 7:
+        if (cols != 64) return hipErrorInvalidValue;
+        return launch_cwl<MT, 16, 8, true, true>(a, split, ws, st);
       default: return hipErrorInvalidValue;
     }
   } else {
@@ -642,7 +713,10 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, 
 bool gemv_cols_valid(int cols) {
   return cols == 16 || cols == 32 || cols == 64 || cols == 128 || cols == 256;
 }
-bool gemv_cfg_valid(int cfg, int M) { return cfg == 1 || (M <= 2 && (cfg == 2 || cfg == 4 || cfg == 5)); }
+bool gemv_cfg_valid(int cfg, int M, int cols) {
+  return cfg == 1 || (M <= 2 && (cfg == 2 || cfg == 4 || cfg == 5)) ||
+         (M <= 2 && cols == 64 && (cfg == 6 || cfg == 7));
+}
 
 int gemv_rows_per_split(int K, int split) {
   const int KP = K / 8;

@@ -41,20 +41,20 @@ inline uint64_t x_extent_bytes(const GemmArgs& a) {
   return a.M > 0 && a.K > 0 ? ((uint64_t)(a.M - 1) * (uint64_t)a.ldx + (uint64_t)a.K) * 2u : 0;
 }
 
-// Decode GEMV (VALU, no MFMA), M <= kGemvMaxM.  A workgroup owns `cols`
-// consecutive columns (16, 32, 64 or 256) and K/8/split packed rows; `cfg`
-// picks 8 (cfg 1) or 16 (cfg 2, M <= 2) waves per workgroup, and cfg 4 / 5
-// the same with the activations staged in LDS (M <= 2; larger M always
-// stages them); cfg 0 and 3 (4 waves) were retired.  With split > 1, `ws`
-// holds the fp32 partials of gemv_workspace_bytes().
+// Decode GEMV, M <= kGemvMaxM.  A workgroup owns `cols` consecutive columns
+// (16, 32, 64, 128 or 256) and K/8/split packed rows; `cfg` picks 8 (cfg 1)
+// or 16 (cfg 2, M <= 2) waves per workgroup, cfg 4 / 5 the same with the
+// activations staged in LDS (M <= 2; larger M always stages them), cfg 6 / 7
+// 16 / 8 waves staged with the dot products on the matrix cores (M <= 2,
+// 64-column blocks); cfg 0 and 3 (4 waves) were retired.  With split > 1,
+// `ws` holds the fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
-constexpr int kGemvConfigs = 6;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the
 // other's outstanding loads; the planner takes 16 waves (cfg 2) for M <= 2 on
 // narrow blocks and short rows, where they measured faster on MI355X.
 constexpr int kGemvDefaultConfig = 1;
 bool gemv_cols_valid(int cols);
-bool gemv_cfg_valid(int cfg, int M);
+bool gemv_cfg_valid(int cfg, int M, int cols);
 size_t gemv_workspace_bytes(int M, int N, int K, int split);
 int gemv_rows_per_split(int K, int split);
 hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws,
