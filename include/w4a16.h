@@ -65,7 +65,8 @@ typedef struct w4a16_plan {
                               activations staged in LDS (M <= 2; larger M
                               always stages them), 6 / 7 = 16 / 8 waves
                               staged with the dot products on the matrix
-                              cores (M <= 2, 64-column blocks only); SKINNY:
+                              cores (M <= 2, 64- or 128-column blocks);
+                              SKINNY:
                               0 / 2 / 3 = 16 / 32 /
                               64-column blocks (32: M <= 32, N even; 64:
                               M <= 16, N % 4 == 0), 4 to 16 waves by K.

@@ -136,13 +136,13 @@ def test_retired_configurations_refused(lib):
         code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, N, K, G,
                                           NULL, 0, NULL)
         assert code == (-4 if cfg in _lib.GEMV_CONFIGS else -5), cfg
-    for cols in (16, 32, 64, 128, 256):      # MFMA dot products: 64-column blocks only
+    for cols in (16, 32, 64, 128, 256):      # MFMA dot products: 64 / 128 columns only
         for cfg in _lib.GEMV_MFMA_CONFIGS:
             p = _lib.plan(1, N, K, G, _lib.KERNEL_GEMV, 4)
             p.tile_cfg, p.tile_n = cfg, cols
             code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, N, K, G,
                                               NULL, 0, NULL)
-            assert code == (-4 if cols == 64 else -5), (cfg, cols)
+            assert code == (-4 if cols in (64, 128) else -5), (cfg, cols)
     for cfg in range(6):
         p = _lib.plan(16, N, K, G, _lib.KERNEL_SKINNY, 0)
         p.tile_cfg = cfg
@@ -345,9 +345,9 @@ def test_planner_gemv_blocks_and_waves():
     M = 1 for any K and at M = 2 up to 8192 rows per split, else 8; 32-column
     blocks where 16-column ones would leave every CU between one and two blocks
     (K < 8192 only); activations staged in LDS for M <= 2 on 64-column blocks
-    (cfg 7: 8 waves, dot products on the matrix cores), 256-column blocks
-    (cfg 4) and, for M = 1, on 128-column blocks where those give 7/8 of the
-    CUs one each (cfg 5: 16 waves), one chunk, no split."""
+    and on 128-column blocks where those give 7/8 of the CUs one each (cfg 7:
+    8 waves, dot products on the matrix cores) and on 256-column blocks (cfg
+    4), one chunk, no split."""
     from w4a16 import _lib
 
     p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
@@ -364,10 +364,10 @@ def test_planner_gemv_blocks_and_waves():
     assert p.tile_cfg == 2
     p = _lib.plan(1, 16384, 4096, 128)           # 64-column blocks: 8 waves, staged, MFMA dots
     assert (p.tile_n, p.tile_cfg) == (64, 7)
-    p = _lib.plan(1, 28672, 4096, 128)           # 224 blocks of 128: 16 waves, staged
-    assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 5, 1)
-    p = _lib.plan(2, 28672, 8192, 128)           # M = 2: 64-column blocks, MFMA dots
-    assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 1)
+    p = _lib.plan(1, 28672, 4096, 128)           # 224 blocks of 128: 8 waves, MFMA dots
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
+    p = _lib.plan(2, 28672, 8192, 128)
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
     p = _lib.plan(1, 65536, 4096, 128)           # 256-column blocks: dot2, staged
     assert (p.tile_n, p.tile_cfg) == (256, 4)
     p = _lib.plan(3, 28672, 8192, 128)           # M > 2 keeps 64-column blocks

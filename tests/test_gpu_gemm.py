@@ -128,7 +128,7 @@ def test_gemv_splits(M, K, N, G):
     X, qw, s, z = _build_case(M, K, N, G, seed=M + K)
     ref = _ref(X, qw, s, z, G)
     for cfg in ((1, 2, 4, 5, 6, 7) if M <= 2 else (1,)):
-        for cols in ((64,) if cfg >= 6 else (16, 32, 64, 128, 256)):
+        for cols in ((64, 128) if cfg >= 6 else (16, 32, 64, 128, 256)):
             for split in (1, 2, 3, 7, 0):
                 if split > K // 8:
                     continue

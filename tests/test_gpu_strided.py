@@ -70,7 +70,7 @@ def test_gemv_strided(M, N):
     X, qw, s, z = _case(M, K, N, G, seed=M)
     cfgs = (1, 2, 4, 5, 6, 7) if M <= 2 else (1,)
     for cfg in cfgs:
-        for cols in ((64,) if cfg >= 6 else (16, 32, 64, 128, 256)):
+        for cols in ((64, 128) if cfg >= 6 else (16, 32, 64, 128, 256)):
             for split in (1, 4):
                 p = plan_for(M, N, K, G, "gemv", split)
                 p.tile_cfg = cfg

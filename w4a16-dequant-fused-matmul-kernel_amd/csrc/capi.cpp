@@ -71,13 +71,13 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 // (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
 // 7.5 us at M = 2).
 int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
-  // M = 1: 128-column blocks where they give at least 7/8 of the CUs one
-  // each (N = 28672 on MI355X: 224), a workgroup per CU reading 512-byte row
-  // segments (measured on MI355X, 16 waves with staged activations against
-  // 64-column blocks of 8: K = 4096, N = 28672 15.4 vs 16.4 us; K = 8192 26.5
-  // vs 28.6; G = 32 26.9 vs 29.6).  M = 2 keeps 64-column blocks, whose dot
-  // products go to the matrix cores (gemv_waves_cfg: 26.8 us there).
-  if (M == 1 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
+  // M <= 2: 128-column blocks where they give at least 7/8 of the CUs one
+  // each (N = 28672 on MI355X: 224), a workgroup per CU reading two 256-byte
+  // segments of each packed row (measured on MI355X with the dot products on
+  // the matrix cores, cfg 7, against 64-column blocks: M = 1, K = 8192,
+  // N = 28672 25.0 vs 25.9 us; K = 4096 15.0 vs 15.9; M = 2, K = 8192 25.0 vs
+  // 26.1)
+  if (M <= 2 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
     if ((N + c - 1) / c >= cus) {
@@ -104,10 +104,13 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
 int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   const int64_t ks = K / (split > 0 ? split : 1);
   if (M > 2) return kGemvDefaultConfig;
-  if (cols == 128) return kGemvDefaultConfig + 4;   // 16 waves, staged
   const bool stage = split <= 1 && ks <= 16384 && cols >= 64;
-  // 64-column blocks: the dot products on the matrix cores (cfg 7, 8 waves)
-  if (stage && cols == 64) return kGemvDefaultConfig + 6;
+  // 64- and 128-column blocks: the dot products on the matrix cores (cfg 7,
+  // 8 waves; measured on MI355X against the dot2 kernel's best, 16 waves on
+  // 128-column blocks: M = 1, K = 8192, N = 28672 25.0 vs 26.3 us, G = 32 25.8
+  // vs 26.3, K = 4096 15.0 vs 15.1; M = 2, K = 8192 25.0 vs 30.6, K = 4096
+  // 15.2 vs 17.2)
+  if (cols == 128 || (stage && cols == 64)) return kGemvDefaultConfig + 6;
   if (stage) return kGemvDefaultConfig + 3;
   return (M == 1 || ks <= 8192) ? 2 : kGemvDefaultConfig;
 }

@@ -159,7 +159,7 @@ __device__ __forceinline__ void gemv_sum_waves_store(float (&red)[WAVES][MT][4 *
   }
 }
 
-template <int MT, int CWL, int WAVES, bool STAGE, bool MF>
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF, int QPL>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
@@ -184,10 +184,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   // -> 26.8 us; M = 1, K = 4096, N = 16384 9.9 -> 9.5; K = 8192, N = 16384
   // 15.5 -> 15.0.  Capped at 128 registers (two workgroups per CU) it spilled
   // and ran 15-20 % slower.
-  static_assert(!MF || (CWL == 16 && MT <= 2), "MFMA dot products: 64-column blocks, M <= 2");
+  // QPL = 2 (MF only): each lane also takes the column quad 64 columns on,
+  // so a workgroup owns 128 columns with the same lane layout (two loads of
+  // 256 contiguous bytes per packed row and wave instead of one of 512).
+  static_assert(!MF || (CWL == 16 && MT <= 2), "MFMA dot products: 64-column layout, M <= 2");
+  static_assert(QPL == 1 || (MF && QPL == 2), "two column quads per lane: MFMA form only");
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
-  constexpr int CW = 4 * CWL;              // columns per workgroup
+  constexpr int CW = 4 * CWL * QPL;        // columns per workgroup
+  constexpr int HW = 4 * CWL;              // columns between a lane's quads
   constexpr int CHUNK = kXsEntries / MT / BR * BR;   // packed rows of X per stage
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
   // M <= 2 on 64-column and wider blocks: every row of a lane's run is
@@ -232,8 +237,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cq = lane % CWL;
   const int rl = wave * RW + lane / CWL;
-  const int n = cb * CW + 4 * cq;
-  const bool nv = n < N;
+  const int n = cb * CW + 4 * cq;            // the lane's first column quad
   const int KP = K >> 3;
   // k / G for 0 <= k < 2^31 without a division in front of the first loads:
   // (umulhi(k, gmagic) + k) >> gshift with gshift = ceil(log2 G) and gmagic =
@@ -259,15 +263,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
-  f32x4 macc[4];
+  f32x4 macc[QPL][4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) macc[c] = f32x4{};
+  for (int q = 0; q < QPL; ++q)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) macc[q][c] = f32x4{};
   // MF, M = 2: m-row 1 of the A operand (lanes with lane % 16 == 1) is x row 1
   const int xrow = (MF && MT == 2 && (lane & 15) == 1) ? 1 : 0;
 
   struct Batch {
-    uint2 s[H], z[H];
-    uint4 w[BR];
+    uint2 s[H][QPL], z[H][QPL];
+    uint4 w[BR][QPL];
   };
   // Rows r0..r0+BR-1 of this lane's run [.., le).  Row u rides in the SGPR
   // offset; weight rows at or past `le` (only in a run's last batch) read as zero.
@@ -276,25 +282,65 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     for (int h = 0; h < H; ++h) {
       // the group differs between row-lanes: its offset goes in the VGPR operand
       const int g = min(group_of((r0 + RH * h) * 8), NG - 1);
-      // a batch past the lane's run (issued only to keep the loads the same
-      // on every path) reads nothing from memory
-      const uint32_t so = (nv && r0 < le) ? s_voff + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
-      b.s[h] = buf_load8(rs, so, 0u);
-      b.z[h] = buf_load8(rz, so, 0u);
+#pragma unroll
+      for (int q = 0; q < QPL; ++q) {
+        // a batch past the lane's run (issued only to keep the loads the same
+        // on every path) reads nothing from memory
+        const bool v = n + HW * q < N && r0 < le;
+        const uint32_t so =
+            v ? s_voff + (uint32_t)(HW * q) * 2u + (uint32_t)g * (uint32_t)N * 2u : kOobOffset;
+        b.s[h][q] = buf_load8(rs, so, 0u);
+        b.z[h][q] = buf_load8(rz, so, 0u);
+      }
     }
     // One path for full and partial batches (a lane-dependent branch here would
     // move the row offset out of the SGPR and serialise the loads).
-    const uint32_t base = nv ? ((uint32_t)r0 * (uint32_t)N + (uint32_t)n) * 4u : kOobOffset;
 #pragma unroll
-    for (int u = 0; u < BR; ++u)
-      b.w[u] = buf_load16<kNonTemporal>(rw, r0 + u < le ? base : kOobOffset,
-                                        uniform((uint32_t)u * row_bytes));
+    for (int q = 0; q < QPL; ++q) {
+      const uint32_t base = n + HW * q < N
+                                ? ((uint32_t)r0 * (uint32_t)N + (uint32_t)(n + HW * q)) * 4u
+                                : kOobOffset;
+#pragma unroll
+      for (int u = 0; u < BR; ++u)
+        b.w[u][q] = buf_load16<kNonTemporal>(rw, r0 + u < le ? base : kOobOffset,
+                                             uniform((uint32_t)u * row_bytes));
+    }
   };
 
   auto process = [&](const Batch& b, int r0, int le, int c0) {
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      const ColQ2 p01 = make_colq2(b.s[h].x, b.z[h].x), p23 = make_colq2(b.s[h].y, b.z[h].y);
+      if constexpr (MF) {
+#pragma unroll
+        for (int q = 0; q < QPL; ++q) {
+          const ColQ2 p01 = make_colq2(b.s[h][q].x, b.z[h][q].x);
+          const ColQ2 p23 = make_colq2(b.s[h][q].y, b.z[h][q].y);
+          const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
+#pragma unroll
+          for (int uu = 0; uu < RH; ++uu) {
+            const int u = h * RH + uu;
+            const int r = r0 + u;
+            f16x2 d[4][4];
+            dq_word_fast(b.w[u][q].x, cq4[0], mg, d[0]);
+            dq_word_fast(b.w[u][q].y, cq4[1], mg, d[1]);
+            dq_word_fast(b.w[u][q].z, cq4[2], mg, d[2]);
+            dq_word_fast(b.w[u][q].w, cq4[3], mg, d[3]);
+            // both operands in pair order: (w0 w4 w1 w5 w2 w6 w3 w7) against
+            // the activations permuted the same way when they were staged
+            const uint4 xp = xs[xrow * XS + min(r - c0, CHUNK)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              macc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(f16x8, xp),
+                  f16x8{d[c][0].x, d[c][0].y, d[c][1].x, d[c][1].y, d[c][2].x, d[c][2].y,
+                        d[c][3].x, d[c][3].y},
+                  macc[q][c], 0, 0, 0);
+          }
+        }
+        continue;
+      }
+      const ColQ2 p01 = make_colq2(b.s[h][0].x, b.z[h][0].x);
+      const ColQ2 p23 = make_colq2(b.s[h][0].y, b.z[h][0].y);
       const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
 #pragma unroll
       for (int uu = 0; uu < RH; ++uu) {
@@ -302,23 +348,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         const int r = r0 + u;
         if (!kBranchFree && r >= le) break;
         f16x2 d[4][4];
-        dq_word_fast(b.w[u].x, cq4[0], mg, d[0]);
-        dq_word_fast(b.w[u].y, cq4[1], mg, d[1]);
-        dq_word_fast(b.w[u].z, cq4[2], mg, d[2]);
-        dq_word_fast(b.w[u].w, cq4[3], mg, d[3]);
-        if constexpr (MF) {
-          // both operands in pair order: (w0 w4 w1 w5 w2 w6 w3 w7) against the
-          // activations permuted the same way when they were staged
-          const uint4 xp = xs[xrow * XS + min(r - c0, CHUNK)];
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            macc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(f16x8, xp),
-                f16x8{d[c][0].x, d[c][0].y, d[c][1].x, d[c][1].y, d[c][2].x, d[c][2].y,
-                      d[c][3].x, d[c][3].y},
-                macc[c], 0, 0, 0);
-          continue;
-        }
+        dq_word_fast(b.w[u][0].x, cq4[0], mg, d[0]);
+        dq_word_fast(b.w[u][0].y, cq4[1], mg, d[1]);
+        dq_word_fast(b.w[u][0].z, cq4[2], mg, d[2]);
+        dq_word_fast(b.w[u][0].w, cq4[3], mg, d[3]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const uint4 xp = xs[m * XS + (kBranchFree ? min(r - c0, CHUNK) : r - c0)];
@@ -416,12 +449,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     // in component m): one partial set per wave into LDS, then the waves in order
     if (lane < 16) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
+      for (int q = 0; q < QPL; ++q)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = macc[c][m];
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) red[wave][m][HW * q + 4 * lane + c] = macc[q][c][m];
     }
     __syncthreads();
-    gemv_sum_waves_store<MT, CWL, WAVES>(red, tid, cb, sk, S, N, ldy, bias, Y, part);
+    gemv_sum_waves_store<MT, CWL * QPL, WAVES>(red, tid, cb, sk, S, N, ldy, bias, Y, part);
   } else {
     gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
   }
@@ -623,9 +658,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
   gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
 }
 
-template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false>
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false, int QPL = 1>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
-  constexpr int CW = 4 * CWL;
+  constexpr int CW = 4 * CWL * QPL;
   const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
   float* part = split > 1 ? static_cast<float*>(ws) : nullptr;
@@ -658,7 +693,7 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
     da.part = part;
     hipLaunchKernelGGL(kern, dim3(nblk * split), dim3(GemvShape<WAVES>::kThreads), 0, st, da);
   } else
-    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF>), dim3(nblk * split),
+    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF, QPL>), dim3(nblk * split),
                        dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
                        reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                        static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
@@ -683,8 +718,8 @@ hipError_t launch_w(const GemmArgs& a, int cols, int split, void* ws, hipStream_
 
 // cfg 1 / 2: 8 / 16 waves; cfg 4 / 5: the same with the activations staged in
 // LDS for M <= 2 (larger M always stages them); cfg 6 / 7: 16 / 8 waves,
-// staged, with the dot products on the matrix cores (M <= 2, 64-column blocks
-// only).  16 waves only for M <= 2 (the reduction buffer grows with waves x
+// staged, with the dot products on the matrix cores (M <= 2, 64- or 128-column
+// blocks only).  16 waves only for M <= 2 (the reduction buffer grows with waves x
 // M).  cfg 0 / 3 (4 waves) measured slower everywhere and were retired.
 template <int MT>
 hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, hipStream_t st) {
@@ -695,11 +730,13 @@ hipError_t launch_mt(const GemmArgs& a, int cols, int cfg, int split, void* ws, 
       case 4: return launch_w<MT, 8, true>(a, cols, split, ws, st);
       case 5: return launch_w<MT, 16, true>(a, cols, split, ws, st);
       case 6:
-        if (cols != 64) return hipErrorInvalidValue;
-        return launch_cwl<MT, 16, 16, true, true>(a, split, ws, st);
+        if (cols == 64) return launch_cwl<MT, 16, 16, true, true, 1>(a, split, ws, st);
+        if (cols == 128) return launch_cwl<MT, 16, 16, true, true, 2>(a, split, ws, st);
+        return hipErrorInvalidValue;
       case 7:
-        if (cols != 64) return hipErrorInvalidValue;
-        return launch_cwl<MT, 16, 8, true, true>(a, split, ws, st);
+        if (cols == 64) return launch_cwl<MT, 16, 8, true, true, 1>(a, split, ws, st);
+        if (cols == 128) return launch_cwl<MT, 16, 8, true, true, 2>(a, split, ws, st);
+        return hipErrorInvalidValue;
       default: return hipErrorInvalidValue;
     }
   } else {
@@ -715,7 +752,7 @@ bool gemv_cols_valid(int cols) {
 }
 bool gemv_cfg_valid(int cfg, int M, int cols) {
   return cfg == 1 || (M <= 2 && (cfg == 2 || cfg == 4 || cfg == 5)) ||
-         (M <= 2 && cols == 64 && (cfg == 6 || cfg == 7));
+         (M <= 2 && (cols == 64 || cols == 128) && (cfg == 6 || cfg == 7));
 }
 
 int gemv_rows_per_split(int K, int split) {

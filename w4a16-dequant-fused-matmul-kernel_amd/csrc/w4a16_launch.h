@@ -46,7 +46,7 @@ inline uint64_t x_extent_bytes(const GemmArgs& a) {
 // or 16 (cfg 2, M <= 2) waves per workgroup, cfg 4 / 5 the same with the
 // activations staged in LDS (M <= 2; larger M always stages them), cfg 6 / 7
 // 16 / 8 waves staged with the dot products on the matrix cores (M <= 2,
-// 64-column blocks); cfg 0 and 3 (4 waves) were retired.  With split > 1,
+// 64- or 128-column blocks); cfg 0 and 3 (4 waves) were retired.  With split > 1,
 // `ws` holds the fp32 partials of gemv_workspace_bytes().
 constexpr int kGemvMaxM = 8;
 // 8 waves per workgroup: two waves per SIMD overlap one wave's dequant with the

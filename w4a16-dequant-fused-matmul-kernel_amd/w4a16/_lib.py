@@ -24,7 +24,7 @@ KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
 MFMA_CONFIGS = (1, 2, 6, 7, 11, 12, 13)
 MFMA_SPLIT_CONFIGS = (7, 11, 12, 13)
 GEMV_CONFIGS = (1, 2, 4, 5)          # 8 / 16 waves, + LDS-staged activations (M <= 2)
-GEMV_MFMA_CONFIGS = (6, 7)           # 16 / 8 waves, staged, MFMA dot products (M <= 2, 64 columns)
+GEMV_MFMA_CONFIGS = (6, 7)           # 16 / 8 waves, staged, MFMA dot products (M <= 2, 64 / 128 columns)
 SKINNY_CONFIGS = (0, 2, 3)           # 16 / 32 / 64-column blocks
 # W4A16_NOALLOC_SCRATCH_BYTES: the static scratch of w4a16_gemm_f16_noalloc
 NOALLOC_SCRATCH_BYTES = 16 << 20
