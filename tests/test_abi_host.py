@@ -322,11 +322,22 @@ def test_planner_gemv_split_rule():
         assert p.tile_cfg in (1, 2, 4, 5, 7)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
     assert _lib.plan(1, 28672, 4096, 128).tile_n == 128
-    for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 2048, 28672)):
+    for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 1024, 28672)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
         assert p.workspace_bytes == 4 * M * N * 4
         assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
+    # long rows on 32 .. 223 64-column blocks: MFMA dot products, K split to
+    # reach 7/8 of the CUs (power of two, at most 8)
+    for M, N, K, split in ((1, 8192, 28672, 2), (1, 4096, 28672, 4), (1, 2048, 28672, 8),
+                           (2, 2048, 28672, 8), (2, 4096, 14336, 4), (2, 8192, 28672, 2)):
+        p = _lib.plan(M, N, K, 128)
+        assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, split), (M, N, K)
+        assert p.workspace_bytes == split * M * N * 4
+        assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
+    for M, N, K in ((1, 4096, 14336), (1, 8192, 8192), (1, 1024, 28672), (3, 8192, 28672)):
+        p = _lib.plan(M, N, K, 128)                  # shorter rows, too few blocks, M > 2
+        assert p.tile_cfg != 7 or p.split_k == 1, (M, N, K)
     assert _lib.plan(1, 28672, 14336, 128).split_k == 1   # enough column blocks
     assert _lib.plan(1, 4096, 14336, 128).split_k == 1    # one block per CU
     for split in (2, 3, 7, 600):
@@ -358,8 +369,10 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(1, 6144, 14336, 128)           # long K keeps 16-column blocks
     assert p.tile_n == 16
-    p = _lib.plan(2, 4096, 14336, 128)           # long rows at M = 2: 8 waves
+    p = _lib.plan(2, 4096, 10240, 128)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
+    p = _lib.plan(2, 4096, 14336, 128)           # ... longer: MFMA dots, split K
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 4)
     p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, direct
     assert p.tile_cfg == 2
     p = _lib.plan(1, 16384, 4096, 128)           # 64-column blocks: 8 waves, staged, MFMA dots
@@ -374,9 +387,11 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg) == (64, 1)
     p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 8192, 28672, 128)           # C5 down-proj: 16 waves, direct
+    p = _lib.plan(1, 8192, 28672, 128)           # C5 down-proj: MFMA dots, split 2
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
+    p = _lib.plan(1, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # unsplit: 16 waves, direct
     assert (p.tile_n, p.tile_cfg) == (32, 2)
-    p = _lib.plan(2, 8192, 28672, 128)           # ... 8 waves at M = 2
+    p = _lib.plan(2, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # ... 8 waves at M = 2
     assert (p.tile_n, p.tile_cfg) == (32, 1)
     p = _lib.plan(2, 1024, 8192, 128)            # split 4: 2048 rows per split
     assert p.split_k == 4 and p.tile_cfg == 2

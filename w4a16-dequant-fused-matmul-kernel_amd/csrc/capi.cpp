@@ -127,6 +127,26 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
   return (K / 8 >= 1024 && nblk < cus * 7 / 8) ? 4 : 1;
 }
 
+// Long rows at M <= 2 (K >= 16384 for M = 1, K >= 12288 for M = 2) on
+// 32 .. 7/8-of-the-CUs 64-column blocks: the dot products on the matrix cores
+// (cfg 7), K split into the fewest powers of two (at most 8) that give 7/8 of
+// the CUs a workgroup, one reduction pass.  Measured on MI355X against the
+// plans these shapes had (16/32-column dot2 blocks): M = 1, K = 28672,
+// N = 8192 27.4 -> 24.6 us (split 2); N = 4096 19.9 -> 16.4 (4); N = 2048 15.8
+// -> 12.2 (8); M = 2, K = 28672, N = 8192 39.3 -> 26.9; K = 14336, N = 4096
+// 16.0 -> 11.6.  Shorter rows lose the reduction pass's cost (M = 1, K = 8192,
+// N = 8192 10.6 -> 11.3 us; K = 14336, N = 8192 15.8 -> 16.3).  Returns the
+// split, or 0 where the rule does not apply.
+int gemv_mfma_split(int64_t M, int64_t N, int64_t K, int cus) {
+  if (M > 2 || K < (M == 2 ? 12288 : 16384)) return 0;
+  const int64_t nblk = (N + 63) / 64;
+  const int64_t want = (int64_t)cus * 7 / 8;
+  if (nblk < 32 || nblk >= want) return 0;
+  int s = 2;
+  while (nblk * s < want && s < 8) s *= 2;
+  return s;
+}
+
 // Prefill tile configuration by shape (measured on MI355X, C4/C5 shapes):
 //   * the 128 x 256 two-waves-per-SIMD 16x16x32 kernel with activations and
 //     weights streamed into LDS (cfg 11, K % 256 == 0) wherever the tiles fill
@@ -292,8 +312,9 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   switch (kernel) {
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
-      const int cols = gemv_cols_auto(M, N, K, cus);
-      int S = split > 0 ? split : gemv_split_auto(N, K, cols, cus);
+      const int mfma_split = split > 0 ? 0 : gemv_mfma_split(M, N, K, cus);
+      const int cols = mfma_split ? 64 : gemv_cols_auto(M, N, K, cus);
+      int S = split > 0 ? split : mfma_split ? mfma_split : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
       if (S > 1) {
@@ -302,7 +323,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
         S = (int)((KP + rows - 1) / rows);
       }
       p->split_k = S;
-      p->tile_cfg = gemv_waves_cfg(M, K, S, cols);
+      p->tile_cfg = mfma_split ? kGemvDefaultConfig + 6 : gemv_waves_cfg(M, K, S, cols);
       p->tile_m = 0;
       p->tile_n = cols;
       p->grid_x = ((N + cols - 1) / cols) * S;
