@@ -22,13 +22,14 @@ __all__ = ["W4A16Linear"]
 
 
 class W4A16Linear(nn.Module):
-    """4-bit weight / fp16 activation linear layer.
+    """Linear layer holding its weight as packed uint4 codes, computing in fp16.
 
-    Buffers:
-        qweight : int32 [K//8, N]
-        scales  : fp16  [K//G, N]
-        zeros   : fp16  [K//G, N]
-        bias    : fp16  [N] (optional)
+    K = ``in_features``, N = ``out_features``, G = ``group_size``.  The module
+    owns four buffers and no parameters (it is for inference): the packed codes
+    ``qweight`` (int32, K/8 rows of N words, eight 4-bit codes per word along
+    K), the per-group ``scales`` and ``zeros`` (fp16, K/G rows of N), and an
+    fp16 ``bias`` of N entries, or ``None`` when built with ``bias=False``.
+    Buffers start zeroed; ``from_linear`` or ``quantize_from_dense`` fills them.
     """
 
     def __init__(
