@@ -68,12 +68,16 @@ typedef struct w4a16_plan {
                               cores (M <= 2, 64- or 128-column blocks);
                               SKINNY:
                               0 / 2 / 3 = 16 / 32 /
-                              64-column blocks (32: M <= 32, N even; 64:
-                              M <= 16, N % 4 == 0), 4 to 16 waves by K.
+                              64-column blocks (32: N even; 64: N % 4 == 0),
+                              4 to 16 waves by K.
                               Other numbers name
                               retired forms and are refused
                               (W4A16_ERR_BAD_PLAN)                           */
-  int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup   */
+  int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup;
+                              SKINNY: rows of y per workgroup (M rounded up
+                              to 16, or 16: one 16-row group per workgroup,
+                              at most 32 on 32-column and 16 on 64-column
+                              blocks) x columns                              */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */
 } w4a16_plan;

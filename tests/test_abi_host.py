@@ -153,6 +153,25 @@ def test_retired_configurations_refused(lib):
         assert code == -5, cfg
 
 
+def test_skinny_row_groups_are_checked(lib):
+    """A skinny plan's tile_m is the rows of y per workgroup: all of them (M
+    rounded up to 16) or one 16-row group; 32-column blocks hold at most 32
+    rows, 64-column blocks 16.  Anything else is refused before a launch."""
+    from w4a16 import _lib
+
+    N, K, G = 1024, 4096, 128
+    a = ctypes.c_void_p(1 << 12)
+    # (the accepted forms -- e.g. M = 40 with 48 or 16 rows on 16-column
+    # blocks, 16 rows on 32- or 64-column blocks -- run in the GPU tests)
+    for M, cfg, rows in ((40, 0, 32), (40, 2, 48), (24, 3, 32), (8, 0, 0), (8, 0, 8),
+                         (64, 3, 64), (64, 2, 64), (17, 0, 17), (16, 0, 48)):
+        p = _lib.plan(M, N, K, G, _lib.KERNEL_SKINNY, 0)
+        p.tile_cfg, p.tile_m = cfg, rows
+        code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, M, N, K, G,
+                                          NULL, 0, NULL)
+        assert code == -5, (M, cfg, rows, code)
+
+
 def test_skinny_plans_check_their_load_alignment(lib):
     """32- and 64-column skinny blocks load 2 / 4 adjacent columns per lane in
     one load: 8 / 16-byte weights and 4 / 8-byte scales and zeros.  Pointers
@@ -280,7 +299,8 @@ def test_quant_entry_points_reject_bad_args(lib):
     (16, 4096, 4096, 32, "skinny"),
     (32, 6144, 4096, 128, "skinny"),  # 32-column blocks beat the streamed tiles to N = 8192
     (16, 14336, 4096, 128, "skinny"),  # ... and to N = 16384 for M <= 16
-    (32, 14336, 4096, 128, "mfma"),
+    (32, 14336, 4096, 128, "skinny"),  # 16-row groups on 64-column blocks, two rounds
+    (48, 14336, 4096, 128, "mfma"),    # ... not three
     (16, 28672, 4096, 128, "skinny"),
     (24, 28672, 4096, 128, "mfma"),
     (4, 8192, 28672, 128, "skinny"),   # long K: whole K per workgroup
@@ -297,13 +317,22 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     assert _lib.KERNEL_NAMES[p.kernel] == kernel
     assert p.grid_x >= 1 and p.grid_y >= 1
     if kernel == "skinny":
-        # 32-column blocks (cfg 2) where 16-column ones outnumber the CUs (256
-        # on MI355X, also the library's value without a device), M <= 32 and N
-        # even; else 16-column blocks with 4 waves
+        # M > 16 with 128-groups and few enough blocks: one 16-row group per
+        # workgroup (test_planner_skinny_row_groups); else 32-column blocks
+        # (cfg 2) where 16-column ones outnumber the CUs (256 on MI355X, also
+        # the library's value without a device), M <= 32 and N even; else
+        # 16-column blocks with 4 waves
+        g = (M + 15) // 16
+        rg = (M > 16 and G % 128 == 0 and K <= 4096 and
+              (N % 2 == 0 and (N + 31) // 32 * g <= 256 or N % 4 == 0 and (N + 63) // 64 * g <= 512))
         quad = M <= 16 and N % 4 == 0 and G % 128 == 0 and (N + 63) // 64 > 128
         wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
-        want = (3, 64) if quad else (2, 32) if wide else (0, 16)
+        if rg:
+            want = (2, 32) if (N + 31) // 32 * g <= 256 else (3, 64)
+        else:
+            want = (3, 64) if quad else (2, 32) if wide else (0, 16)
         assert (p.tile_cfg, p.tile_n) == want, (M, N)
+        assert p.tile_m == (16 if rg else g * 16), (M, N)
 
 
 def test_planner_gemv_split_rule():
@@ -406,8 +435,8 @@ def test_planner_small_batch_wide_weights_stream():
     from w4a16 import _lib
 
     for M, N, K, cfg, s in ((32, 28672, 4096, 12, 4), (24, 28672, 8192, 12, 4),
-                            (32, 4096, 14336, 12, 28), (64, 28672, 8192, 13, 4),
-                            (48, 14336, 4096, 13, 8), (64, 4096, 4096, 13, 8)):
+                            (17, 28672, 8192, 12, 4), (64, 28672, 8192, 13, 4),
+                            (48, 14336, 4096, 13, 8), (64, 4096, 8192, 13, 16)):
         p = _lib.plan(M, N, K, 128)
         rows = 32 if cfg == 12 else 64
         assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == cfg, (M, N, K)
@@ -419,7 +448,7 @@ def test_planner_small_batch_wide_weights_stream():
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
     # up to N = 8192 (N = 16384 for M <= 16) the skinny kernel's 32-column
     # blocks beat the streamed tiles, long K included
-    for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (32, 6144, 4096), (24, 8192, 8192)):
+    for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (17, 8192, 8192), (20, 8192, 6144)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (2, 32), (M, N, K)
         assert p.grid_x == N // 32
@@ -431,6 +460,35 @@ def test_planner_small_batch_wide_weights_stream():
     for G in (32, 64):
         p = _lib.plan(16, 8192, 28672, G)
         assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 12, G
+
+
+def test_planner_skinny_row_groups():
+    """17 <= M <= 64, G % 128 == 0: skinny blocks with one 16-row group per
+    workgroup (tile_m 16, ceil(M / 16) workgroups per column block) where the
+    workgroups stay near the CU count: 32-column blocks while they fit one
+    round, else 64-column blocks up to two rounds for K <= 4096; with longer K
+    only two row groups on one round (64 columns from M = 24)."""
+    from w4a16 import _lib
+
+    for M, N, K, cfg in ((32, 4096, 4096, 2), (17, 4096, 4096, 2), (24, 6144, 4096, 3),
+                         (40, 4096, 4096, 3), (64, 4096, 4096, 3), (64, 8192, 4096, 3),
+                         (32, 14336, 4096, 3), (32, 4096, 14336, 2), (17, 4096, 14336, 2),
+                         (24, 8192, 8192, 3), (32, 8192, 28672, 3)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K)
+        cols = 64 if cfg == 3 else 32
+        assert (p.tile_cfg, p.tile_m, p.tile_n) == (cfg, 16, cols), (M, N, K)
+        assert p.grid_x == (N + cols - 1) // cols * ((M + 15) // 16) and p.split_k == 1
+    # not: wide N, three or more row groups with K > 4096, M = 17 on 64-column
+    # blocks with K > 4096, groups below 128, M <= 16
+    for M, N, K, G in ((32, 28672, 4096, 128), (48, 14336, 4096, 128), (48, 8192, 8192, 128),
+                       (64, 4096, 14336, 128), (17, 8192, 8192, 128), (32, 4096, 4096, 64),
+                       (16, 4096, 4096, 128)):
+        p = _lib.plan(M, N, K, G)
+        assert not (_lib.KERNEL_NAMES[p.kernel] == "skinny" and p.tile_m == 16 and M > 16), (M, N, K, G)
+    # a forced skinny plan takes the same row groups
+    p = _lib.plan(32, 4096, 4096, 128, _lib.KERNEL_SKINNY, 0)
+    assert (p.tile_cfg, p.tile_m) == (2, 16)
 
 
 def test_planner_prefill_split_k():

@@ -210,23 +210,27 @@ def test_mfma_split_k(M, K, N, G):
 ])
 def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
-    with 16-column blocks, (M <= 32, N even) 32-column blocks with two columns
-    per lane and (M <= 16, N % 4 == 0) 64-column blocks with four."""
+    with 16-column blocks, (N even) 32-column blocks with two columns per lane
+    and (N % 4 == 0) 64-column blocks with four; each with all rows in one
+    workgroup (32- / 64-column blocks: M <= 32 / 16) and with one 16-row group
+    per workgroup (the last one ragged)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    cfgs = (0,) + ((2,) if M <= 32 and N % 2 == 0 else ()) + (
-        (3,) if M <= 16 and N % 4 == 0 else ())
-    for cfg in cfgs:
-        log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg}")
-        p = plan_for(M, N, K, G, "skinny")
-        p.tile_cfg = cfg
-        out = w4a16_matmul_planned(X, qw, s, z, G, p)
-        assert_gemm_close(out, ref, f"skinny cfg={cfg}")
-        outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
-        assert torch.equal(outb, out + b)
+    whole = (M + 15) // 16 * 16
+    for rows in sorted({whole, 16}):
+        cfgs = (0,) + ((2,) if rows <= 32 and N % 2 == 0 else ()) + (
+            (3,) if rows <= 16 and N % 4 == 0 else ())
+        for cfg in cfgs:
+            log(f"skinny M={M} K={K} N={N} G={G} cfg={cfg} rows={rows}")
+            p = plan_for(M, N, K, G, "skinny")
+            p.tile_cfg, p.tile_m = cfg, rows
+            out = w4a16_matmul_planned(X, qw, s, z, G, p)
+            assert_gemm_close(out, ref, f"skinny cfg={cfg} rows={rows}")
+            outb = w4a16_matmul_planned(X, qw, s, z, G, p, bias=b)
+            assert torch.equal(outb, out + b)
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 64, 130, 32), (17, 96, 7, 32), (4, 24, 12, 12), (2, 8, 5, 4)])

@@ -237,6 +237,40 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
   return M <= 16 && N % 4 == 0 && G % 128 == 0 && (N + 63) / 64 > cus / 2;
 }
 
+// Skinny blocks with one 16-row group per workgroup (plan tile_m = 16) for
+// 17 <= M <= 64: each workgroup streams 16 rows of X instead of all M, which
+// is what bounds the kernel from M = 24 (X's bytes per CU, not the weights'),
+// and no cross-workgroup reduction is needed.  The block width keeps the
+// workgroups near the CU count: 32 columns while 2 x N / 32 groups fit the
+// CUs, else 64 columns up to two rounds (K <= 4096, one batch per wave); with
+// longer K (the 4-wave loop) only two row groups on one round, 64-column
+// blocks from M = 24 (a 17th row alone costs a second weight pass there).
+// Returns the skinny cfg (2 or 3), or -1.  Measured on MI355X against the
+// automatic plan before it (µs, G = 128): K = 4096, N = 4096, M = 24 / 32 /
+// 48 / 64: 9.60 / 10.91 / 16.17 / 16.57 -> 8.14 / 8.12 / 9.28 / 8.56; N = 6144
+// M = 32 / 48: 11.88 / 19.00 -> 9.80 / 15.96; N = 8192 M = 64: 21.16 ->
+// 15.84; N = 14336 M = 32: 19.19 -> 17.72; K = 14336, N = 4096, M = 17 / 32:
+// 22.10 / 23.49 -> 20.72 / 20.94; K = 28672, N = 8192, M = 32: 63.86 ->
+// 52.40.  Slower (kept on the streamed tiles): N = 28672 at every M (M = 32:
+// 26.4 vs 34.2), three or four row groups with K > 4096 (M = 48, K = 8192,
+// N = 8192: 25.6 vs 29.4), M = 17 on 64-column blocks with K > 4096.  Smaller
+// groups than 128 add scale / zero loads to every k-step and were not measured.
+int skinny_row_groups_cfg(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  if (M <= 16 || M > kSkinnyMaxM || G % 128 != 0) return -1;
+  const int64_t g = (M + 15) / 16;
+  const int64_t wg2 = (N + 31) / 32 * g, wg3 = (N + 63) / 64 * g;
+  const bool c2 = N % 2 == 0, c3 = N % 4 == 0;
+  if (K <= 4096) {
+    if (c2 && wg2 <= cus) return 2;
+    if (c3 && wg3 <= 2 * cus) return 3;
+    return -1;
+  }
+  if (g != 2) return -1;
+  if (c2 && wg2 <= cus) return 2;
+  if (c3 && M >= 24 && wg3 <= cus) return 3;
+  return -1;
+}
+
 // k-splits for the streamed kernel on few tiles: about 448 workgroups (two
 // per CU at most), at least 8 k-steps per split.
 int stream_split_for(int64_t tiles, int64_t K) {
@@ -293,6 +327,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
+    else if (skinny_applicable(M, G) && skinny_row_groups_cfg(M, N, K, G, cus) >= 0)
+      kernel = W4A16_KERNEL_SKINNY;
     else if (small_m_takes_stream(M, N, K, G))
       kernel = skinny_applicable(M, G) && (skinny_quad(M, N, G, cus) ||
                                            skinny_wide_beats_stream(M, N, G, cus))
@@ -351,11 +387,15 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       p->workspace_bytes = (int64_t)mfma_workspace_bytes(M, N, K, c.split);
       return W4A16_OK;
     }
-    case W4A16_KERNEL_SKINNY:
+    case W4A16_KERNEL_SKINNY: {
       if (!skinny_applicable(M, G)) return W4A16_ERR_BAD_PLAN;
-      p->tile_m = (int32_t)((M + 15) / 16 * 16);
-      p->tile_n = skinny_quad(M, N, G, cus) ? 64 : skinny_wide(M, N, cus) ? 32 : 16;
-      p->grid_x = (N + p->tile_n - 1) / p->tile_n;
+      const int rg = skinny_row_groups_cfg(M, N, K, G, cus);
+      p->tile_m = rg >= 0 ? 16 : (int32_t)((M + 15) / 16 * 16);
+      p->tile_n = rg >= 0               ? (rg == 3 ? 64 : 32)
+                  : skinny_quad(M, N, G, cus) ? 64
+                  : skinny_wide(M, N, cus)    ? 32
+                                              : 16;
+      p->grid_x = (N + p->tile_n - 1) / p->tile_n * ((M + 15) / 16 * 16 / p->tile_m);
       p->grid_y = 1;
       // 64- or 32-column blocks where they apply (cfg 3 / 2), else 16-column
       // blocks (cfg 0); the kernel's wave count follows K.  (An 8-wave form
@@ -366,6 +406,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       // 11.5 vs 12.1 -- and was retired.)
       p->tile_cfg = p->tile_n == 64 ? 3 : p->tile_n == 32 ? 2 : 0;
       return W4A16_OK;
+    }
     case W4A16_KERNEL_SIMT:
       p->tile_m = 4;
       p->tile_n = 64;
@@ -447,8 +488,8 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
     }
     case W4A16_KERNEL_SKINNY: {
       const int c = p->tile_cfg;
-      if (!skinny_applicable(M, G) || !fits(M, N, K, G) || !(c == 0 || c == 2 || c == 3) ||
-          (c == 2 && (M > 32 || N % 2 != 0)) || (c == 3 && (M > 16 || N % 4 != 0)))
+      if (!skinny_applicable(M, G) || !fits(M, N, K, G) ||
+          !skinny_plan_valid(c, (int)M, (int)N, p->tile_m))
         return W4A16_ERR_BAD_PLAN;
       // each lane loads 1, 2 or 4 adjacent columns' words, scales and zeros
       // in one load: 4 / 8 / 16-byte weights, 2 / 4 / 8-byte scales and zeros
@@ -456,7 +497,7 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
       if (!aligned(x, 16) || !aligned(qw, 4 * cols) || !aligned(sc, 2 * cols) ||
           !aligned(zr, 2 * cols))
         return W4A16_ERR_BAD_PLAN;
-      return to_status(launch_skinny(a, c, s));
+      return to_status(launch_skinny(a, c, p->tile_m, s));
     }
     case W4A16_KERNEL_SIMT:
       return to_status(launch_simt(a, s));

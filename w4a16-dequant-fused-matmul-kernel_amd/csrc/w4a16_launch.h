@@ -105,15 +105,19 @@ hipError_t launch_occ2_gemm(const GemmArgs& a, int split, float* part, hipStream
 bool operands_fit(int M, int N, int K, int G);
 
 // Skinny-M GEMM on MFMA (v_mfma_f32_16x16x32_f16), 1 <= M <= kSkinnyMaxM,
-// one workgroup per column block over the whole of K (4 waves, 8 or 16 when
-// that gives each wave one 256-k batch: K <= 2048 / 4096).  cfg 0: 16-column blocks (one
-// column per lane, 4-byte weight loads, 2-byte scale / zero loads); cfg 2:
-// 32-column blocks (M <= 32, N even: two columns per lane, 8-byte weight
-// loads, 4-byte scale / zero loads); cfg 3: 64-column blocks (M <= 16,
-// N % 4 == 0: four columns per lane, 16-byte weight loads, 8-byte scale /
-// zero loads).  cfg 1 (8 waves in the loop) was retired.
+// one workgroup per column block and row group over the whole of K (4 waves,
+// 8 or 16 when that gives each wave one 256-k batch: K <= 2048 / 4096).
+// cfg 0: 16-column blocks (one column per lane, 4-byte weight loads, 2-byte
+// scale / zero loads); cfg 2: 32-column blocks (N even: two columns per lane,
+// 8-byte weight loads, 4-byte scale / zero loads); cfg 3: 64-column blocks
+// (N % 4 == 0: four columns per lane, 16-byte weight loads, 8-byte scale /
+// zero loads).  `rows` = rows of y per workgroup: M rounded up to 16 (one
+// row group) or 16 (M / 16 row groups); at most 32 on 32-column blocks and 16
+// on 64-column blocks (skinny_plan_valid).  cfg 1 (8 waves in the loop) was
+// retired.
 constexpr int kSkinnyMaxM = 64;
-hipError_t launch_skinny(const GemmArgs& a, int cfg, hipStream_t st);
+bool skinny_plan_valid(int cfg, int M, int N, int rows);
+hipError_t launch_skinny(const GemmArgs& a, int cfg, int rows, hipStream_t st);
 
 // Sequential-k SIMT kernel: any N, any G dividing K, no alignment needs.
 hipError_t launch_simt(const GemmArgs& a, hipStream_t st);
