@@ -75,9 +75,9 @@ typedef struct w4a16_plan {
                               (W4A16_ERR_BAD_PLAN)                           */
   int32_t tile_m, tile_n;  /* workgroup tile; GEMV: 0 x columns per workgroup;
                               SKINNY: rows of y per workgroup (M rounded up
-                              to 16, or 16: one 16-row group per workgroup,
-                              at most 32 on 32-column and 16 on 64-column
-                              blocks) x columns                              */
+                              to 16, or 16 / 8: one 16- / 8-row group per
+                              workgroup, at most 32 on 32-column and 16 on
+                              64-column blocks) x columns                    */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */
 } w4a16_plan;

@@ -155,16 +155,16 @@ def test_retired_configurations_refused(lib):
 
 def test_skinny_row_groups_are_checked(lib):
     """A skinny plan's tile_m is the rows of y per workgroup: all of them (M
-    rounded up to 16) or one 16-row group; 32-column blocks hold at most 32
-    rows, 64-column blocks 16.  Anything else is refused before a launch."""
+    rounded up to 16) or one 16- or 8-row group; 32-column blocks hold at most
+    32 rows, 64-column blocks 16.  Anything else is refused before a launch."""
     from w4a16 import _lib
 
     N, K, G = 1024, 4096, 128
     a = ctypes.c_void_p(1 << 12)
     # (the accepted forms -- e.g. M = 40 with 48 or 16 rows on 16-column
     # blocks, 16 rows on 32- or 64-column blocks -- run in the GPU tests)
-    for M, cfg, rows in ((40, 0, 32), (40, 2, 48), (24, 3, 32), (8, 0, 0), (8, 0, 8),
-                         (64, 3, 64), (64, 2, 64), (17, 0, 17), (16, 0, 48)):
+    for M, cfg, rows in ((40, 0, 32), (40, 2, 48), (24, 3, 32), (8, 0, 0), (8, 0, 4),
+                         (64, 3, 64), (64, 2, 64), (17, 0, 17), (16, 0, 48), (40, 0, 24)):
         p = _lib.plan(M, N, K, G, _lib.KERNEL_SKINNY, 0)
         p.tile_cfg, p.tile_m = cfg, rows
         code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, M, N, K, G,
@@ -325,14 +325,15 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
         g = (M + 15) // 16
         rg = (M > 16 and G % 128 == 0 and K <= 4096 and
               (N % 2 == 0 and (N + 31) // 32 * g <= 256 or N % 4 == 0 and (N + 63) // 64 * g <= 512))
+        rg8 = 13 <= M <= 16 and G % 128 == 0 and N % 2 == 0 and (N + 31) // 32 * 2 <= 256
         quad = M <= 16 and N % 4 == 0 and G % 128 == 0 and (N + 63) // 64 > 128
         wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
-        if rg:
-            want = (2, 32) if (N + 31) // 32 * g <= 256 else (3, 64)
+        if rg or rg8:
+            want = (2, 32) if (N + 31) // 32 * g <= 256 or rg8 else (3, 64)
         else:
             want = (3, 64) if quad else (2, 32) if wide else (0, 16)
         assert (p.tile_cfg, p.tile_n) == want, (M, N)
-        assert p.tile_m == (16 if rg else g * 16), (M, N)
+        assert p.tile_m == (16 if rg else 8 if rg8 else g * 16), (M, N)
 
 
 def test_planner_gemv_split_rule():
@@ -479,13 +480,18 @@ def test_planner_skinny_row_groups():
         cols = 64 if cfg == 3 else 32
         assert (p.tile_cfg, p.tile_m, p.tile_n) == (cfg, 16, cols), (M, N, K)
         assert p.grid_x == (N + cols - 1) // cols * ((M + 15) // 16) and p.split_k == 1
+    # 13 <= M <= 16: two 8-row groups on 32-column blocks that fit the CUs
+    for M, N, K in ((16, 4096, 4096), (13, 4096, 14336)):
+        p = _lib.plan(M, N, K, 128)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K)
+        assert (p.tile_cfg, p.tile_m, p.tile_n, p.grid_x) == (2, 8, 32, N // 32 * 2), (M, N, K)
     # not: wide N, three or more row groups with K > 4096, M = 17 on 64-column
-    # blocks with K > 4096, groups below 128, M <= 16
+    # blocks with K > 4096, groups below 128, M <= 12, M <= 16 on more blocks
     for M, N, K, G in ((32, 28672, 4096, 128), (48, 14336, 4096, 128), (48, 8192, 8192, 128),
                        (64, 4096, 14336, 128), (17, 8192, 8192, 128), (32, 4096, 4096, 64),
-                       (16, 4096, 4096, 128)):
+                       (12, 4096, 4096, 128), (16, 6144, 4096, 128), (16, 4096, 4096, 64)):
         p = _lib.plan(M, N, K, G)
-        assert not (_lib.KERNEL_NAMES[p.kernel] == "skinny" and p.tile_m == 16 and M > 16), (M, N, K, G)
+        assert not (_lib.KERNEL_NAMES[p.kernel] == "skinny" and p.tile_m < (M + 15) // 16 * 16), (M, N, K, G)
     # a forced skinny plan takes the same row groups
     p = _lib.plan(32, 4096, 4096, 128, _lib.KERNEL_SKINNY, 0)
     assert (p.tile_cfg, p.tile_m) == (2, 16)

@@ -212,15 +212,15 @@ def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,
     with 16-column blocks, (N even) 32-column blocks with two columns per lane
     and (N % 4 == 0) 64-column blocks with four; each with all rows in one
-    workgroup (32- / 64-column blocks: M <= 32 / 16) and with one 16-row group
-    per workgroup (the last one ragged)."""
+    workgroup (32- / 64-column blocks: M <= 32 / 16) and with one 16- or 8-row
+    group per workgroup (the last one ragged)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=M * 7 + N)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
     whole = (M + 15) // 16 * 16
-    for rows in sorted({whole, 16}):
+    for rows in sorted({whole, 16, 8}):
         cfgs = (0,) + ((2,) if rows <= 32 and N % 2 == 0 else ()) + (
             (3,) if rows <= 16 and N % 4 == 0 else ())
         for cfg in cfgs:

@@ -239,13 +239,14 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
 
 // Skinny blocks with one 16-row group per workgroup (plan tile_m = 16) for
 // 17 <= M <= 64: each workgroup streams 16 rows of X instead of all M, which
-// is what bounds the kernel from M = 24 (X's bytes per CU, not the weights'),
+// is what bounds the kernel from M = 16 (X's bytes per CU, not the weights'),
 // and no cross-workgroup reduction is needed.  The block width keeps the
 // workgroups near the CU count: 32 columns while 2 x N / 32 groups fit the
 // CUs, else 64 columns up to two rounds (K <= 4096, one batch per wave); with
 // longer K (the 4-wave loop) only two row groups on one round, 64-column
 // blocks from M = 24 (a 17th row alone costs a second weight pass there).
-// Returns the skinny cfg (2 or 3), or -1.  Measured on MI355X against the
+// Returns the skinny cfg (2 or 3) and rows per workgroup, or cfg -1 for the
+// whole-rows plans.  Measured on MI355X against the
 // automatic plan before it (µs, G = 128): K = 4096, N = 4096, M = 24 / 32 /
 // 48 / 64: 9.60 / 10.91 / 16.17 / 16.57 -> 8.14 / 8.12 / 9.28 / 8.56; N = 6144
 // M = 32 / 48: 11.88 / 19.00 -> 9.80 / 15.96; N = 8192 M = 64: 21.16 ->
@@ -255,20 +256,27 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
 // 26.4 vs 34.2), three or four row groups with K > 4096 (M = 48, K = 8192,
 // N = 8192: 25.6 vs 29.4), M = 17 on 64-column blocks with K > 4096.  Smaller
 // groups than 128 add scale / zero loads to every k-step and were not measured.
-int skinny_row_groups_cfg(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  if (M <= 16 || M > kSkinnyMaxM || G % 128 != 0) return -1;
+// 13 <= M <= 16: two 8-row groups on 32-column blocks where those fit the CUs
+// (N = 4096: K = 4096 7.61 -> 7.00 us, K = 14336 19.47 -> 18.13; M <= 12, or
+// more blocks, or 64-column blocks: slower).
+struct SkinnyRows {
+  int cfg, rows;   // cfg -1: all rows in one workgroup
+};
+SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  if (M <= 12 || M > kSkinnyMaxM || G % 128 != 0) return {-1, 0};
+  const bool c2 = N % 2 == 0, c3 = N % 4 == 0;
+  if (M <= 16) return c2 && (N + 31) / 32 * 2 <= cus ? SkinnyRows{2, 8} : SkinnyRows{-1, 0};
   const int64_t g = (M + 15) / 16;
   const int64_t wg2 = (N + 31) / 32 * g, wg3 = (N + 63) / 64 * g;
-  const bool c2 = N % 2 == 0, c3 = N % 4 == 0;
   if (K <= 4096) {
-    if (c2 && wg2 <= cus) return 2;
-    if (c3 && wg3 <= 2 * cus) return 3;
-    return -1;
+    if (c2 && wg2 <= cus) return {2, 16};
+    if (c3 && wg3 <= 2 * cus) return {3, 16};
+    return {-1, 0};
   }
-  if (g != 2) return -1;
-  if (c2 && wg2 <= cus) return 2;
-  if (c3 && M >= 24 && wg3 <= cus) return 3;
-  return -1;
+  if (g != 2) return {-1, 0};
+  if (c2 && wg2 <= cus) return {2, 16};
+  if (c3 && M >= 24 && wg3 <= cus) return {3, 16};
+  return {-1, 0};
 }
 
 // k-splits for the streamed kernel on few tiles: about 448 workgroups (two
@@ -327,7 +335,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
-    else if (skinny_applicable(M, G) && skinny_row_groups_cfg(M, N, K, G, cus) >= 0)
+    else if (skinny_applicable(M, G) && skinny_row_groups(M, N, K, G, cus).cfg >= 0)
       kernel = W4A16_KERNEL_SKINNY;
     else if (small_m_takes_stream(M, N, K, G))
       kernel = skinny_applicable(M, G) && (skinny_quad(M, N, G, cus) ||
@@ -389,13 +397,13 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     }
     case W4A16_KERNEL_SKINNY: {
       if (!skinny_applicable(M, G)) return W4A16_ERR_BAD_PLAN;
-      const int rg = skinny_row_groups_cfg(M, N, K, G, cus);
-      p->tile_m = rg >= 0 ? 16 : (int32_t)((M + 15) / 16 * 16);
-      p->tile_n = rg >= 0               ? (rg == 3 ? 64 : 32)
+      const SkinnyRows rg = skinny_row_groups(M, N, K, G, cus);
+      p->tile_m = rg.cfg >= 0 ? rg.rows : (int32_t)((M + 15) / 16 * 16);
+      p->tile_n = rg.cfg >= 0           ? (rg.cfg == 3 ? 64 : 32)
                   : skinny_quad(M, N, G, cus) ? 64
                   : skinny_wide(M, N, cus)    ? 32
                                               : 16;
-      p->grid_x = (N + p->tile_n - 1) / p->tile_n * ((M + 15) / 16 * 16 / p->tile_m);
+      p->grid_x = (N + p->tile_n - 1) / p->tile_n * ((M + p->tile_m - 1) / p->tile_m);
       p->grid_y = 1;
       // 64- or 32-column blocks where they apply (cfg 3 / 2), else 16-column
       // blocks (cfg 0); the kernel's wave count follows K.  (An 8-wave form

@@ -61,7 +61,7 @@ template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
-    int N, int K, int G, int mgs, int ldx, int ldy) {
+    int N, int K, int G, int mgs, int rpg, int ldx, int ldy) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four columns per lane");
   constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][NT][64];
@@ -69,10 +69,12 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const int nb = (int)gridDim.x;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
-  // mgs > 1: the workgroup owns rows [row0, row0 + 16 MT) of its column
-  // block; the mgs row groups of a block are consecutive workgroups (one XCD)
+  // The workgroup owns rows [row0, row0 + rpg) of its column block: all of
+  // them (mgs = 1, rpg = 16 MT) or one of mgs row groups of 16 or 8 rows
+  // (MT = 1; tile rows past rpg load and store nothing), the groups of a
+  // block on consecutive workgroups (one XCD, sharing its weights in L2).
   const int cb = mgs == 1 ? lin : lin / mgs;
-  const int row0 = (lin - cb * mgs) * (16 * MT);
+  const int row0 = (lin - cb * mgs) * rpg;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -106,7 +108,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int row = row0 + mt * 16 + c;
-    x_off[mt] = row < M ? ((uint32_t)row * (uint32_t)ldx + (uint32_t)q * 8u) * 2u : kOobOffset;
+    x_off[mt] = row < M && mt * 16 + c < rpg
+                    ? ((uint32_t)row * (uint32_t)ldx + (uint32_t)q * 8u) * 2u
+                    : kOobOffset;
   }
 
   struct Batch {
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = row0 + mt * 16 + 4 * q + r;
-          if (row < M) {
+          if (row < M && mt * 16 + 4 * q + r < rpg) {
             f16 y = f32_to_f16(v[r]);
             if (bias) y = y + bv;
             Y[(size_t)row * ldy + col + t] = y;
@@ -286,7 +290,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 // 7.85 us -> 5.74 / 6.29 / 7.49; M = 16, N = 28672 (64 columns): 22.6 ->
 // 21.1; M = 8, K = 2048, N = 4096: 4.99 -> 4.55 with 8 waves.
 template <int MT, int GSTEP, int NT>
-hipError_t launch_nt(const GemmArgs& a, int mgs, hipStream_t st) {
+hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
+  const int mgs = (a.M + rpg - 1) / rpg;
   const int nblk = (a.N + 16 * NT - 1) / (16 * NT);
   const int ks = a.K >> 5;
   // 16 waves hold 128 registers each: 64 rows with a scale / zero load per
@@ -301,31 +306,31 @@ hipError_t launch_nt(const GemmArgs& a, int mgs, hipStream_t st) {
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                     a.G, mgs, a.ldx, a.ldy);
+                     a.G, mgs, rpg, a.ldx, a.ldy);
   return hipGetLastError();
 }
 
 template <int MT, int GSTEP>
-hipError_t launch_g(const GemmArgs& a, int cfg, int mgs, hipStream_t st) {
+hipError_t launch_g(const GemmArgs& a, int cfg, int rpg, hipStream_t st) {
   if constexpr (MT <= 2) {
-    if (cfg == 2) return launch_nt<MT, GSTEP, 2>(a, mgs, st);   // 32-column blocks
+    if (cfg == 2) return launch_nt<MT, GSTEP, 2>(a, rpg, st);   // 32-column blocks
   }
   if constexpr (MT == 1) {
-    if (cfg == 3) return launch_nt<MT, GSTEP, 4>(a, mgs, st);   // 64-column blocks
+    if (cfg == 3) return launch_nt<MT, GSTEP, 4>(a, rpg, st);   // 64-column blocks
   }
-  return launch_nt<MT, GSTEP, 1>(a, mgs, st);                    // 16-column blocks
+  return launch_nt<MT, GSTEP, 1>(a, rpg, st);                    // 16-column blocks
 }
 
 template <int MT>
-hipError_t launch_mt(const GemmArgs& a, int cfg, int mgs, hipStream_t st) {
+hipError_t launch_mt(const GemmArgs& a, int cfg, int rpg, hipStream_t st) {
   // batch slots per group when group boundaries land on fixed slots of an
   // aligned 8-step (256-k) batch: G / 32 a power of two
   const int gs = a.G / 32;
-  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, cfg, mgs, st);
+  if (gs >= 8 && (gs & (gs - 1)) == 0) return launch_g<MT, 8>(a, cfg, rpg, st);
   switch (gs) {
-    case 4: return launch_g<MT, 4>(a, cfg, mgs, st);
-    case 2: return launch_g<MT, 2>(a, cfg, mgs, st);
-    default: return launch_g<MT, 1>(a, cfg, mgs, st);
+    case 4: return launch_g<MT, 4>(a, cfg, rpg, st);
+    case 2: return launch_g<MT, 2>(a, cfg, rpg, st);
+    default: return launch_g<MT, 1>(a, cfg, rpg, st);
   }
 }
 
@@ -334,16 +339,17 @@ hipError_t launch_mt(const GemmArgs& a, int cfg, int mgs, hipStream_t st) {
 // cfg 0: 16-column blocks; 2: 32-column blocks (N even); 3: 64-column blocks
 // (N % 4 == 0); the wave count follows K (launch_nt).  `rows`: rows of y per
 // workgroup, all of them (M rounded up to 16) or 16, one row group per
-// workgroup and M / 16 workgroups per column block: each workgroup then
-// streams 16 rows of X instead of all M (X's bytes per CU, not the weights',
-// bound the kernel from M = 24 at K = N = 4096) and the weights are read once
+// workgroup and M / 16 workgroups per column block, or 8 (half a tile, the
+// other half's lanes load and store nothing): each workgroup then streams
+// 16 (8) rows of X instead of all M (X's bytes per CU, not the weights',
+// bound the kernel from M = 16 at K = N = 4096) and the weights are read once
 // per row group, from L2 after the first.  32-column blocks hold at most two
 // row tiles per workgroup, 64-column blocks one.  cfg 1 (8 waves in the
 // two-batch loop on 16-column blocks) measured slower on every shape and was
 // retired.
 bool skinny_plan_valid(int cfg, int M, int N, int rows) {
   const int whole = (M + 15) / 16 * 16;
-  if (M < 1 || M > kSkinnyMaxM || !(rows == whole || rows == 16)) return false;
+  if (M < 1 || M > kSkinnyMaxM || !(rows == whole || rows == 16 || rows == 8)) return false;
   if (cfg == 0) return true;
   if (cfg == 2) return rows <= 32 && N % 2 == 0;
   if (cfg == 3) return rows <= 16 && N % 4 == 0;
@@ -352,11 +358,12 @@ bool skinny_plan_valid(int cfg, int M, int N, int rows) {
 
 hipError_t launch_skinny(const GemmArgs& a, int cfg, int rows, hipStream_t st) {
   if (!skinny_plan_valid(cfg, a.M, a.N, rows)) return hipErrorInvalidValue;
-  if (rows == 16) return launch_mt<1>(a, cfg, (a.M + 15) / 16, st);
-  switch (rows / 16) {
-    case 2: return launch_mt<2>(a, cfg, 1, st);
-    case 3: return launch_mt<3>(a, cfg, 1, st);
-    case 4: return launch_mt<4>(a, cfg, 1, st);
+  switch (rows) {
+    case 8:
+    case 16: return launch_mt<1>(a, cfg, rows, st);
+    case 32: return launch_mt<2>(a, cfg, rows, st);
+    case 48: return launch_mt<3>(a, cfg, rows, st);
+    case 64: return launch_mt<4>(a, cfg, rows, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -112,9 +112,9 @@ bool operands_fit(int M, int N, int K, int G);
 // 8-byte weight loads, 4-byte scale / zero loads); cfg 3: 64-column blocks
 // (N % 4 == 0: four columns per lane, 16-byte weight loads, 8-byte scale /
 // zero loads).  `rows` = rows of y per workgroup: M rounded up to 16 (one
-// row group) or 16 (M / 16 row groups); at most 32 on 32-column blocks and 16
-// on 64-column blocks (skinny_plan_valid).  cfg 1 (8 waves in the loop) was
-// retired.
+// row group), 16 or 8 (M / 16 or M / 8 row groups); at most 32 on 32-column
+// blocks and 16 on 64-column blocks (skinny_plan_valid).  cfg 1 (8 waves in
+// the loop) was retired.
 constexpr int kSkinnyMaxM = 64;
 bool skinny_plan_valid(int cfg, int M, int N, int rows);
 hipError_t launch_skinny(const GemmArgs& a, int cfg, int rows, hipStream_t st);
