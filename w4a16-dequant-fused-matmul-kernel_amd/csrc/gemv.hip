@@ -517,6 +517,14 @@ template <int MT, int CWL, int WAVES, bool ONE_BATCH>
 __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArgs args) {
   static_assert(MT <= 2, "direct activations are for M <= 2");
   constexpr int BR = GemvShape<WAVES>::kBatch;
+  // 32-column and wider blocks: the CWL / 4 lane quads of a packed row each
+  // load their row's activation octet once, one dword per lane, and rebuild
+  // it with four quad-permute moves, instead of every lane loading all 16
+  // bytes (12 fewer bytes through the load-return path per lane and slot, 4
+  // more VALU).  Measured on MI355X, M = 1: K = 4096, N = 6144 6.80 -> 6.40
+  // us; N = 8192 6.85 -> 6.56; K = 14336, N = 4096 11.74 -> 11.49.  On
+  // 16-column blocks (C2) it measured slower (4.74 -> 4.79).
+  constexpr bool kXShare = CWL >= 8;
   constexpr int RW = 64 / CWL;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
   constexpr int CW = 4 * CWL;              // columns per workgroup
@@ -573,7 +581,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
 
   struct Batch {
     uint2 s[BR], z[BR];
-    uint4 x[MT * BR];
+    uint4 x[MT * BR];     // kXShare: the lane's dword in .x
     uint4 w[BR];
   };
   // Slots b * BR .. b * BR + BR - 1: offsets first, then the loads in the
@@ -586,7 +594,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
       const bool v = nv && r < re;
       wo[i] = v ? w_voff : kOobOffset;
       so[i] = v ? ((uint32_t)group_of(r * 8) * (uint32_t)N + (uint32_t)n) * 2u : kOobOffset;
-      xo[i] = v ? (uint32_t)r * 16u : kOobOffset;
+      // a shared octet is loaded whatever the lane's columns: its quad needs it
+      xo[i] = kXShare ? (r < re ? (uint32_t)r * 16u + 4u * (uint32_t)(lane & 3) : kOobOffset)
+                      : (v ? (uint32_t)r * 16u : kOobOffset);
     }
 #pragma unroll
     for (int i = 0; i < BR; ++i) {
@@ -596,7 +606,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
       bt.z[i] = buf_load8(rz, so[i], 0u);
 #pragma unroll
       for (int m = 0; m < MT; ++m)
-        bt.x[m * BR + i] = buf_load16(rx, xo[i], uniform((uint32_t)m * (uint32_t)ldx * 2u));
+        if constexpr (kXShare)
+          bt.x[m * BR + i].x = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+              rx, (int)xo[i], (int)uniform((uint32_t)m * (uint32_t)ldx * 2u), 0);
+        else
+          bt.x[m * BR + i] = buf_load16(rx, xo[i], uniform((uint32_t)m * (uint32_t)ldx * 2u));
       __builtin_amdgcn_sched_barrier(0);   // keep the slots in order
     }
   };
@@ -623,7 +637,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
       dq_word_fast(bt.w[i].w, cq4[3], mg, d[3]);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const uint4 xp = perm_pairs(bt.x[m * BR + i]);
+        uint4 xo4 = bt.x[m * BR + i];
+        if constexpr (kXShare) {
+          // quad_perm [k, k, k, k]: every lane of the quad takes lane k's dword
+          const int xd = (int)xo4.x;
+          xo4 = make_uint4((uint32_t)__builtin_amdgcn_update_dpp(0, xd, 0x00, 0xF, 0xF, false),
+                           (uint32_t)__builtin_amdgcn_update_dpp(0, xd, 0x55, 0xF, 0xF, false),
+                           (uint32_t)__builtin_amdgcn_update_dpp(0, xd, 0xAA, 0xF, 0xF, false),
+                           (uint32_t)__builtin_amdgcn_update_dpp(0, xd, 0xFF, 0xF, 0xF, false));
+        }
+        const uint4 xp = perm_pairs(xo4);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           float a = acc[m][c];
