@@ -466,6 +466,7 @@ TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 # --traffic-probe's workloads, in order: (key, config, M, K, N, calls, cold)
 PROBE = [("C2", "C2", 1, 4096, 4096, 8, True),
          ("C3_M8_K4096_N4096", "C3", 8, 4096, 4096, 4, True),
+         ("C3_M32_K4096_N4096", "C3", 32, 4096, 4096, 4, True),
          ("C3_M16_K4096_N28672", "C3", 16, 4096, 28672, 4, True),
          ("C3_M32_K4096_N28672", "C3", 32, 4096, 28672, 4, True),
          ("C4_M4096", "C4", 4096, 4096, 14336, 3, False)]
