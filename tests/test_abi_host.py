@@ -500,15 +500,32 @@ def test_planner_skinny_row_groups():
 def test_planner_prefill_split_k():
     from w4a16 import _lib
 
-    # C5 down-projection at M = 256: 64 tiles of 128 x 256 -> 7 splits (~448
-    # workgroups); the up-projection's 224 tiles -> 2
+    # 128 x 256 tiles that fit one per CU (256 without a device): two k-slices
+    # per workgroup (cfg 14), split for about one workgroup per CU.  C5
+    # down-projection at M = 256: 64 tiles -> 4 splits; the up-projection's 224
+    # tiles -> none; M = 128 (112 tiles) -> 2
     p = _lib.plan(256, 8192, 28672, 128)
-    assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 11
-    assert p.split_k == 7 and p.grid_x == 448
-    assert _lib.plan(256, 28672, 8192, 128).split_k == 2
-    assert _lib.plan(128, 28672, 8192, 128).split_k == 4
-    assert _lib.plan(2048, 14336, 4096, 128).split_k == 1    # 896 tiles
+    assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 14
+    assert p.split_k == 4 and p.grid_x == 256
     assert p.workspace_bytes >= p.split_k * 256 * 8192 * 4
+    q = _lib.plan(256, 28672, 8192, 128)
+    assert (q.tile_cfg, q.split_k, q.workspace_bytes) == (14, 1, 0)
+    assert (_lib.plan(128, 28672, 8192, 128).tile_cfg, _lib.plan(128, 28672, 8192, 128).split_k) == (14, 2)
+    assert _lib.plan(512, 14336, 4096, 128).tile_cfg == 14      # C4 M = 512: 224 tiles
+    # ... at least 4 k-steps per slice: K = 4096 caps the splits at 8
+    assert _lib.plan(128, 4096, 4096, 128).split_k == 8
+    # G = 32 (a scale / zero load per half-step): cfg 11 split for ~448 workgroups
+    p = _lib.plan(256, 8192, 28672, 32)
+    assert p.tile_cfg == 11 and p.split_k == 7 and p.grid_x == 448
+    # a forced split that two k-slices (8-step units) cannot honour: cfg 11
+    p = _lib.plan(256, 1028, 2048, 64, _lib.KERNEL_MFMA, 3)
+    assert (p.tile_cfg, p.split_k) == (11, 3)
+    p = _lib.plan(256, 1028, 2048, 64, _lib.KERNEL_MFMA, 2)
+    assert (p.tile_cfg, p.split_k) == (14, 2)
+    # more tiles than CUs: cfg 11
+    p = _lib.plan(1024, 14336, 4096, 128)
+    assert (p.tile_cfg, p.split_k) == (11, 1)
+    assert _lib.plan(2048, 14336, 4096, 128).split_k == 1    # 896 tiles
     # large M: no split, no workspace
     p = _lib.plan(4096, 14336, 4096, 128)
     assert p.split_k == 1 and p.workspace_bytes == 0 and p.tile_cfg == 11

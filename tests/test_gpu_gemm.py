@@ -153,7 +153,8 @@ def test_mfma_tile_configs(M, K, N, G):
     two waves per SIMD with 16x16x32 MFMAs, where K % 64 == 0; config 6, two
     waves per SIMD with 32x32x16 MFMAs, where K % 128 == 0; configs 11, 12
     and 13, activations and weights streamed into LDS with 128-, 32- and
-    64-row tiles, where K % 256 == 0)."""
+    64-row tiles, and 14, the 128-row tile with two k-slices of four waves
+    per workgroup, where K % 256 == 0)."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
     from w4a16 import _lib
 
@@ -185,7 +186,7 @@ def test_mfma_split_k(M, K, N, G):
     X, qw, s, z = _build_case(M, K, N, G, seed=M + N + K)
     ref = _ref(X, qw, s, z, G)
     b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
-    for cfg in (7, 11, 12, 13) if K % 256 == 0 else (7,):
+    for cfg in (7, 11, 12, 13, 14) if K % 256 == 0 else (7,):
         for split in (2, 3, 5, K // 64):
             p = plan_for(M, N, K, G, "mfma", split)
             p.tile_cfg = cfg
@@ -365,7 +366,7 @@ def test_gemv_auto_split_long_k(M, K, N, G):
 
 
 def test_streamed_prefill_far_apart_scales_zeros():
-    """The streamed prefill kernels (cfg 11 / 12 / 13) read scales and zeros
+    """The streamed prefill kernels (cfg 11 / 12 / 13 / 14) read scales and zeros
     through one buffer resource based at the lower of the two; placed more
     than 2 GiB apart they take the register kernel of 128 x 256 tiles (cfg 7)
     instead, with the plan's k-split and workspace (its own split count never
@@ -385,7 +386,7 @@ def test_streamed_prefill_far_apart_scales_zeros():
     dist = abs(z_far.data_ptr() - s_far.data_ptr())
     log(f"scales/zeros {dist / 2**30:.2f} GiB apart")
     assert dist >= (1 << 31)
-    for cfg, split in ((11, 1), (11, 3), (12, 2), (13, 4), (12, 8)):
+    for cfg, split in ((11, 1), (11, 3), (12, 2), (13, 4), (12, 8), (14, 1), (14, 2)):
         p = plan_for(M, N, K, G, "mfma", split)
         p.tile_cfg = cfg
         assert p.split_k == split

@@ -108,7 +108,7 @@ def test_mfma_strided_every_config(M, K, N, G):
         log(f"mfma strided M={M} K={K} N={N} cfg={cfg}")
         _check_same(X, qw, s, z, G, p, padx=40, pady=4, bias=b if cfg % 3 == 0 else None,
                     what=f"mfma cfg={cfg}")
-    for cfg in (7, 11, 12, 13):
+    for cfg in (7, 11, 12, 13, 14):
         p = plan_for(M, N, K, G, "mfma", 3)
         p.tile_cfg = cfg
         assert p.split_k > 1

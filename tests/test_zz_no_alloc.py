@@ -144,13 +144,13 @@ def test_noalloc_explicit_plans_and_bias():
 
 @pytest.mark.gpu
 def test_noalloc_large_layer_fits_scratch():
-    """A prefill layer whose automatic plan's partials (2 x 256 x 28672 fp32 =
-    56 MiB) exceed the scratch runs with fewer k-splits instead; equal to the
+    """A prefill layer whose automatic plan's partials (4 x 256 x 8192 fp32 =
+    32 MiB) exceed the scratch runs with fewer k-splits instead; equal to the
     workspace entry point with that plan."""
     from w4a16 import _lib as L
     from w4a16.hip_kernel import plan_for
 
-    M, K, N, G = 256, 8192, 28672, 128
+    M, K, N, G = 256, 28672, 8192, 128
     assert plan_for(M, N, K, G).workspace_bytes > L.NOALLOC_SCRATCH_BYTES
     X, qw, s, z = _case(M, K, N, G, seed=4)
     p = _check(X, qw, s, z, G, "large layer", sampled=True)

@@ -298,6 +298,24 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
   const bool c7 = mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G);
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
+  // 128 x 256 tiles that fit one per CU: cfg 14 (the cfg 11 kernel with two
+  // k-slices per workgroup, one workgroup per CU), split along K for about a
+  // workgroup per CU with at least 4 steps per slice, instead of cfg 11 split
+  // for two per CU (whose fp32 partials and reduction cost more).  G % 64 == 0:
+  // with a scale / zero load per half-step the kernel spills and loses.
+  // Measured on MI355X against the plans before it (µs): C4 M = 512 81.2 ->
+  // 67.5; M = 384, K = 4096, N = 14336 67.0 -> 60.0; C5 M = 256, K = 8192,
+  // N = 28672 137.5 -> 126.3 (G = 64: 135.0 -> 127.6); C5 M = 256, K = 28672,
+  // N = 8192 132.3 -> 128.8 (4 splits); M = 128, K = 4096, N = 14336 34.9 ->
+  // 32.0 (4 splits); M = 512, K = N = 4096 38.8 -> 36.0; M = 256, K = 14336,
+  // N = 4096 48.5 -> 46.2 (8 splits); ties at M = 128 / 256, K = N = 4096.
+  // More tiles than CUs (M = 1024, N = 14336: 131.0 vs 119.4) keep cfg 11.
+  if (c11 && G % 64 == 0 && t6 <= cus) {
+    int64_t s = cus / t6;
+    if (s > K / 512) s = K / 512;
+    if (s < 1) s = 1;
+    return {14, s > 1 ? stream_splits((int)K, (int)s, 2) : 1};
+  }
   if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
   // cfg 11 on fewer than ~448 tiles: split K for about two workgroups per CU
   // (measured on MI355X: M = 128, K = 8192, N = 28672: 77.7 us at 4 splits vs
@@ -381,7 +399,13 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       if (split > 0) {   // a forced split runs on the streamed kernel (cfg 7 where K % 256 != 0)
         const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
         c.cfg = split > 1 ? (c.cfg >= 11 ? c.cfg : (c11 ? 11 : 7)) : c.cfg;
-        c.split = split > 1 ? (c11 ? stream_splits((int)K, split) : occ2_splits((int)K, split)) : 1;
+        // two k-slices split K in 8-step units: where that makes fewer splits
+        // than asked for, the one-slice kernel's 4-step units honour the request
+        if (split > 1 && c.cfg == 14 && stream_splits((int)K, split, 2) < stream_splits((int)K, split, 1))
+          c.cfg = 11;
+        c.split = split > 1 ? (c11 ? stream_splits((int)K, split, c.cfg == 14 ? 2 : 1)
+                                   : occ2_splits((int)K, split))
+                            : 1;
         if (c.split > 1 && !mfma_cfg_applicable(c.cfg, (int)M, (int)N, (int)K, (int)G))
           return W4A16_ERR_BAD_PLAN;
       }

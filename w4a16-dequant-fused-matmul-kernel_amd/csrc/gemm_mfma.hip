@@ -530,6 +530,7 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
 //         ahead (gemm_stream.hip)
 // cfg 12:  32 x 256, the cfg 11 kernel with 2 m-tiles per wave (small M)
 // cfg 13:  64 x 256, the cfg 11 kernel with 4 m-tiles per wave
+// cfg 14: 128 x 256, the cfg 11 kernel with 8 waves in two k-slices
 // Numbers 0, 3, 4, 5, 8, 9 and 10 belonged to tilings that measured slower
 // on every shape and were retired; a plan naming them is refused.
 MfmaTile mfma_tile(int cfg) {
@@ -541,6 +542,7 @@ MfmaTile mfma_tile(int cfg) {
     case 11: return {128, 256};
     case 12: return {32, 256};
     case 13: return {64, 256};
+    case 14: return {128, 256};
     default: return {0, 0};
   }
 }
@@ -555,7 +557,8 @@ bool mfma_cfg_applicable(int cfg, int M, int N, int K, int G) {
     case 7: return occ2_gemm_applicable(M, N, K, G);
     case 11:
     case 12:
-    case 13: return stream_gemm_applicable(M, N, K, G);
+    case 13:
+    case 14: return stream_gemm_applicable(M, N, K, G);
     default: return false;
   }
 }
@@ -580,6 +583,7 @@ hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipSt
     case 11: return launch_stream_gemm(a, 128, split, part, st);
     case 12: return launch_stream_gemm(a, 32, split, part, st);
     case 13: return launch_stream_gemm(a, 64, split, part, st);
+    case 14: return launch_stream_gemm(a, 128, split, part, st, 2);
     default: return hipErrorInvalidValue;
   }
 }

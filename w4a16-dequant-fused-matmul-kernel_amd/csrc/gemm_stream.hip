@@ -104,8 +104,18 @@ __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t 
 
 // kSZ1: G % 64 == 0, so both half-steps of a step lie in one group and one
 // scale / zero load per step serves both (else one per half-step).
-template <int kMT, bool kSZ1>
-__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// kKS: k-slices per workgroup.  1: four waves, two workgroups per CU.  2 (plan
+// cfg 14, 128-row tiles): eight waves in two slices of four, each slice the
+// four-wave kernel over half the workgroup's k-steps with its own activation
+// buffers and weight stages (144 KiB of LDS, one workgroup per CU, still two
+// waves per SIMD); at the end slice 1 hands its accumulators to slice 0
+// through LDS.  For shapes with fewer tiles than two per CU this takes the
+// place of split-K across workgroups, whose fp32 partials and reduction
+// kernel it avoids.  Both slices run the same number of steps (a slice's
+// steps past its range load zeros and add exactly 0), so every wave reaches
+// every barrier.
+template <int kMT, bool kSZ1, int kKS = 1>
+__global__ __launch_bounds__(kNT * kKS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
                    uint32_t sz_bytes, const f16* __restrict__ bias, f16* __restrict__ Y,
@@ -113,24 +123,28 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                    int ldy, uint32_t gmagic, int gshift) {
   static_assert(kStages == 4, "stage arrays below are written out for four stages");
   static_assert(kMT == 2 || kMT == 4 || kMT == 8, "8-row activation loads per wave");
+  static_assert(kKS == 1 || (kKS == 2 && kMT == 8), "two k-slices: 128-row tiles");
+  constexpr int kW = kWaves * kKS;       // waves per workgroup
   constexpr int kBM = 16 * kMT;          // rows per workgroup tile
   constexpr int kRPW = kBM / kWaves;     // activation rows each wave streams
   constexpr int kAL = kRPW / 8;          // its 8-row loads per step
   // dequant VALU per MFMA in the interleave: ~64 per half-step over its MFMAs
   constexpr int kVPM = 64 / (kMT * kNTiles);
-  // activation buffers: [row][8 octet slots], slot = octet ^ ((row / 2) % 8)
-  __shared__ uint4 As0[kBM * 8], As1[kBM * 8];
+  // activation buffers: [slice][row][8 octet slots], slot = octet ^ ((row / 2) % 8)
+  __shared__ uint4 As0[kKS * kBM * 8], As1[kKS * kBM * 8];
   // weight stages, one array each (the compiler tracks at most 8 LDS-direct
   // targets for its waits; 2 + 4 arrays stay within that):
   //   [wave][half][lane] 16-byte word quads, then
   //   [wave][half][column quad] (scales 0-1, scales 2-3, zeros 0-1, zeros 2-3)
-  constexpr int kStageQ = kWaves * 128;                 // word-quad part (uint4)
-  constexpr int kStage = kStageQ + kWaves * 2 * 16;     // + scale / zero part (uint4)
+  constexpr int kStageQ = kW * 128;                     // word-quad part (uint4)
+  constexpr int kStage = kStageQ + kW * 2 * 16;         // + scale / zero part (uint4)
   __shared__ uint4 St0[kStage], St1[kStage], St2[kStage], St3[kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // 0 .. kW - 1
+  const int wv = wave % kWaves;                // position along N
+  const int slice = wave / kWaves;             // k-slice (kKS == 2)
   const int l16 = lane & 15;    // column quad (B) / row (A) within a tile
   const int oct = lane >> 4;    // k-octet within a 32-k half-step
 
@@ -153,12 +167,16 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   const int rem = T - group * kGroupM * ntn;
   const int m0 = (first_m + rem % gsz) * kBM;
   const int n0 = (rem / gsz) * kBN;
-  const int wcol = n0 + wave * (16 * kNTiles);   // first column of this wave
+  const int wcol = n0 + wv * (16 * kNTiles);     // first column of this wave
   const int ncol = wcol + 4 * l16;               // this lane's 4 columns
   const bool nv = ncol < N;
   const int KP = K >> 3;
-  const int KS0 = sp * KTS;
-  const int KT = min(K / kBK, KS0 + KTS);
+  // this slice's k-steps [KS0, KT) of the workgroup's [sp KTS, sp KTS + KTS);
+  // with two slices KTS is a whole number of 8-step blocks and each slice
+  // runs KTS / 2 steps (steps at or past KT load zeros)
+  const int KSL = KTS / kKS;
+  const int KS0 = sp * KTS + slice * KSL;
+  const int KT = min(K / kBK, KS0 + KSL);
   const int NG = K / G;
 
   uint32_t magic_mix;
@@ -179,10 +197,11 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
       ((uint32_t)(lane >> 3) * (uint32_t)ldx + (uint32_t)((lane & 7) ^ (lane >> 4)) * 8u) * 2u;
   const uint32_t a_voff1 =
       ((uint32_t)(lane >> 3) * (uint32_t)ldx + (uint32_t)((lane & 7) ^ (lane >> 4) ^ 4) * 8u) * 2u;
-  const uint32_t a_row0 = (uint32_t)(m0 + kRPW * wave) * (uint32_t)ldx * 2u;
-  // A fragment of m-tile i, half-step h: row 16i + l16, octet oct + 4h
-  const int a_frag0 = l16 * 8 + ((oct) ^ ((l16 >> 1) & 7));
-  const int a_frag1 = l16 * 8 + ((oct + 4) ^ ((l16 >> 1) & 7));
+  const uint32_t a_row0 = (uint32_t)(m0 + kRPW * wv) * (uint32_t)ldx * 2u;
+  // A fragment of m-tile i, half-step h: row 16i + l16, octet oct + 4h (in
+  // this slice's buffer)
+  const int a_frag0 = slice * kBM * 8 + l16 * 8 + ((oct) ^ ((l16 >> 1) & 7));
+  const int a_frag1 = slice * kBM * 8 + l16 * 8 + ((oct + 4) ^ ((l16 >> 1) & 7));
   // weight word quad of this lane: packed row 4h + oct of a step, columns ncol..+3
   const uint32_t b_off = nv ? ((uint32_t)oct * (uint32_t)N + (uint32_t)ncol) * 4u : kOobOffset;
   // scale / zero load of this lane: column quad lane / 4, part lane % 4 =
@@ -208,12 +227,12 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   // Past this workgroup's k-range (kt >= KT) the loads below take an offset no
   // buffer range holds and write zeros that are never read.
   auto stream_a = [&](auto bc, int kt) {
-    uint4* a = as(bc) + kRPW * wave * 8;
+    uint4* a = as(bc) + slice * kBM * 8 + kRPW * wv * 8;
     const uint32_t kb = (uint32_t)kt * (uint32_t)(kBK * 2);
 #pragma unroll
     for (int j = 0; j < kAL; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (lds_void*)(a + 64 * j), 16, ((kRPW / 8 * wave + j) & 1) ? a_voff1 : a_voff0,
+          rx, (lds_void*)(a + 64 * j), 16, ((kRPW / 8 * wv + j) & 1) ? a_voff1 : a_voff0,
           uniform((kt < KT ? a_row0 + (uint32_t)(8 * j) * (uint32_t)ldx * 2u + kb : kOobOffset)), 0,
           0);
   };
@@ -359,11 +378,46 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
     read_in(std::integral_constant<int, 0>{}, 1, in1);
     dequant(in0, bf);
   }
-  for (int kb = KS0; kb < KT; kb += kStages) {
+  // one trip count for the whole workgroup with two slices (each slice's
+  // KSL steps from KS0), the slice's own range with one
+  const int kend = kKS == 1 ? KT : KS0 + KSL;
+  for (int kb = KS0; kb < kend; kb += kStages) {
     step(std::integral_constant<int, 0>{}, kb);
     step(std::integral_constant<int, 1>{}, kb + 1);
     step(std::integral_constant<int, 2>{}, kb + 2);
     step(std::integral_constant<int, 3>{}, kb + 3);
+  }
+
+  if constexpr (kKS == 2) {
+    // Slice 1's accumulators to slice 0 through the activation buffers, half
+    // the m-tiles per round (16 KiB per wave: [register][lane], no bank
+    // conflicts).  The last steps' LDS-direct loads (zeros past the range)
+    // are drained first so that none lands on the handed-over values; every
+    // wave passes every barrier.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    tile_barrier();
+    uint4* xb = (wv < 2 ? As0 : As1) + (wv & 1) * (kMT / 2 * kNTiles * 64);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (slice == 1) {
+#pragma unroll
+        for (int i = 0; i < kMT / 2; ++i)
+#pragma unroll
+          for (int c = 0; c < kNTiles; ++c)
+            xb[(i * kNTiles + c) * 64 + lane] =
+                __builtin_bit_cast(uint4, acc[r * (kMT / 2) + i][c]);
+      }
+      tile_barrier();
+      if (slice == 0) {
+#pragma unroll
+        for (int i = 0; i < kMT / 2; ++i)
+#pragma unroll
+          for (int c = 0; c < kNTiles; ++c)
+            acc[r * (kMT / 2) + i][c] += __builtin_bit_cast(f32x4, xb[(i * kNTiles + c) * 64 + lane]);
+      }
+      if (r == 0) tile_barrier();   // round 1 overwrites what round 0 handed over
+    }
+    if (slice == 1) return;
   }
 
   const int rbase = m0 + 4 * oct;
@@ -416,21 +470,24 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   }
 }
 
-// k-steps per split: whole 4-step blocks
-int split_steps(int K, int split) {
+// k-steps per split: whole 4-step blocks per k-slice
+int split_steps(int K, int split, int slices) {
   const int KT = K / kBK;
-  return ((KT + split - 1) / split + kStages - 1) / kStages * kStages;
+  const int unit = kStages * slices;
+  return ((KT + split - 1) / split + unit - 1) / unit * unit;
 }
 
-template <int kMT, bool kSZ1>
+template <int kMT, bool kSZ1, int kKS>
 hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t st) {
   constexpr int kBM = 16 * kMT;
   const int tiles = ((a.N + kBN - 1) / kBN) * ((a.M + kBM - 1) / kBM);
   const int KT = a.K / kBK;
   // never more splits than occ2_splits() gives for the same request, so
   // occ2_workspace_bytes() covers the partials
-  const int kts = split_steps(a.K, split);
+  const int kts = split_steps(a.K, split, kKS);
   const int nsplit = split > 1 ? (KT + kts - 1) / kts : 1;   // every split non-empty
+  // unsplit with two slices: whole 8-step blocks (steps past KT load zeros)
+  const int kts1 = (KT + kStages * kKS - 1) / (kStages * kKS) * (kStages * kKS);
   // scales and zeros through one buffer resource based at the lower address
   const char* sc = static_cast<const char*>(a.sc);
   const char* zr = static_cast<const char*>(a.zr);
@@ -438,28 +495,28 @@ hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t 
   const uint32_t sz_bytes = (uint32_t)((sc < zr ? zr : sc) - base) +
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
   const GroupDiv gd = group_div(a.G);
-  hipLaunchKernelGGL((stream_kernel<kMT, kSZ1>), dim3(tiles * nsplit), dim3(kNT), 0, st,
+  hipLaunchKernelGGL((stream_kernel<kMT, kSZ1, kKS>), dim3(tiles * nsplit), dim3(kNT * kKS), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
-                     nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : KT, a.ldx,
+                     nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : kts1, a.ldx,
                      a.ldy, gd.magic, gd.shift);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
 }
 
-template <int kMT>
+template <int kMT, int kKS = 1>
 hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
-  return a.G % (2 * 32) == 0 ? launch_kernel<kMT, true>(a, split, part, st)
-                             : launch_kernel<kMT, false>(a, split, part, st);
+  return a.G % (2 * 32) == 0 ? launch_kernel<kMT, true, kKS>(a, split, part, st)
+                             : launch_kernel<kMT, false, kKS>(a, split, part, st);
 }
 
 }  // namespace
 
-int stream_splits(int K, int split) {
+int stream_splits(int K, int split, int slices) {
   if (split <= 1 || K / kBK <= 1) return 1;
-  const int kts = split_steps(K, split);
+  const int kts = split_steps(K, split, slices);
   return (K / kBK + kts - 1) / kts;
 }
 
@@ -467,19 +524,20 @@ bool stream_gemm_applicable(int M, int N, int K, int G) {
   return occ2_gemm_applicable(M, N, K, G) && K % (kBK * kStages) == 0;
 }
 
-// rows x 256 tiles, rows = 128, 64 or 32.  Same applicability and split rule
-// as the two-waves-per-SIMD register kernel, plus K % 256 == 0.  Scales and
-// zeros further than 2 GiB apart (one buffer resource cannot span them) take
-// that register kernel (128 x 256 tiles, same results up to fp32 summation
-// order inside an MFMA).
+// rows x 256 tiles, rows = 128, 64 or 32; two k-slices per workgroup only
+// with 128 rows.  Same applicability and split rule as the two-waves-per-SIMD
+// register kernel, plus K % 256 == 0.  Scales and zeros further than 2 GiB
+// apart (one buffer resource cannot span them) take that register kernel
+// (128 x 256 tiles, same results up to fp32 summation order inside an MFMA).
 hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* part,
-                              hipStream_t st) {
+                              hipStream_t st, int slices) {
   if (!stream_gemm_applicable(a.M, a.N, a.K, a.G)) return hipErrorInvalidValue;
   if (occ2_splits(a.K, split) > 1 && !part) return hipErrorInvalidValue;
   const uintptr_t sc = reinterpret_cast<uintptr_t>(a.sc), zr = reinterpret_cast<uintptr_t>(a.zr);
   const uint64_t dist = sc < zr ? zr - sc : sc - zr;
   const uint64_t bytes = (uint64_t)(a.K / a.G) * (uint64_t)a.N * 2u;
   if (dist + bytes >= (1ull << 31)) return launch_occ2_gemm(a, split, part, st);
+  if (slices == 2) return rows == 128 ? launch_wg<8, 2>(a, split, part, st) : hipErrorInvalidValue;
   switch (rows) {
     case 128: return launch_wg<8>(a, split, part, st);
     case 64: return launch_wg<4>(a, split, part, st);

@@ -63,12 +63,13 @@ hipError_t launch_gemv(const GemmArgs& a, int cols, int cfg, int split, void* ws
 // Prefill GEMM on MFMA.  `cfg` picks the tiling (mfma_tile): 1, 2 (one wave
 // per SIMD, 32x32x16), 6 (two waves per SIMD, 32x32x16), 7 (two waves per
 // SIMD, 16x16x32, gemm_occ2.hip), 11 / 12 / 13 (128- / 32- / 64-row tiles with
-// activations and packed weights streamed into LDS, gemm_stream.hip).  Other
+// activations and packed weights streamed into LDS, gemm_stream.hip), 14 (the
+// 128-row streamed tile with two k-slices of four waves per workgroup).  Other
 // numbers are refused (retired tilings).
 struct MfmaTile {
   int bm, bn;
 };
-constexpr int kMfmaConfigs = 14;
+constexpr int kMfmaConfigs = 15;
 MfmaTile mfma_tile(int cfg);
 bool mfma_fits(int M, int N, int K, int G);
 // Whether tile configuration `cfg` exists and can run this shape (some need
@@ -94,11 +95,12 @@ size_t occ2_workspace_bytes(int M, int N, int K, int split);
 // (cfg 12 / 13): needs K % 256 == 0.
 bool stream_gemm_applicable(int M, int N, int K, int G);
 // Splits the streamed kernel makes of a split request (whole 4-step blocks per
-// split; never more than occ2_splits() for the same request).
-int stream_splits(int K, int split);
-// rows = 128, 64 or 32 (tile rows of cfg 11, 13, 12).
+// split and k-slice; never more than occ2_splits() for the same request).
+int stream_splits(int K, int split, int slices = 1);
+// rows = 128, 64 or 32 (tile rows of cfg 11 / 14, 13, 12); slices = 2: two
+// k-slices of four waves per workgroup (cfg 14, 128 rows).
 hipError_t launch_stream_gemm(const GemmArgs& a, int rows, int split, float* part,
-                              hipStream_t st);
+                              hipStream_t st, int slices = 1);
 hipError_t launch_occ2_gemm(const GemmArgs& a, int split, float* part, hipStream_t st);
 
 // Buffer-addressed kernels need every operand below 2 GiB.

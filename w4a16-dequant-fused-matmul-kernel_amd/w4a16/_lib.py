@@ -21,8 +21,8 @@ KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT, KERNEL_SKINNY = 0, 1, 2, 3, 
 KERNEL_NAMES = {KERNEL_GEMV: "gemv", KERNEL_MFMA: "mfma", KERNEL_SIMT: "simt",
                 KERNEL_SKINNY: "skinny"}
 # plan tile_cfg numbers each family has (others are refused: retired tilings)
-MFMA_CONFIGS = (1, 2, 6, 7, 11, 12, 13)
-MFMA_SPLIT_CONFIGS = (7, 11, 12, 13)
+MFMA_CONFIGS = (1, 2, 6, 7, 11, 12, 13, 14)
+MFMA_SPLIT_CONFIGS = (7, 11, 12, 13, 14)
 GEMV_CONFIGS = (1, 2, 4, 5)          # 8 / 16 waves, + LDS-staged activations (M <= 2)
 GEMV_MFMA_CONFIGS = (6, 7)           # 16 / 8 waves, staged, MFMA dot products (M <= 2, 64 / 128 columns)
 SKINNY_CONFIGS = (0, 2, 3)           # 16 / 32 / 64-column blocks
