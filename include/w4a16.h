@@ -58,9 +58,11 @@ enum w4a16_kernel {
 /* The launch a GEMM call will make.  Filled by w4a16_gemm_plan(). */
 typedef struct w4a16_plan {
   int32_t kernel;          /* enum w4a16_kernel (never AUTO once planned)       */
-  int32_t split_k;         /* GEMV, MFMA cfg 7/8/11-13: k-splits (1 = none)     */
-  int32_t tile_cfg;        /* MFMA: tiling 1, 2, 6, 7, 11, 12 or 13 (tile_m x
-                              tile_n); GEMV: 1 / 2 = 8 / 16 waves per workgroup
+  int32_t split_k;         /* GEMV, MFMA cfg 7/11-14: k-splits (1 = none)       */
+  int32_t tile_cfg;        /* MFMA: tiling 1, 2, 6, 7, 11, 12, 13 or 14
+                              (tile_m x tile_n; 14: the 128 x 256 streamed
+                              tile with two k-slices per workgroup);
+                              GEMV: 1 / 2 = 8 / 16 waves per workgroup
                               (16 for M <= 2), 4 / 5 = the same with the
                               activations staged in LDS (M <= 2; larger M
                               always stages them), 6 / 7 = 16 / 8 waves
