@@ -383,7 +383,8 @@ def test_planner_gemv_split_rule():
 def test_planner_gemv_blocks_and_waves():
     """Decode block, wave and activation-staging rules (measured on MI355X): on
     16/32-column blocks the activations are read directly with 16 waves at
-    M = 1 for any K and at M = 2 up to 8192 rows per split, else 8; 32-column
+    M = 1 for any K (but 8 on 16-column blocks with 2048 < K <= 4096) and at
+    M = 2 up to 8192 rows per split, else 8; 32-column
     blocks where 16-column ones would leave every CU between one and two blocks
     (K < 8192 only); activations staged in LDS for M <= 2 on 64-column blocks
     and on 128-column blocks where those give 7/8 of the CUs one each (cfg 7:
@@ -391,7 +392,11 @@ def test_planner_gemv_blocks_and_waves():
     4), one chunk, no split."""
     from w4a16 import _lib
 
-    p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs)
+    p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs), 8 waves
+    assert (p.tile_n, p.tile_cfg) == (16, 1)
+    p = _lib.plan(2, 4096, 4096, 128)            # ... 16 at M = 2
+    assert (p.tile_n, p.tile_cfg) == (16, 2)
+    p = _lib.plan(1, 4096, 2048, 128)            # ... and at K = 2048
     assert (p.tile_n, p.tile_cfg) == (16, 2)
     p = _lib.plan(1, 6144, 4096, 128)            # 384 blocks of 16 -> 192 of 32
     assert (p.tile_n, p.tile_cfg) == (32, 2)

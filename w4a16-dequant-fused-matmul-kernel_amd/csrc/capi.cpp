@@ -98,8 +98,12 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
 //     (cfg 4), 128-column blocks with 16 waves (cfg 5);
 //   * 16- and 32-column blocks read them directly with 16 waves (cfg 2) at
 //     M = 1 for any K (K = 28672, N = 8192: 27.2 us against 30.8 with 8 waves
-//     and 28.7 staged; K = 14336, N = 4096: 11.7 against 11.9 staged; C2 4.7)
-//     and at M = 2 up to K / split = 8192, with 8 waves (cfg 1) beyond;
+//     and 28.7 staged; K = 14336, N = 4096: 11.9 against 13.9 with 8 waves;
+//     32-column blocks, K = 4096, N = 6144: 6.43 against 7.19), except
+//     16-column blocks with 2048 < K <= 4096 at M = 1, where 8 waves with four
+//     rows per lane do better (C2: 4.66 against 4.75 us, G = 64 4.81 against
+//     4.92; N = 2048 and K = 2048 a tie), and at M = 2 up to K / split =
+//     8192, with 8 waves (cfg 1) beyond;
 //   * M > 2 always stages them (gemv_kernel, cfg 1).
 int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   const int64_t ks = K / (split > 0 ? split : 1);
@@ -112,6 +116,7 @@ int gemv_waves_cfg(int64_t M, int64_t K, int split, int cols) {
   // 15.2 vs 17.2)
   if (cols == 128 || (stage && cols == 64)) return kGemvDefaultConfig + 6;
   if (stage) return kGemvDefaultConfig + 3;
+  if (M == 1 && cols == 16 && ks > 2048 && ks <= 4096) return kGemvDefaultConfig;
   return (M == 1 || ks <= 8192) ? 2 : kGemvDefaultConfig;
 }
 
