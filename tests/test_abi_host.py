@@ -336,6 +336,27 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
         assert p.tile_m == (16 if rg else 8 if rg8 else g * 16), (M, N)
 
 
+def test_planner_decode_64_column_band():
+    """M <= 2 where 32-column blocks would outnumber the CUs (256 without a
+    device) but 64-column ones would not (8192 < N < 16384), K > 2048:
+    64-column blocks, unsplit -- the skinny kernel's for K <= 4096 with
+    G % 128 == 0, else the GEMV with staged activations and MFMA dot products
+    (cfg 7); K = 2048 keeps the 32-column GEMV."""
+    from w4a16 import _lib
+
+    for M, N, K, G, kern, cfg in ((1, 11008, 4096, 128, "skinny", 3), (2, 14336, 4096, 128, "skinny", 3),
+                                  (1, 11008, 4096, 32, "gemv", 7), (1, 10240, 8192, 128, "gemv", 7),
+                                  (2, 11008, 8192, 64, "gemv", 7)):
+        p = _lib.plan(M, N, K, G)
+        assert (_lib.KERNEL_NAMES[p.kernel], p.tile_cfg, p.tile_n, p.split_k) == (kern, cfg, 64, 1), (M, N, K, G)
+    p = _lib.plan(1, 11008, 2048, 128)
+    assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n) == ("gemv", 32)
+    # at the band's edges: N = 8192 (256 32-column blocks) and N = 16384 (256
+    # 64-column blocks) keep their plans
+    assert _lib.plan(1, 8192, 8192, 128).tile_n == 32
+    assert (_lib.plan(1, 16384, 4096, 128).tile_n, _lib.plan(1, 16384, 4096, 128).tile_cfg) == (64, 7)
+
+
 def test_planner_gemv_split_rule():
     """The automatic decode plan splits K four ways only for long K (>= 8192) with
     fewer 16-column blocks than CUs (measured faster there, slower at K = 4096

@@ -70,6 +70,20 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 // blocks would leave the CUs between one and two blocks each, 32-column blocks
 // (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
 // 7.5 us at M = 2).
+// M <= 2, K > 2048, where 32-column blocks would outnumber the CUs but
+// 64-column ones would not (8192 < N < 16384 on MI355X): 64-column blocks
+// with staged activations and the dot products on the matrix cores (cfg 7),
+// unsplit (the skinny kernel's 64-column blocks instead for K <= 4096 where
+// they apply: decode_takes_skinny).  The 32-column blocks take more than one
+// round there.  Measured on MI355X, µs, against 32-column blocks: M = 1,
+// K = 8192, N = 10240 17.39 -> 12.76; N = 14336 18.21 -> 13.84; M = 2,
+// K = 8192, N = 11008 20.78 -> 12.85; K = 14336, N = 12288 27.29 -> 19.81;
+// M = 1, K = 4096, N = 11008 11.03 -> 8.37 (skinny 7.82); K = 2048 slower
+// (5.57 -> 6.14).
+bool gemv_band64(int64_t M, int64_t N, int64_t K, int cus) {
+  return M <= 2 && K > 2048 && (N + 31) / 32 > cus && (N + 63) / 64 < cus;
+}
+
 int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
   // M <= 2: 128-column blocks where they give at least 7/8 of the CUs one
   // each (N = 28672 on MI355X: 224), a workgroup per CU reading two 256-byte
@@ -78,6 +92,7 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
   // N = 28672 25.0 vs 25.9 us; K = 4096 15.0 vs 15.9; M = 2, K = 8192 25.0 vs
   // 26.1)
   if (M <= 2 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
+  if (gemv_band64(M, N, K, cus)) return 64;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
     if ((N + c - 1) / c >= cus) {
@@ -181,9 +196,15 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
 // the GEMV is faster where the skinny kernel loops over K (M = 4, K = 8192,
 // N = 28672: 47 vs 75 us), not where its 64-column blocks take K in one batch
 // per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us).
+// M <= 2 in the 64-column band of gemv_band64 with K <= 4096: the skinny
+// kernel's 64-column blocks (one batch per wave) beat the GEMV's (M = 1,
+// K = 4096, N = 9216 / 11008 / 14336: 7.71 / 7.77 / 8.42 against 8.30 / 8.37 /
+// 8.69 us; M = 2, N = 14336 8.59 against 8.85), where G % 128 == 0 (G = 32:
+// 9.65 against 8.43).
 bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  return M >= 3 && M <= kGemvMaxM && skinny_applicable(M, G) &&
-         (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, G, cus)));
+  if (!skinny_applicable(M, G)) return false;
+  if (M <= 2) return K <= 4096 && gemv_band64(M, N, K, cus) && skinny_quad(M, N, G, cus);
+  return M <= kGemvMaxM && (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, G, cus)));
 }
 
 // Small batches (4 <= M <= 64) on large enough weights: the streamed prefill
@@ -381,7 +402,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
       const int mfma_split = split > 0 ? 0 : gemv_mfma_split(M, N, K, cus);
       const int cols = mfma_split ? 64 : gemv_cols_auto(M, N, K, cus);
-      int S = split > 0 ? split : mfma_split ? mfma_split : gemv_split_auto(N, K, cols, cus);
+      int S = split > 0                                   ? split
+              : mfma_split                                ? mfma_split
+              : cols == 64 && gemv_band64(M, N, K, cus)   ? 1
+                                                          : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
       if (S > 1) {
