@@ -286,7 +286,8 @@ def test_quant_entry_points_reject_bad_args(lib):
     (3, 28672, 8192, 128, "gemv"),    # ... longer K (the skinny loop): the GEMV up to M = 4
     (3, 28672, 4096, 64, "gemv"),     # ... and without 64-column blocks (G % 128 != 0)
     (4, 28672, 4096, 128, "skinny"),
-    (2, 6144, 4096, 128, "gemv"),
+    (2, 6144, 4096, 128, "skinny"),   # M <= 2, 4096 < N <= 8192: the skinny kernel's 32-column blocks
+    (2, 6144, 2048, 128, "gemv"),     # ... not for K <= 2048
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
     (8, 4096, 4096, 128, "skinny"),
     (5, 28672, 4096, 128, "skinny"),
@@ -366,7 +367,7 @@ def test_planner_gemv_split_rule():
 
     lib = _lib.load()
     for N in (512, 1024, 4096, 6144, 28672):
-        p = _lib.plan(1, N, 4096, 128)
+        p = _lib.plan(1, N, 4096, 128, _lib.KERNEL_GEMV, 0)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv"
         assert p.split_k == 1 and p.workspace_bytes == 0
         assert p.tile_n in (16, 32, 64, 128, 256)

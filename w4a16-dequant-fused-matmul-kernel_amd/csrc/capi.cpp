@@ -91,7 +91,9 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
   // the matrix cores, cfg 7, against 64-column blocks: M = 1, K = 8192,
   // N = 28672 25.0 vs 25.9 us; K = 4096 15.0 vs 15.9; M = 2, K = 8192 25.0 vs
   // 26.1)
-  if (M <= 2 && (N + 255) / 256 < cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
+  // (and at most one each: N = 37888, 296 blocks, took 25.9 us at K = 3584
+  // against 21.7 on 64-column blocks, 45.1 against 37.9 at K = 8192)
+  if (M <= 2 && (N + 127) / 128 <= cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
   if (gemv_band64(M, N, K, cus)) return 64;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
@@ -196,14 +198,31 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
 // the GEMV is faster where the skinny kernel loops over K (M = 4, K = 8192,
 // N = 28672: 47 vs 75 us), not where its 64-column blocks take K in one batch
 // per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us).
-// M <= 2 in the 64-column band of gemv_band64 with K <= 4096: the skinny
-// kernel's 64-column blocks (one batch per wave) beat the GEMV's (M = 1,
-// K = 4096, N = 9216 / 11008 / 14336: 7.71 / 7.77 / 8.42 against 8.30 / 8.37 /
-// 8.69 us; M = 2, N = 14336 8.59 against 8.85), where G % 128 == 0 (G = 32:
-// 9.65 against 8.43).
+// M <= 2, G % 128 == 0, K > 2048: the skinny kernel (MFMA dots, one batch per
+// wave up to K = 4096) where the GEMV's blocks fit the CUs badly
+// (measured on MI355X, µs, against the GEMV's plan):
+//   * 32-column blocks where 16-column ones outnumber the CUs but 32-column
+//     ones do not (4096 < N <= 8192), K <= 8192: M = 1, K = 4096, N = 4608 /
+//     6144 / 8192: 6.25 / 6.45 / 6.61 -> 6.02 / 6.17 / 6.29; K = 3584,
+//     N = 6144 6.35 -> 6.05; K = 8192, N = 6144 12.78 -> 11.12; M = 2,
+//     K = 4096, N = 6144 / 8192 7.52 / 7.79 -> 6.33 / 6.50 (K = 2048 slower:
+//     4.06 -> 4.41; G = 32 a tie);
+//   * 64-column blocks with K <= 4096 in the 64-column band of gemv_band64
+//     (M = 1, K = 4096, N = 9216 / 11008 / 14336: 8.30 / 8.37 / 8.69 ->
+//     7.71 / 7.77 / 8.42; M = 2, N = 14336 8.85 -> 8.59) and where 128-column
+//     blocks would outnumber the CUs but 256-column ones would not fill them
+//     (M = 1, K = 3584 / 4096, N = 37888: 21.7 / 22.5 -> 20.9 / 21.3; M = 2,
+//     K = 4096 22.7 -> 21.8; from N = 65536 the GEMV's 256-column blocks fill
+//     the CUs).
 bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (!skinny_applicable(M, G)) return false;
-  if (M <= 2) return K <= 4096 && gemv_band64(M, N, K, cus) && skinny_quad(M, N, G, cus);
+  if (M <= 2) {
+    if (G % 128 != 0 || K <= 2048) return false;
+    const bool wide32 = N % 2 == 0 && (N + 15) / 16 > cus && (N + 31) / 32 <= cus;
+    if (wide32) return K <= 8192;
+    return K <= 4096 && skinny_quad(M, N, G, cus) &&
+           (gemv_band64(M, N, K, cus) || ((N + 127) / 128 > cus && (N + 255) / 256 < cus));
+  }
   return M <= kGemvMaxM && (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, G, cus)));
 }
 
