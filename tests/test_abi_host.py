@@ -544,6 +544,12 @@ def test_planner_prefill_split_k():
     # G = 32 (a scale / zero load per half-step): cfg 11 split for ~448 workgroups
     p = _lib.plan(256, 8192, 28672, 32)
     assert p.tile_cfg == 11 and p.split_k == 7 and p.grid_x == 448
+    # splits never take the streamed tiles past two workgroups per CU (512
+    # without a device): 296 tiles stay unsplit, 148 64-row tiles split 3 ways
+    p = _lib.plan(256, 37888, 3584, 128)
+    assert (p.tile_cfg, p.split_k, p.grid_x) == (11, 1, 296)
+    p = _lib.plan(64, 37888, 3584, 128)
+    assert (p.tile_cfg, p.split_k, p.grid_x) == (13, 3, 444)
     # a forced split that two k-slices (8-step units) cannot honour: cfg 11
     p = _lib.plan(256, 1028, 2048, 64, _lib.KERNEL_MFMA, 3)
     assert (p.tile_cfg, p.split_k) == (11, 3)

@@ -324,11 +324,15 @@ SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus
   return {-1, 0};
 }
 
-// k-splits for the streamed kernel on few tiles: about 448 workgroups (two
-// per CU at most), at least 8 k-steps per split.
-int stream_split_for(int64_t tiles, int64_t K) {
+// k-splits for the streamed kernel on few tiles: about 448 workgroups, at
+// least 8 k-steps per split, and never more workgroups than two per CU (a
+// split that spills into a second round costs its partials and a round:
+// M = 256, K = 3584, N = 37888, 296 tiles: 97.3 us at 2 splits, 84.8 unsplit;
+// M = 64, 148 64-row tiles: 44.2 at 4, 39.4 at 2).
+int stream_split_for(int64_t tiles, int64_t K, int cus) {
   const int64_t kt = K / 64;
   int64_t s = (448 + tiles - 1) / tiles;
+  if (s * tiles > 2 * (int64_t)cus) s = 2 * (int64_t)cus / tiles;
   if (s > kt / 8) s = kt / 8;
   return s < 1 ? 1 : (int)s;
 }
@@ -337,7 +341,7 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) {
     if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return {2, 1};
     const int rows = M <= 32 ? 32 : 64;
-    const int s = stream_split_for((N + 255) / 256 * ((M + rows - 1) / rows), K);
+    const int s = stream_split_for((N + 255) / 256 * ((M + rows - 1) / rows), K, cus);
     return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
@@ -368,7 +372,7 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // 8192: 137.9 at 7 vs 146.8 at 4; M = 512, K = 4096, N = 14336: 80.8 at 2 vs
   // 82.7)
   if (c11 && t6 < 448) {
-    const int s = stream_split_for(t6, K);
+    const int s = stream_split_for(t6, K, cus);
     if (s >= 2) return {11, stream_splits((int)K, s)};
   }
   if (2 * t6 >= cus) {
