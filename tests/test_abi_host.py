@@ -420,12 +420,16 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg) == (16, 2)
     p = _lib.plan(1, 4096, 2048, 128)            # ... and at K = 2048
     assert (p.tile_n, p.tile_cfg) == (16, 2)
-    p = _lib.plan(1, 6144, 4096, 128)            # 384 blocks of 16 -> 192 of 32
+    p = _lib.plan(1, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)   # 384 blocks of 16 -> 192 of 32
     assert (p.tile_n, p.tile_cfg) == (32, 2)
-    p = _lib.plan(2, 6144, 4096, 128)
+    p = _lib.plan(2, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)
     assert (p.tile_n, p.tile_cfg) == (32, 2)
-    p = _lib.plan(1, 6144, 14336, 128)           # long K keeps 16-column blocks
-    assert p.tile_n == 16
+    p = _lib.plan(1, 6144, 14336, 128)           # ... at any K, unsplit, 16 waves
+    assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n, p.tile_cfg, p.split_k) == ("gemv", 32, 2, 1)
+    p = _lib.plan(1, 6144, 28672, 128)           # ... even past the long-row split's K
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (32, 2, 1)
+    p = _lib.plan(1, 8192, 28672, 128)           # not at N = 8192 (256 blocks of 32)
+    assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
     p = _lib.plan(2, 4096, 10240, 128)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
     p = _lib.plan(2, 4096, 14336, 128)           # ... longer: MFMA dots, split K

@@ -70,6 +70,17 @@ bool fits(int64_t M, int64_t N, int64_t K, int64_t G) {
 // blocks would leave the CUs between one and two blocks each, 32-column blocks
 // (at most one per CU) win (K = 4096, N = 6144: 7.3 -> 6.5 us at M = 1, 9.0 ->
 // 7.5 us at M = 2).
+// Where 16-column blocks would leave the CUs between one and two blocks each
+// (4096 < N <= 8192 on MI355X): 32-column blocks (at most one per CU), at any K
+// and unsplit.  Measured on MI355X, M = 1, µs, against 16-column blocks:
+// K = 4096, N = 6144 7.3 -> 6.5; K = 8192, N = 5120 / 6144 12.66 / 12.78 ->
+// 9.64 / 9.70; K = 13824 19.86 / 20.22 -> 14.72 / 14.73 (split 4 ways: 18.9,
+// 8 waves: 15.8); M = 2, K = 8192, N = 6144 15.38 -> 11.29.
+bool gemv_band32(int64_t N, int cus) {
+  const int64_t b16 = (N + 15) / 16;
+  return b16 > cus && b16 <= 2 * (int64_t)cus;
+}
+
 // M <= 2, K > 2048, where 32-column blocks would outnumber the CUs but
 // 64-column ones would not (8192 < N < 16384 on MI355X): 64-column blocks
 // with staged activations and the dot products on the matrix cores (cfg 7),
@@ -97,11 +108,7 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
   if (gemv_band64(M, N, K, cus)) return 64;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
-    if ((N + c - 1) / c >= cus) {
-      const int64_t b16 = (N + 15) / 16;
-      if (c == 16 && K < 8192 && b16 > cus && b16 <= 2 * (int64_t)cus) return 32;
-      return c;
-    }
+    if ((N + c - 1) / c >= cus) return c == 16 && gemv_band32(N, cus) ? 32 : c;
   return 16;
 }
 
@@ -161,6 +168,11 @@ int gemv_split_auto(int64_t N, int64_t K, int cols, int cus) {
 // split, or 0 where the rule does not apply.
 int gemv_mfma_split(int64_t M, int64_t N, int64_t K, int cus) {
   if (M > 2 || K < (M == 2 ? 12288 : 16384)) return 0;
+  // M = 1 where 32-column blocks are fewer than the CUs (4096 < N < 8192):
+  // those, unsplit (K = 16384, N = 6144: 16.4 against 18.0 us; K = 28672
+  // 25.4 against 27.1; K = 20480, N = 5120 19.2 against 22.0; not at N = 8192,
+  // one full round: 27.0 against 24.8, nor at M = 2: 19.4 against 18.2)
+  if (M == 1 && gemv_band32(N, cus) && (N + 31) / 32 < cus) return 0;
   const int64_t nblk = (N + 63) / 64;
   const int64_t want = (int64_t)cus * 7 / 8;
   if (nblk < 32 || nblk >= want) return 0;
@@ -202,11 +214,13 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
 // wave up to K = 4096) where the GEMV's blocks fit the CUs badly
 // (measured on MI355X, µs, against the GEMV's plan):
 //   * 32-column blocks where 16-column ones outnumber the CUs but 32-column
-//     ones do not (4096 < N <= 8192), K <= 8192: M = 1, K = 4096, N = 4608 /
-//     6144 / 8192: 6.25 / 6.45 / 6.61 -> 6.02 / 6.17 / 6.29; K = 3584,
-//     N = 6144 6.35 -> 6.05; K = 8192, N = 6144 12.78 -> 11.12; M = 2,
-//     K = 4096, N = 6144 / 8192 7.52 / 7.79 -> 6.33 / 6.50 (K = 2048 slower:
-//     4.06 -> 4.41; G = 32 a tie);
+//     ones do not (4096 < N <= 8192), up to K = 4096 at M = 1 (one batch per
+//     wave) and K = 8192 at M = 2, against the GEMV's 32-column blocks: M = 1,
+//     K = 4096, N = 4608 / 6144 / 8192: 6.25 / 6.45 / 6.61 -> 6.02 / 6.17 /
+//     6.29; K = 3584, N = 6144 6.35 -> 6.05; M = 2, K = 4096, N = 6144 /
+//     8192 7.52 / 7.79 -> 6.33 / 6.50, K = 5120 9.51 -> 8.56, K = 8192 a tie
+//     (M = 1, K = 5120 .. 13824: the GEMV's blocks 5-15 % faster; K = 2048
+//     slower: 4.06 -> 4.41; G = 32 a tie);
 //   * 64-column blocks with K <= 4096 in the 64-column band of gemv_band64
 //     (M = 1, K = 4096, N = 9216 / 11008 / 14336: 8.30 / 8.37 / 8.69 ->
 //     7.71 / 7.77 / 8.42; M = 2, N = 14336 8.85 -> 8.59) and where 128-column
@@ -219,7 +233,7 @@ bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 2) {
     if (G % 128 != 0 || K <= 2048) return false;
     const bool wide32 = N % 2 == 0 && (N + 15) / 16 > cus && (N + 31) / 32 <= cus;
-    if (wide32) return K <= 8192;
+    if (wide32) return K <= (M == 1 ? 4096 : 8192);
     return K <= 4096 && skinny_quad(M, N, G, cus) &&
            (gemv_band64(M, N, K, cus) || ((N + 127) / 128 > cus && (N + 255) / 256 < cus));
   }
@@ -428,6 +442,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       int S = split > 0                                   ? split
               : mfma_split                                ? mfma_split
               : cols == 64 && gemv_band64(M, N, K, cus)   ? 1
+              : cols == 32 && gemv_band32(N, cus)         ? 1
                                                           : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
