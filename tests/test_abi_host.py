@@ -430,6 +430,12 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg, p.split_k) == (32, 2, 1)
     p = _lib.plan(1, 8192, 28672, 128)           # not at N = 8192 (256 blocks of 32)
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
+    # 128-column blocks, unsplit, where 64-column ones would take more than one
+    # round (N > 16384) and 128-column ones not; N = 16384 keeps one round of 64
+    for N, K in ((16896, 4096), (20480, 8192), (20480, 28672), (32768, 4096)):
+        p = _lib.plan(1, N, K, 128)
+        assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1), (N, K)
+    assert _lib.plan(1, 16384, 4096, 128).tile_n == 64
     p = _lib.plan(2, 4096, 10240, 128)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
     p = _lib.plan(2, 4096, 14336, 128)           # ... longer: MFMA dots, split K

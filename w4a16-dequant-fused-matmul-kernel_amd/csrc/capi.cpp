@@ -103,8 +103,12 @@ int gemv_cols_auto(int64_t M, int64_t N, int64_t K, int cus) {
   // N = 28672 25.0 vs 25.9 us; K = 4096 15.0 vs 15.9; M = 2, K = 8192 25.0 vs
   // 26.1)
   // (and at most one each: N = 37888, 296 blocks, took 25.9 us at K = 3584
-  // against 21.7 on 64-column blocks, 45.1 against 37.9 at K = 8192)
-  if (M <= 2 && (N + 127) / 128 <= cus && (N + 127) / 128 >= cus * 7 / 8) return 128;
+  // against 21.7 on 64-column blocks, 45.1 against 37.9 at K = 8192), and
+  // down to where 64-column blocks would take more than one round (N > 16384
+  // on MI355X: M = 1, K = 4096, N = 18432 / 20480 / 24576 14.84 / 14.80 /
+  // 15.46 -> 13.69 / 13.68 / 14.47 us; K = 8192 24.22 / 24.38 / 25.06 ->
+  // 22.16 / 22.93 / 23.91; M = 2, K = 8192, N = 20480 24.60 -> 23.02), unsplit
+  if (M <= 2 && (N + 127) / 128 <= cus && (N + 63) / 64 > cus) return 128;
   if (gemv_band64(M, N, K, cus)) return 64;
   static const int kCols[] = {256, 64, 32, 16};
   for (int c : kCols)
@@ -443,6 +447,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
               : mfma_split                                ? mfma_split
               : cols == 64 && gemv_band64(M, N, K, cus)   ? 1
               : cols == 32 && gemv_band32(N, cus)         ? 1
+              : cols == 128 && M <= 2                     ? 1
                                                           : gemv_split_auto(N, K, cols, cus);
       const int64_t KP = K / 8;
       if (KP == 0) S = 1;
