@@ -284,14 +284,28 @@ def test_quant_entry_points_reject_bad_args(lib):
     (1, 4096, 4096, 128, "gemv"),
     (3, 28672, 4096, 128, "skinny"),  # wide N, K <= 4096: 64-column skinny blocks from M = 3
     (3, 28672, 8192, 128, "gemv"),    # ... longer K (the skinny loop): the GEMV up to M = 4
-    (3, 28672, 4096, 64, "gemv"),     # ... and without 64-column blocks (G % 128 != 0)
+    (3, 28672, 4096, 32, "skinny"),   # ... at any G
     (4, 28672, 4096, 128, "skinny"),
     (2, 6144, 4096, 128, "skinny"),   # M <= 2, 4096 < N <= 8192: the skinny kernel's 32-column blocks
+    (2, 6144, 4096, 32, "skinny"),    # ... at any G up to K = 4096
+    (2, 6144, 8192, 128, "skinny"),   # ... at M = 2 up to K = 8192 with G % 128 == 0
+    (2, 6144, 8192, 64, "gemv"),
     (2, 6144, 2048, 128, "gemv"),     # ... not for K <= 2048
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
     (8, 4096, 4096, 128, "skinny"),
     (5, 28672, 4096, 128, "skinny"),
-    (5, 28672, 4096, 64, "mfma"),     # G = 64: the streamed small-M tiles
+    (5, 28672, 4096, 64, "skinny"),   # 64-column blocks with G % 64 == 0 ...
+    (8, 28672, 8192, 64, "skinny"),
+    (8, 28672, 8192, 32, "mfma"),     # ... or K <= 4096; else the streamed small-M tiles
+    (16, 11008, 4096, 32, "skinny"),
+    (8, 4096, 28672, 128, "skinny"),  # long rows on 16-column blocks: skinny up to M = 8 ...
+    (12, 4096, 28672, 128, "mfma"),   # ... the streamed tiles from M = 9 at K >= 24576
+    (16, 4096, 20480, 64, "mfma"),    # ... from M = 16 beyond K = 16384
+    (16, 4096, 14336, 64, "skinny"),
+    (16, 4096, 11008, 32, "mfma"),    # ... and beyond K = 8192 with G = 32
+    (17, 4096, 11008, 64, "mfma"),    # ... or from M = 17 with G = 64
+    (12, 8192, 28672, 128, "skinny"),  # 32-column blocks at long K up to M = 16
+    (32, 8192, 28672, 128, "mfma"),    # ... not beyond
     (9, 4096, 4096, 128, "skinny"),
     (64, 4096, 11008, 64, "mfma"),
     (24, 4096, 4096, 128, "skinny"),  # 8 MiB of weights: skinny up to M = 32
@@ -318,16 +332,18 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     assert _lib.KERNEL_NAMES[p.kernel] == kernel
     assert p.grid_x >= 1 and p.grid_y >= 1
     if kernel == "skinny":
-        # M > 16 with 128-groups and few enough blocks: one 16-row group per
+        # M > 16 with K <= 4096 and few enough blocks: one 16-row group per
         # workgroup (test_planner_skinny_row_groups); else 32-column blocks
         # (cfg 2) where 16-column ones outnumber the CUs (256 on MI355X, also
         # the library's value without a device), M <= 32 and N even; else
         # 16-column blocks with 4 waves
         g = (M + 15) // 16
-        rg = (M > 16 and G % 128 == 0 and K <= 4096 and
-              (N % 2 == 0 and (N + 31) // 32 * g <= 256 or N % 4 == 0 and (N + 63) // 64 * g <= 512))
-        rg8 = 13 <= M <= 16 and G % 128 == 0 and N % 2 == 0 and (N + 31) // 32 * 2 <= 256
-        quad = M <= 16 and N % 4 == 0 and G % 128 == 0 and (N + 63) // 64 > 128
+        rg = (M > 16 and K <= 4096 and
+              (N % 2 == 0 and (N + 31) // 32 * g <= 256 or
+               N % 4 == 0 and (N + 63) // 64 * g <= (512 if G % 64 == 0 else 256)))
+        rg8 = (13 <= M <= 16 and N % 2 == 0 and (N + 31) // 32 * 2 <= 256 and
+               (K <= 4096 or G % 128 == 0 and K <= 16384))
+        quad = M <= 16 and N % 4 == 0 and (G % 64 == 0 or K <= 4096) and (N + 63) // 64 > 128
         wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
         if rg or rg8:
             want = (2, 32) if (N + 31) // 32 * g <= 256 or rg8 else (3, 64)
@@ -485,48 +501,69 @@ def test_planner_small_batch_wide_weights_stream():
                     (9, 8192, 8192), (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
     # up to N = 8192 (N = 16384 for M <= 16) the skinny kernel's 32-column
-    # blocks beat the streamed tiles, long K included
+    # blocks beat the streamed tiles, long K included up to M = 16, K <= 8192
+    # beyond
     for M, N, K in ((16, 8192, 28672), (4, 8192, 28672), (17, 8192, 8192), (20, 8192, 6144)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (2, 32), (M, N, K)
         assert p.grid_x == N // 32
-    # M <= 16 with more than 128 64-column blocks: 64-column skinny blocks
-    for M, N, K in ((16, 28672, 4096), (8, 28672, 8192), (4, 14336, 4096)):
-        p = _lib.plan(M, N, K, 128)
-        assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (3, 64), (M, N, K)
-    # ... measured with G = 128; smaller groups keep the streamed tiles
-    for G in (32, 64):
-        p = _lib.plan(16, 8192, 28672, G)
-        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 12, G
+    for M, N, K in ((17, 8192, 14336), (24, 8192, 28672)):
+        assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 128).kernel] == "mfma", (M, N, K)
+    # M <= 16 with more than 128 64-column blocks: 64-column skinny blocks,
+    # with G % 64 == 0 or K <= 4096
+    for M, N, K, G in ((16, 28672, 4096, 128), (8, 28672, 8192, 128), (4, 14336, 4096, 128),
+                       (8, 28672, 8192, 64), (8, 14336, 4096, 32)):
+        p = _lib.plan(M, N, K, G)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny" and (p.tile_cfg, p.tile_n) == (3, 64), (M, N, K, G)
+    # ... the 32-column blocks' rule was measured with G = 128; smaller groups
+    # keep the streamed tiles there, as does G = 32 with K > 4096 on 64-column
+    # blocks
+    for M, N, K, G in ((16, 8192, 28672, 32), (16, 8192, 28672, 64), (8, 28672, 8192, 32)):
+        p = _lib.plan(M, N, K, G)
+        assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == 12, (M, N, K, G)
 
 
 def test_planner_skinny_row_groups():
-    """17 <= M <= 64, G % 128 == 0: skinny blocks with one 16-row group per
-    workgroup (tile_m 16, ceil(M / 16) workgroups per column block) where the
-    workgroups stay near the CU count: 32-column blocks while they fit one
-    round, else 64-column blocks up to two rounds for K <= 4096; with longer K
-    only two row groups on one round (64 columns from M = 24)."""
+    """17 <= M <= 64: skinny blocks with one 16-row group per workgroup
+    (tile_m 16, ceil(M / 16) workgroups per column block) where the workgroups
+    stay near the CU count: 32-column blocks while they fit one round, else
+    64-column blocks up to two rounds for K <= 4096 (one round at G = 32);
+    with longer K only two row groups on one round, 32-column blocks up to
+    K = 16384 (K = 8192 below G = 128) and 64-column ones from M = 24 up to
+    K = 8192 with G % 128 == 0."""
     from w4a16 import _lib
 
-    for M, N, K, cfg in ((32, 4096, 4096, 2), (17, 4096, 4096, 2), (24, 6144, 4096, 3),
-                         (40, 4096, 4096, 3), (64, 4096, 4096, 3), (64, 8192, 4096, 3),
-                         (32, 14336, 4096, 3), (32, 4096, 14336, 2), (17, 4096, 14336, 2),
-                         (24, 8192, 8192, 3), (32, 8192, 28672, 3)):
-        p = _lib.plan(M, N, K, 128)
-        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K)
+    for M, N, K, G, cfg in ((32, 4096, 4096, 128, 2), (17, 4096, 4096, 128, 2),
+                            (24, 6144, 4096, 128, 3), (40, 4096, 4096, 128, 3),
+                            (64, 4096, 4096, 128, 3), (64, 8192, 4096, 128, 3),
+                            (32, 14336, 4096, 128, 3), (32, 4096, 14336, 128, 2),
+                            (17, 4096, 14336, 128, 2), (24, 8192, 8192, 128, 3),
+                            (32, 4096, 16384, 128, 2), (32, 4096, 4096, 64, 2),
+                            (32, 4096, 4096, 32, 2), (48, 4096, 4096, 32, 3),
+                            (64, 8192, 4096, 64, 3), (32, 4096, 8192, 64, 2),
+                            (24, 4096, 8192, 32, 2)):
+        p = _lib.plan(M, N, K, G)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K, G)
         cols = 64 if cfg == 3 else 32
-        assert (p.tile_cfg, p.tile_m, p.tile_n) == (cfg, 16, cols), (M, N, K)
+        assert (p.tile_cfg, p.tile_m, p.tile_n) == (cfg, 16, cols), (M, N, K, G)
         assert p.grid_x == (N + cols - 1) // cols * ((M + 15) // 16) and p.split_k == 1
-    # 13 <= M <= 16: two 8-row groups on 32-column blocks that fit the CUs
-    for M, N, K in ((16, 4096, 4096), (13, 4096, 14336)):
-        p = _lib.plan(M, N, K, 128)
-        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K)
-        assert (p.tile_cfg, p.tile_m, p.tile_n, p.grid_x) == (2, 8, 32, N // 32 * 2), (M, N, K)
+    # 13 <= M <= 16: two 8-row groups on 32-column blocks that fit the CUs, up
+    # to K = 4096 at any G and K = 16384 with G % 128 == 0
+    for M, N, K, G in ((16, 4096, 4096, 128), (13, 4096, 14336, 128), (16, 4096, 4096, 64),
+                       (16, 4096, 4096, 32)):
+        p = _lib.plan(M, N, K, G)
+        assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K, G)
+        assert (p.tile_cfg, p.tile_m, p.tile_n, p.grid_x) == (2, 8, 32, N // 32 * 2), (M, N, K, G)
     # not: wide N, three or more row groups with K > 4096, M = 17 on 64-column
-    # blocks with K > 4096, groups below 128, M <= 12, M <= 16 on more blocks
+    # blocks with K > 4096, long rows (32-column blocks beyond K = 16384,
+    # 64-column ones beyond 8192), smaller groups with longer K or (G = 32)
+    # 64-column blocks beyond one round, M <= 12, M <= 16 on more blocks
     for M, N, K, G in ((32, 28672, 4096, 128), (48, 14336, 4096, 128), (48, 8192, 8192, 128),
-                       (64, 4096, 14336, 128), (17, 8192, 8192, 128), (32, 4096, 4096, 64),
-                       (12, 4096, 4096, 128), (16, 6144, 4096, 128), (16, 4096, 4096, 64)):
+                       (64, 4096, 14336, 128), (17, 8192, 8192, 128), (32, 8192, 28672, 128),
+                       (32, 4096, 28672, 128), (24, 4096, 20480, 128), (32, 6144, 14336, 128),
+                       (16, 4096, 28672, 128), (32, 4096, 14336, 64), (32, 6144, 8192, 64),
+                       (16, 4096, 14336, 64), (32, 14336, 4096, 32), (48, 6144, 4096, 32),
+                       (12, 4096, 4096, 128), (16, 6144, 4096, 128)):
         p = _lib.plan(M, N, K, G)
         assert not (_lib.KERNEL_NAMES[p.kernel] == "skinny" and p.tile_m < (M + 15) // 16 * 16), (M, N, K, G)
     # a forced skinny plan takes the same row groups

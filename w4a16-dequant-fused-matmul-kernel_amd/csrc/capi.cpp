@@ -203,7 +203,7 @@ struct MfmaChoice {
   int cfg, split;
 };
 
-bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
+bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus);
 
 // Decode batches 3 <= M <= 8: the MFMA skinny kernel does the M dot products
 // per dequantised pair on the matrix cores where the GEMV spends M v_dot2 on
@@ -213,35 +213,42 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus);
 // (M = 5, K = 4096, N = 28672: 29.7 vs 32.6 us).  At M <= 4 on wider weights
 // the GEMV is faster where the skinny kernel loops over K (M = 4, K = 8192,
 // N = 28672: 47 vs 75 us), not where its 64-column blocks take K in one batch
-// per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us).
-// M <= 2, G % 128 == 0, K > 2048: the skinny kernel (MFMA dots, one batch per
-// wave up to K = 4096) where the GEMV's blocks fit the CUs badly
-// (measured on MI355X, µs, against the GEMV's plan):
+// per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us; G = 64 /
+// 32: 17.8 / 20.2 vs 21.9 / 22.3; N = 37888, G = 64 / 32: 23.5 / 27.3 vs
+// 30.1 / 30.7).
+// M <= 2, K > 2048: the skinny kernel (MFMA dots, one batch per wave up to
+// K = 4096) where the GEMV's blocks fit the CUs badly (measured on MI355X, µs,
+// against the GEMV's plan):
 //   * 32-column blocks where 16-column ones outnumber the CUs but 32-column
-//     ones do not (4096 < N <= 8192), up to K = 4096 at M = 1 (one batch per
-//     wave) and K = 8192 at M = 2, against the GEMV's 32-column blocks: M = 1,
-//     K = 4096, N = 4608 / 6144 / 8192: 6.25 / 6.45 / 6.61 -> 6.02 / 6.17 /
-//     6.29; K = 3584, N = 6144 6.35 -> 6.05; M = 2, K = 4096, N = 6144 /
-//     8192 7.52 / 7.79 -> 6.33 / 6.50, K = 5120 9.51 -> 8.56, K = 8192 a tie
-//     (M = 1, K = 5120 .. 13824: the GEMV's blocks 5-15 % faster; K = 2048
-//     slower: 4.06 -> 4.41; G = 32 a tie);
-//   * 64-column blocks with K <= 4096 in the 64-column band of gemv_band64
+//     ones do not (4096 < N <= 8192), up to K = 4096 (one batch per wave; any
+//     G), and at M = 2 with G % 128 == 0 up to K = 8192, against the GEMV's
+//     32-column blocks: M = 1, K = 4096, N = 4608 / 6144 / 8192: 6.25 / 6.45 /
+//     6.61 -> 6.02 / 6.17 / 6.29; K = 3584, N = 6144 6.35 -> 6.05; M = 2,
+//     K = 4096, N = 6144 / 8192 7.52 / 7.79 -> 6.33 / 6.50, K = 5120 9.51 ->
+//     8.56, K = 8192 a tie (M = 1, K = 5120 .. 13824: the GEMV's blocks 5-15 %
+//     faster; K = 2048 slower: 4.06 -> 4.41).  Smaller groups, N = 6144:
+//     M = 2, K = 3584 / 4096, G = 64: 7.57 / 7.57 -> 6.43 / 6.50, G = 32:
+//     7.66 / 7.68 -> 6.78 / 6.81; M = 1 G = 64 6.43 / 6.50 -> 6.22 / 6.37,
+//     G = 32 a tie; K = 5120 the GEMV's (M = 2, G = 64: 9.63 vs 10.17);
+//   * G % 128 == 0: 64-column blocks with K <= 4096 in the 64-column band of
+//     gemv_band64
 //     (M = 1, K = 4096, N = 9216 / 11008 / 14336: 8.30 / 8.37 / 8.69 ->
 //     7.71 / 7.77 / 8.42; M = 2, N = 14336 8.85 -> 8.59) and where 128-column
 //     blocks would outnumber the CUs but 256-column ones would not fill them
 //     (M = 1, K = 3584 / 4096, N = 37888: 21.7 / 22.5 -> 20.9 / 21.3; M = 2,
 //     K = 4096 22.7 -> 21.8; from N = 65536 the GEMV's 256-column blocks fill
-//     the CUs).
+//     the CUs; G = 64 a tie, G = 32 the GEMV's: K = 4096, N = 11008 8.54
+//     vs 9.67).
 bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (!skinny_applicable(M, G)) return false;
   if (M <= 2) {
-    if (G % 128 != 0 || K <= 2048) return false;
+    if (K <= 2048) return false;
     const bool wide32 = N % 2 == 0 && (N + 15) / 16 > cus && (N + 31) / 32 <= cus;
-    if (wide32) return K <= (M == 1 ? 4096 : 8192);
-    return K <= 4096 && skinny_quad(M, N, G, cus) &&
+    if (wide32) return K <= (M == 2 && G % 128 == 0 ? 8192 : 4096);
+    return K <= 4096 && G % 128 == 0 && skinny_quad(M, N, K, G, cus) &&
            (gemv_band64(M, N, K, cus) || ((N + 127) / 128 > cus && (N + 255) / 256 < cus));
   }
-  return M <= kGemvMaxM && (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, G, cus)));
+  return M <= kGemvMaxM && (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, K, G, cus)));
 }
 
 // Small batches (4 <= M <= 64) on large enough weights: the streamed prefill
@@ -256,11 +263,29 @@ bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
 // M = 16 keeps the skinny kernel at K = 14336, N = 4096 (20.3 vs 22.4) and
 // below 20 MB; M = 9 wins only from N = 14336 (16.9 vs 18.1); M <= 3 keeps the
 // GEMV (M = 3, K = 4096, N = 28672: 21.9 vs 22.7).
+// Long rows on 16-column skinny blocks (N <= 4096 here; wider weights take the
+// skinny kernel's 32- / 64-column blocks, which pass X once per 32 / 64
+// columns, through the size rules and the skinny branch of make_plan): a
+// workgroup's time grows with K x M (every block streams all of X), the split
+// streamed tiles' with the weight bytes, so from M = 9 at K >= 24576, from
+// M = 16 beyond K = 16384, and beyond K = 8192 with smaller groups (G = 32
+// from M = 16, G = 64 from M = 17) the streamed tiles win (measured on MI355X,
+// µs, N = 4096, skinny vs streamed): K = 28672, G = 128, M = 12 / 16 / 17 / 20:
+// 31.0 / 33.2 / 37.6 / 37.6 vs 28.1 / 28.6 / 28.9 / 29.3 (G = 64: 32.2 / 36.4
+// / 40.5 / 44.7 vs 28.3 / 28.2 / 28.6 / 29.2); K = 20480, M = 16: G = 128 a
+// tie, G = 64 27.1 vs 24.9; G = 32, M = 16, K = 11008 / 14336: 19.8 / 23.5 vs
+// 18.3 / 22.3, M = 17 / 20, K = 14336 / 11008: 25.1 / 23.0 vs 22.3 / 19.2;
+// G = 64, M = 17, K = 14336: 22.7 vs 22.1.  Kept on the skinny kernel: M <= 8
+// (K = 28672, M = 4 / 8, G = 128: 24.4 / 27.0 vs 28.6 / 27.7; K = 20480,
+// M = 8: 20.7 vs 24.2), M = 16 at K = 14336 (G = 64: 20.2 vs 22.0), K = 8192
+// (G = 32, M = 16: 15.3 vs 16.8).
 bool small_m_takes_stream(int64_t M, int64_t N, int64_t K, int64_t G) {
   if (M < 4 || M > kSkinnyMaxM) return false;
   if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return false;
   const int64_t mb = K / 2 * N >> 20;   // packed weight MiB
   if (M >= 48) return true;
+  if (M >= 9 && K >= 24576) return true;
+  if (M >= 16 && K > (G % 128 == 0 || (G % 64 == 0 && M == 16) ? 16384 : 8192)) return true;
   if (M >= 24) return mb > 8;
   if (M >= 16) return N >= 8192 && mb >= 20;
   return (N >= 14336 && mb >= 24) || mb >= 64;
@@ -284,20 +309,35 @@ bool skinny_wide(int64_t M, int64_t N, int cus) {
 // N = 14336: 22.6 vs 19.6).  Measured with G = 128; smaller groups add
 // scale / zero loads to every skinny k-step and lose (M = 16, K = 28672,
 // N = 8192: G = 32 55.1 vs 48.6 us, G = 64 48.1 vs 46.1; G = 128 a tie).
-bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t G, int cus) {
-  return skinny_wide(M, N, cus) && G % 128 == 0 && (N <= 8192 || (N <= 16384 && M <= 16));
+// Beyond M = 16 up to K = 8192 (M = 17 / 20, K = 8192, N = 8192: 17.1 / 18.2
+// vs 20.7 / 20.9; M = 20, K = 6144, N = 8192: 17.8 vs 20.4; K = 8192,
+// N = 6144: 15.2 vs 19.6); longer rows with all M rows in each workgroup
+// gain nothing (M = 17, K = 14336, N = 8192: 26.1 vs 25.7) or lose (16-row
+// groups on the same blocks already do: M = 32, N = 6144, K = 14336: 39.0 vs
+// 25.6; N = 8192, K = 28672: 75.4 vs 44.0).
+bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  return skinny_wide(M, N, cus) && G % 128 == 0 && (M <= 16 || K <= 8192) &&
+         (N <= 8192 || (N <= 16384 && M <= 16));
 }
 
 // 64-column blocks (four columns per lane: 16-B weight loads, one activation
-// stream per 64 columns) for M <= 16, G % 128 == 0, where they still give more
-// than half the CUs a block (N > 8192 on MI355X).  Measured there against the
-// best other plan: M = 4 / 8, K = 4096, N = 28672: 20.9 / 22.4 vs 22.3 / 23.6
-// us (streamed tiles); M = 8, K = 8192, N = 28672: 35.6 vs 40.1; M = 16,
-// K = 4096, N = 14336: 14.7 vs 16.4 (32-column blocks); M = 16, K = 4096,
-// N = 28672: 23.7 vs 23.3.  Fewer blocks or smaller groups lose (K = 28672,
-// N = 8192: 52.5 vs 43.4; G = 32, K = 8192, N = 28672: 47.1 vs 43.1).
-bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
-  return M <= 16 && N % 4 == 0 && G % 128 == 0 && (N + 63) / 64 > cus / 2;
+// stream per 64 columns) for M <= 16 where they still give more than half the
+// CUs a block (N > 8192 on MI355X), with G % 64 == 0, or any G with K <= 4096
+// (one batch per wave, whose scale / zero loads are few).  Measured there
+// against the best other plan (µs): M = 4 / 8, K = 4096, N = 28672: 20.9 /
+// 22.4 vs 22.3 / 23.6 (streamed tiles; G = 64: 18.3 / 19.5 vs 22.4 / 22.8;
+// G = 32: 20.7 / 22.1 vs 23.2 / 23.6); M = 8, K = 8192, N = 28672: 35.6 vs
+// 40.1 (G = 64: 35.9 vs 38.4); M = 4: G = 64 34.1 vs 42.7; M = 16, K = 4096,
+// N = 14336: 14.7 vs 16.4 (32-column blocks; G = 64 / 32: 11.1 / 12.9 vs
+// 17.1 / 17.6 streamed); M = 16, K = 4096, N = 28672: 23.7 vs 23.3 (G = 64:
+// 21.8 vs 23.9); long rows: M = 8, K = 28672, N = 16384: 57.2 vs 67.9;
+// M = 12 / 16, K = 14336, N = 14336: 29.6 / 31.0 vs 38.8 / 34.6; M = 12,
+// K = 8192, N = 16384, G = 64: 22.8 vs 27.1.  Fewer blocks lose (K = 28672,
+// N = 8192: 52.5 vs 43.4), and so does G = 32 with K > 4096 (K = 8192,
+// N = 28672, M = 4 / 8: 39.9 / 41.3 vs 38.9 / 39.2; M = 8, K = N = 14336:
+// 38.4 vs 34.3).
+bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  return M <= 16 && N % 4 == 0 && (G % 64 == 0 || K <= 4096) && (N + 63) / 64 > cus / 2;
 }
 
 // Skinny blocks with one 16-row group per workgroup (plan tile_m = 16) for
@@ -314,31 +354,55 @@ bool skinny_quad(int64_t M, int64_t N, int64_t G, int cus) {
 // 48 / 64: 9.60 / 10.91 / 16.17 / 16.57 -> 8.14 / 8.12 / 9.28 / 8.56; N = 6144
 // M = 32 / 48: 11.88 / 19.00 -> 9.80 / 15.96; N = 8192 M = 64: 21.16 ->
 // 15.84; N = 14336 M = 32: 19.19 -> 17.72; K = 14336, N = 4096, M = 17 / 32:
-// 22.10 / 23.49 -> 20.72 / 20.94; K = 28672, N = 8192, M = 32: 63.86 ->
-// 52.40.  Slower (kept on the streamed tiles): N = 28672 at every M (M = 32:
-// 26.4 vs 34.2), three or four row groups with K > 4096 (M = 48, K = 8192,
-// N = 8192: 25.6 vs 29.4), M = 17 on 64-column blocks with K > 4096.  Smaller
-// groups than 128 add scale / zero loads to every k-step and were not measured.
+// 22.10 / 23.49 -> 20.72 / 20.94; N = 6144 / 8192, K = 8192, M = 32: 20.64 /
+// 21.49 -> 19.10 / 19.11.  Slower (kept on the streamed tiles): N = 28672 at
+// every M (M = 32: 26.4 vs 34.2), three or four row groups with K > 4096
+// (M = 48, K = 8192, N = 8192: 25.6 vs 29.4), M = 17 on 64-column blocks with
+// K > 4096, and long rows, whose time on a workgroup grows with K while the
+// split streamed tiles' grows with the weight bytes: 32-column blocks beyond
+// K = 16384 (K = 28672, N = 4096, M = 24 / 32: 38.3 / 39.5 vs 29.6 / 30.4),
+// 64-column ones beyond K = 8192 (N = 6144, M = 32, K = 14336 / 28672: 28.3 /
+// 49.7 vs 25.6 / 35.3; N = 8192, M = 24, K = 14336 28.6 vs 26.5; M = 32,
+// K = 28672: 54.5 vs 44.0; K = 11008 a tie).
+// Smaller groups (µs, G = 64 / 32, against the automatic plan before): with
+// K <= 4096 the same rules win, except 64-column blocks beyond one round at
+// G = 32 (K = 4096, N = 4096, M = 24 / 32 / 48 / 64: 9.71 / 11.01 / 16.36 /
+// 16.80 -> 8.34 / 8.40 / 9.85 / 9.31, G = 32 11.01 / 12.63 / 16.74 / 17.24
+// -> 8.67 / 9.27 / 11.29 / 10.36; N = 6144, M = 32: 15.53 -> 10.49, G = 32
+// 16.03 -> 11.89; N = 8192, M = 32: 17.44 -> 10.38, G = 32 17.70 -> 11.92;
+// 448 or 288 64-column blocks at G = 32: K = 4096, N = 14336, M = 32 20.1 vs
+// 22.2; N = 6144, M = 48 19.2 vs 20.1); with K > 4096 the 4-wave loop loads
+// them every k-step or two, and only two 16-row groups on 32-column blocks up
+// to K = 8192 still win (N = 4096, K = 8192, M = 24 / 32: G = 64 17.55 /
+// 18.88 -> 14.43 / 14.71, G = 32 17.97 / 19.39 -> 16.98 / 18.45; K = 11008
+// a tie, K = 14336 2-14 % slower; 64-column blocks, N = 6144, K = 8192, G = 64:
+// 22.6 vs 20.1).
 // 13 <= M <= 16: two 8-row groups on 32-column blocks where those fit the CUs
-// (N = 4096: K = 4096 7.61 -> 7.00 us, K = 14336 19.47 -> 18.13; M <= 12, or
-// more blocks, or 64-column blocks: slower).
+// (N = 4096: K = 4096 7.61 -> 7.00 us, G = 64 / 32 7.64 / 8.70 -> 7.17 /
+// 7.69; K = 14336 19.47 -> 18.13, up to K = 16384 at G = 128 only: G = 64
+// 20.2 vs 22.8, K = 28672 the streamed tiles'; M <= 12, or more blocks, or
+// 64-column blocks: slower).
 struct SkinnyRows {
   int cfg, rows;   // cfg -1: all rows in one workgroup
 };
 SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  if (M <= 12 || M > kSkinnyMaxM || G % 128 != 0) return {-1, 0};
+  if (M <= 12 || M > kSkinnyMaxM) return {-1, 0};
+  const bool g128 = G % 128 == 0;
   const bool c2 = N % 2 == 0, c3 = N % 4 == 0;
-  if (M <= 16) return c2 && (N + 31) / 32 * 2 <= cus ? SkinnyRows{2, 8} : SkinnyRows{-1, 0};
+  if (M <= 16)
+    return c2 && (N + 31) / 32 * 2 <= cus && (K <= 4096 || (g128 && K <= 16384))
+               ? SkinnyRows{2, 8}
+               : SkinnyRows{-1, 0};
   const int64_t g = (M + 15) / 16;
   const int64_t wg2 = (N + 31) / 32 * g, wg3 = (N + 63) / 64 * g;
   if (K <= 4096) {
     if (c2 && wg2 <= cus) return {2, 16};
-    if (c3 && wg3 <= 2 * cus) return {3, 16};
+    if (c3 && wg3 <= (G % 64 == 0 ? 2 : 1) * (int64_t)cus) return {3, 16};
     return {-1, 0};
   }
   if (g != 2) return {-1, 0};
-  if (c2 && wg2 <= cus) return {2, 16};
-  if (c3 && M >= 24 && wg3 <= cus) return {3, 16};
+  if (c2 && wg2 <= cus && K <= (g128 ? 16384 : 8192)) return {2, 16};
+  if (c3 && g128 && M >= 24 && wg3 <= cus && K <= 8192) return {3, 16};
   return {-1, 0};
 }
 
@@ -423,8 +487,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     else if (skinny_applicable(M, G) && skinny_row_groups(M, N, K, G, cus).cfg >= 0)
       kernel = W4A16_KERNEL_SKINNY;
     else if (small_m_takes_stream(M, N, K, G))
-      kernel = skinny_applicable(M, G) && (skinny_quad(M, N, G, cus) ||
-                                           skinny_wide_beats_stream(M, N, G, cus))
+      kernel = skinny_applicable(M, G) && (skinny_quad(M, N, K, G, cus) ||
+                                           skinny_wide_beats_stream(M, N, K, G, cus))
                    ? W4A16_KERNEL_SKINNY
                    : W4A16_KERNEL_MFMA;
     else if (gemv_applicable(M, N, G) && !decode_takes_skinny(M, N, K, G, cus))
@@ -496,7 +560,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       const SkinnyRows rg = skinny_row_groups(M, N, K, G, cus);
       p->tile_m = rg.cfg >= 0 ? rg.rows : (int32_t)((M + 15) / 16 * 16);
       p->tile_n = rg.cfg >= 0           ? (rg.cfg == 3 ? 64 : 32)
-                  : skinny_quad(M, N, G, cus) ? 64
+                  : skinny_quad(M, N, K, G, cus) ? 64
                   : skinny_wide(M, N, cus)    ? 32
                                               : 16;
       p->grid_x = (N + p->tile_n - 1) / p->tile_n * ((M + p->tile_m - 1) / p->tile_m);
