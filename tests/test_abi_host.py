@@ -283,8 +283,15 @@ def test_quant_entry_points_reject_bad_args(lib):
 @pytest.mark.parametrize("M,N,K,G,kernel", [
     (1, 4096, 4096, 128, "gemv"),
     (3, 28672, 4096, 128, "skinny"),  # wide N, K <= 4096: 64-column skinny blocks from M = 3
-    (3, 28672, 8192, 128, "gemv"),    # ... longer K (the skinny loop): the GEMV up to M = 4
-    (3, 28672, 4096, 32, "skinny"),   # ... at any G
+    (3, 28672, 8192, 128, "skinny"),  # ... and at longer K (the skinny loop)
+    (3, 28672, 4096, 32, "skinny"),   # ... at any G with K <= 4096
+    (3, 28672, 8192, 32, "gemv"),     # ... but G = 32 with K > 4096 keeps the GEMV
+    (3, 2048, 16384, 128, "gemv"),    # few column blocks, long K: the GEMV split along K
+    (5, 2048, 16384, 128, "skinny"),  # ... at M <= 4 for half the CUs' worth of blocks
+    (6, 1024, 8192, 128, "gemv"),     # ... up to M = 8 for a quarter
+    (1, 2560, 2048, 128, "skinny"),   # M <= 2, K <= 2048: the skinny kernel ...
+    (1, 6144, 2048, 128, "gemv"),     # ... outside the 32-column band
+    (2, 6144, 1024, 128, "skinny"),   # ... (which it takes up to K = 1024)
     (4, 28672, 4096, 128, "skinny"),
     (2, 6144, 4096, 128, "skinny"),   # M <= 2, 4096 < N <= 8192: the skinny kernel's 32-column blocks
     (2, 6144, 4096, 32, "skinny"),    # ... at any G up to K = 4096
@@ -358,7 +365,7 @@ def test_planner_decode_64_column_band():
     device) but 64-column ones would not (8192 < N < 16384), K > 2048:
     64-column blocks, unsplit -- the skinny kernel's for K <= 4096 with
     G % 128 == 0, else the GEMV with staged activations and MFMA dot products
-    (cfg 7); K = 2048 keeps the 32-column GEMV."""
+    (cfg 7); K = 2048 takes the skinny kernel's 64-column blocks."""
     from w4a16 import _lib
 
     for M, N, K, G, kern, cfg in ((1, 11008, 4096, 128, "skinny", 3), (2, 14336, 4096, 128, "skinny", 3),
@@ -366,8 +373,8 @@ def test_planner_decode_64_column_band():
                                   (2, 11008, 8192, 64, "gemv", 7)):
         p = _lib.plan(M, N, K, G)
         assert (_lib.KERNEL_NAMES[p.kernel], p.tile_cfg, p.tile_n, p.split_k) == (kern, cfg, 64, 1), (M, N, K, G)
-    p = _lib.plan(1, 11008, 2048, 128)
-    assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n) == ("gemv", 32)
+    p = _lib.plan(1, 11008, 2048, 128)          # K <= 2048: the skinny kernel's blocks
+    assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n) == ("skinny", 64)
     # at the band's edges: N = 8192 (256 32-column blocks) and N = 16384 (256
     # 64-column blocks) keep their plans
     assert _lib.plan(1, 8192, 8192, 128).tile_n == 32
@@ -434,8 +441,9 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg) == (16, 1)
     p = _lib.plan(2, 4096, 4096, 128)            # ... 16 at M = 2
     assert (p.tile_n, p.tile_cfg) == (16, 2)
-    p = _lib.plan(1, 4096, 2048, 128)            # ... and at K = 2048
+    p = _lib.plan(1, 4096, 2048, 128, _lib.KERNEL_GEMV, 0)   # ... and at K = 2048
     assert (p.tile_n, p.tile_cfg) == (16, 2)
+    assert _lib.KERNEL_NAMES[_lib.plan(1, 4096, 2048, 128).kernel] == "skinny"   # (planned there)
     p = _lib.plan(1, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)   # 384 blocks of 16 -> 192 of 32
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(2, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)
@@ -466,7 +474,7 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
     p = _lib.plan(1, 65536, 4096, 128)           # 256-column blocks: dot2, staged
     assert (p.tile_n, p.tile_cfg) == (256, 4)
-    p = _lib.plan(3, 28672, 8192, 128)           # M > 2 keeps 64-column blocks
+    p = _lib.plan(3, 28672, 8192, 128, _lib.KERNEL_GEMV, 0)   # M > 2 keeps 64-column blocks
     assert (p.tile_n, p.tile_cfg) == (64, 1)
     p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
     assert p.tile_cfg == 2
@@ -490,7 +498,7 @@ def test_planner_small_batch_wide_weights_stream():
 
     for M, N, K, cfg, s in ((32, 28672, 4096, 12, 4), (24, 28672, 8192, 12, 4),
                             (17, 28672, 8192, 12, 4), (64, 28672, 8192, 13, 4),
-                            (48, 14336, 4096, 13, 8), (64, 4096, 8192, 13, 16)):
+                            (48, 14336, 4096, 13, 8), (64, 4096, 16384, 13, 22)):
         p = _lib.plan(M, N, K, 128)
         rows = 32 if cfg == 12 else 64
         assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == cfg, (M, N, K)

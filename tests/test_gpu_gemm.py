@@ -208,6 +208,9 @@ def test_mfma_split_k(M, K, N, G):
     (9, 96, 260, 32), (16, 4096, 4096, 128), (17, 160, 7, 32), (32, 11008, 1028, 64),
     (33, 1024, 130, 32), (48, 4096, 516, 128), (64, 4096, 4100, 64), (1, 4096, 1000, 128),
     (5, 320, 33, 32), (24, 2048, 6150, 64), (4, 4096, 8194, 128),
+    # G = 32 (scales / zeros every k-step) on 16 single-batch waves and on the
+    # 4-wave loop, as the planner now picks for K <= 4096 and K <= 8192
+    (48, 4096, 4100, 32), (20, 8192, 1030, 32),
 ])
 def test_skinny_path(M, K, N, G):
     """Skinny-M MFMA kernel (16x16x32) over ragged M (1..64), any N, K % 64 != 0,

@@ -211,11 +211,21 @@ bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus);
 // K = N = 4096: 7.7 vs 12.1 us; M = 3, K = 14336, N = 4096: 17.2 vs 20.8 us;
 // M = 4, K = 4096, N = 6144: 9.7 vs 11.5 us) and from M = 5 on wider weights
 // (M = 5, K = 4096, N = 28672: 29.7 vs 32.6 us).  At M <= 4 on wider weights
-// the GEMV is faster where the skinny kernel loops over K (M = 4, K = 8192,
-// N = 28672: 47 vs 75 us), not where its 64-column blocks take K in one batch
-// per wave (K <= 4096; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us; G = 64 /
-// 32: 17.8 / 20.2 vs 21.9 / 22.3; N = 37888, G = 64 / 32: 23.5 / 27.3 vs
-// 30.1 / 30.7).
+// the skinny kernel's 64-column blocks win at any K where they apply
+// (skinny_quad; M = 3, K = 4096, N = 28672: 18.3 vs 22.0 us; G = 64 / 32:
+// 17.8 / 20.2 vs 21.9 / 22.3; N = 37888, G = 64 / 32: 23.5 / 27.3 vs 30.1 /
+// 30.7; K = 5120 / 6144 / 8192, N = 27648 / 28672 / 28672: 21.1 / 24.8 /
+// 30.8 vs 26.0 / 33.8 / 43.4; K = 8192, N = 16896 26.1 vs 40.0; G = 64,
+// K = 8192, N = 28672 33.7 vs 44.6), else the GEMV (its 32-column blocks:
+// G = 32, K = 5120, N = 27648: 30.7 vs 25.9).  Few column blocks with long K
+// take the GEMV split along K: where 16-column blocks would give at most a
+// quarter of the CUs one (N <= 1024 on MI355X) from K = 8192, at most half
+// (N <= 2048) from K = 16384 at M <= 4 (M = 3 / 4 / 5 / 6 / 8, K = 16384,
+// N = 1024: 8.9 / 9.4 / 11.9 / 12.7 / 14.0 vs 14.7 / 14.7 / 14.7 / 15.0 /
+// 16.1 us; K = 8192, M = 3 / 6: 7.8 / 8.6 vs 8.8 / 9.2, M = 8 9.5 vs 10.0 the
+// other way; N = 2048, K = 16384, M = 3 / 4: 11.4 / 12.4 vs 14.9 / 15.0, M = 5
+// 15.0 vs 16.1 the other way; G = 32 / 64, M = 4, N = 2048: 12.6 / 12.4 vs
+// 21.9 / 17.9).
 // M <= 2, K > 2048: the skinny kernel (MFMA dots, one batch per wave up to
 // K = 4096) where the GEMV's blocks fit the CUs badly (measured on MI355X, µs,
 // against the GEMV's plan):
@@ -226,7 +236,9 @@ bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus);
 //     6.61 -> 6.02 / 6.17 / 6.29; K = 3584, N = 6144 6.35 -> 6.05; M = 2,
 //     K = 4096, N = 6144 / 8192 7.52 / 7.79 -> 6.33 / 6.50, K = 5120 9.51 ->
 //     8.56, K = 8192 a tie (M = 1, K = 5120 .. 13824: the GEMV's blocks 5-15 %
-//     faster; K = 2048 slower: 4.06 -> 4.41).  Smaller groups, N = 6144:
+//     faster; 1024 < K <= 2048 slower: 4.06 -> 4.41; K <= 1024 faster:
+//     K = 1024, N = 5120 / 8192 3.97 / 3.94 -> 3.51 / 3.51, M = 2 4.60 /
+//     4.66 -> 3.61 / 3.68).  Smaller groups, N = 6144:
 //     M = 2, K = 3584 / 4096, G = 64: 7.57 / 7.57 -> 6.43 / 6.50, G = 32:
 //     7.66 / 7.68 -> 6.78 / 6.81; M = 1 G = 64 6.43 / 6.50 -> 6.22 / 6.37,
 //     G = 32 a tie; K = 5120 the GEMV's (M = 2, G = 64: 9.63 vs 10.17);
@@ -238,17 +250,27 @@ bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus);
 //     (M = 1, K = 3584 / 4096, N = 37888: 21.7 / 22.5 -> 20.9 / 21.3; M = 2,
 //     K = 4096 22.7 -> 21.8; from N = 65536 the GEMV's 256-column blocks fill
 //     the CUs; G = 64 a tie, G = 32 the GEMV's: K = 4096, N = 11008 8.54
-//     vs 9.67).
+//     vs 9.67);
+//   * K <= 2048 outside the 32-column band: every workgroup's single batch
+//     is short, and the skinny kernel's 16- / 64-column blocks beat the
+//     GEMV's (M = 1, K = 2048, N = 2048 / 4096 / 16384 / 28672: 3.92 / 4.00 /
+//     6.61 / 10.28 -> 3.60 / 3.70 / 5.75 / 8.70; M = 2 4.50 / 4.63 / 6.70 /
+//     10.34 -> 3.78 / 3.94 / 5.85 / 8.87; K = 1024 20-35 % faster; G = 64
+//     alike; G = 32 only on 16-column blocks: M = 2, N = 4096 4.66 -> 4.17,
+//     64-column blocks a tie).
 bool decode_takes_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (!skinny_applicable(M, G)) return false;
+  const int64_t b16 = (N + 15) / 16;
   if (M <= 2) {
-    if (K <= 2048) return false;
-    const bool wide32 = N % 2 == 0 && (N + 15) / 16 > cus && (N + 31) / 32 <= cus;
-    if (wide32) return K <= (M == 2 && G % 128 == 0 ? 8192 : 4096);
+    const bool wide32 = N % 2 == 0 && b16 > cus && (N + 31) / 32 <= cus;
+    if (wide32) return K <= 1024 || (K > 2048 && K <= (M == 2 && G % 128 == 0 ? 8192 : 4096));
+    if (K <= 2048) return b16 <= cus || G % 64 == 0;
     return K <= 4096 && G % 128 == 0 && skinny_quad(M, N, K, G, cus) &&
            (gemv_band64(M, N, K, cus) || ((N + 127) / 128 > cus && (N + 255) / 256 < cus));
   }
-  return M <= kGemvMaxM && (N <= 16384 || M >= 5 || (K <= 4096 && skinny_quad(M, N, K, G, cus)));
+  if (M > kGemvMaxM) return false;
+  if ((K >= 8192 && b16 * 4 <= cus) || (K >= 16384 && M <= 4 && b16 * 2 <= cus)) return false;
+  return N <= 16384 || M >= 5 || skinny_quad(M, N, K, G, cus);
 }
 
 // Small batches (4 <= M <= 64) on large enough weights: the streamed prefill
@@ -348,6 +370,18 @@ bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
 // CUs, else 64 columns up to two rounds (K <= 4096, one batch per wave); with
 // longer K (the 4-wave loop) only two row groups on one round, 64-column
 // blocks from M = 24 (a 17th row alone costs a second weight pass there).
+// Three or four row groups with K > 4096 (G = 128) where their blocks fit one
+// round: K = 5120 / 8192 / 16384, N = 2048, M = 48 / 64 on 32-column blocks:
+// 10.5 / 13.7 / 23.1 and 9.8 / 13.1 / 23.0 vs 15.1 / 18.3 / 25.5 and 15.3 /
+// 18.4 / 25.9 on the streamed tiles (M = 33: 13.3 vs 16.8 at K = 8192);
+// N = 4096 / 5120, K = 5120 / 8192 on 64-column blocks: M = 48 14.3 / 14.7 /
+// 18.5 / 18.7 vs 17.6 / 19.0 / 21.8 / 24.6 (64-column blocks at K = 16384 and
+// two rounds slower, as with two groups).  With K <= 4096 the 64-column
+// blocks may take more rounds the shorter K is: K = 2048, M = 40 / 48 / 64,
+// N = 11008 / 16384 (516-1024 workgroups): 12.1 / 15.4, 12.8 / 15.8, 12.3 /
+// 15.4 vs 16.0 / 18.7, 16.7 / 19.8, 17.8 / 21.3; not N = 28672 (1344-1792:
+// 22.3-24.9 vs 21.7-23.7), nor K = 4096 beyond two rounds (M = 48 / 64,
+// N = 11008: 24.3 / 23.9 vs 22.5 / 22.5).
 // Returns the skinny cfg (2 or 3) and rows per workgroup, or cfg -1 for the
 // whole-rows plans.  Measured on MI355X against the
 // automatic plan before it (µs, G = 128): K = 4096, N = 4096, M = 24 / 32 /
@@ -397,11 +431,12 @@ SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus
   const int64_t wg2 = (N + 31) / 32 * g, wg3 = (N + 63) / 64 * g;
   if (K <= 4096) {
     if (c2 && wg2 <= cus) return {2, 16};
-    if (c3 && wg3 <= (G % 64 == 0 ? 2 : 1) * (int64_t)cus) return {3, 16};
+    // 64-column blocks over as many rounds as keep rounds x K within 8192
+    // (4096 at G = 32): a round's workgroups are short at small K
+    if (c3 && wg3 * K <= (G % 64 == 0 ? 8192 : 4096) * (int64_t)cus) return {3, 16};
     return {-1, 0};
   }
-  if (g != 2) return {-1, 0};
-  if (c2 && wg2 <= cus && K <= (g128 ? 16384 : 8192)) return {2, 16};
+  if (c2 && wg2 <= cus && K <= (g128 ? 16384 : 8192) && (g == 2 || g128)) return {2, 16};
   if (c3 && g128 && M >= 24 && wg3 <= cus && K <= 8192) return {3, 16};
   return {-1, 0};
 }
