@@ -606,10 +606,24 @@ def test_planner_prefill_split_k():
     p = _lib.plan(64, 37888, 3584, 128)
     assert (p.tile_cfg, p.split_k, p.grid_x) == (13, 3, 444)
     # a forced split that two k-slices (8-step units) cannot honour: cfg 11
-    p = _lib.plan(256, 1028, 2048, 64, _lib.KERNEL_MFMA, 3)
+    p = _lib.plan(512, 1028, 2048, 64, _lib.KERNEL_MFMA, 3)
     assert (p.tile_cfg, p.split_k) == (11, 3)
-    p = _lib.plan(256, 1028, 2048, 64, _lib.KERNEL_MFMA, 2)
+    p = _lib.plan(512, 1028, 2048, 64, _lib.KERNEL_MFMA, 2)
     assert (p.tile_cfg, p.split_k) == (14, 2)
+    # 64 < M <= 256 on small layers: 64-row tiles (cfg 13) where cfg 14's
+    # slices would hold <= 4 k-steps, split for ~a workgroup per CU ...
+    for M, N, K, split in ((96, 4096, 4096, 8), (192, 4096, 4096, 4), (256, 4096, 4096, 4),
+                           (128, 4096, 2048, 4)):
+        p = _lib.plan(M, N, K, 128)
+        assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
+        assert p.grid_x == split * (N // 256) * ((M + 63) // 64)
+    # ... or unsplit with K <= 2048 where the tiles give half the CUs one each
+    for M in (128, 192, 256):
+        p = _lib.plan(M, 16384, 2048, 128)
+        assert (p.tile_cfg, p.split_k, p.workspace_bytes) == (13, 1, 0), M
+    # ... not with longer slices, nor beyond M = 256
+    for M, N, K in ((96, 14336, 4096), (128, 4096, 14336), (128, 8192, 8192), (384, 4096, 4096)):
+        assert _lib.plan(M, N, K, 128).tile_cfg == 14, (M, N, K)
     # more tiles than CUs: cfg 11
     p = _lib.plan(1024, 14336, 4096, 128)
     assert (p.tile_cfg, p.split_k) == (11, 1)

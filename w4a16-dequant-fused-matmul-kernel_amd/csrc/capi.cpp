@@ -480,6 +480,29 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     int64_t s = cus / t6;
     if (s > K / 512) s = K / 512;
     if (s < 1) s = 1;
+    // 64 < M <= 256 on small layers: the 64-row streamed tiles (cfg 13, one
+    // k-slice) instead, where the two-slice split would leave each slice at
+    // most 4 k-steps (K / s <= 512; then split for about a workgroup per CU,
+    // >= 8 k-steps each), or, with K <= 2048, unsplit where their tiles give
+    // half the CUs one each (no partials, no reduction pass).  Measured on
+    // MI355X against cfg 14's plan (µs, G = 128): K = N = 4096, M = 96 / 128 /
+    // 192 / 256: 22.3 / 24.2 / 28.8 / 29.2 -> 19.4 / 21.3 / 24.6 / 26.4;
+    // K = 2048, N = 4096, M = 96 / 128 / 192: 18.0 / 19.7 / 22.2 -> 14.5 /
+    // 16.0 / 18.8; K = 2048, N = 16384, M = 96 / 128 / 192 / 256: 25.9 / 27.4
+    // / 30.9 / 33.9 -> 24.7 / 26.5 / 25.7 / 26.0.  Longer slices keep cfg 14
+    // (K = 4096, N = 14336, M = 96 / 128: 28.0 / 30.3 vs 28.3 / 30.2 at best;
+    // K = 14336, N = 4096 and K = N = 8192 ties or slower; unsplit at K = 4096
+    // 47 us at every M).
+    if (M <= 256 && s > 1) {
+      const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
+      if (K <= 2048 && 2 * t13 >= cus) return {13, 1};
+      if (K / s <= 512) {
+        int64_t s13 = cus / t13;
+        if (s13 > K / 512) s13 = K / 512;
+        if (s13 < 1) s13 = 1;
+        return {13, s13 > 1 ? stream_splits((int)K, (int)s13) : 1};
+      }
+    }
     return {14, s > 1 ? stream_splits((int)K, (int)s, 2) : 1};
   }
   if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
