@@ -352,9 +352,16 @@ FLOOR_SHAPES = [("C2", "C2", 4096, 4096), ("C3 N=28672", "C3", 4096, 28672),
 FLOOR_ROWS = [(64, 16, 2), (64, 8, 4), (128, 16, 2), (256, 8, 4), (256, 16, 2), (512, 8, 4),
               (512, 16, 2)]
 FLOOR_LINEAR = [(256, 8, 4), (512, 8, 4), (1024, 4, 8)]
+# tiles (K split across workgroups): (column-block bytes, k-ranges); each with
+# mode 0 (partials stored, no cross-workgroup step), 1 (in-kernel reduction over
+# device-coherent stores / loads and a counter) and 2 (the same chain through
+# the L2 alone; timing only).  Kept where they give 256 or 512 workgroups.
+FLOOR_TILES = [(128, 2), (256, 4), (512, 8), (256, 2), (512, 4), (256, 8), (512, 2)]
+TILE_MODES = {0: "partials stored, no reduction", 1: "in-kernel reduction, device-coherent",
+              2: "in-kernel reduction through L2 only (timing only)"}
 
 
-def floor_probe(steps: int) -> str:
+def floor_probe(steps: int, only: tuple[str, ...] | None = None) -> str:
     """Markdown table: µs per call and GB/s of packed-weight bytes for the
     loads-only probe's row shapes (a GEMV column block of 64 / 128 / 256 / 512
     bytes, i.e. 16 / 32 / 64 / 128 columns) and linear reads of the same bytes, cold like
@@ -374,8 +381,11 @@ def floor_probe(steps: int) -> str:
     lib.w4a16_probe_rows_out_words.argtypes = [i32, i32, i32]
     lib.w4a16_probe_linear_out_words.restype = ctypes.c_int64
     lib.w4a16_probe_linear_out_words.argtypes = [i32, i32]
+    lib.w4a16_probe_tiles.argtypes = [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp]
     rows = ["| shape | packed weights | access | µs | GB/s |", "|---|---|---|---|---|"]
     for label, cfg, K, N in FLOOR_SHAPES:
+        if only and label not in only:
+            continue
         KP, row_bytes = K // 8, N * 4
         nbytes = KP * row_bytes
         ncopy = max(2, -(-COLD_BYTES // nbytes) + 1)
@@ -410,6 +420,40 @@ def floor_probe(steps: int) -> str:
                 if rc:
                     raise RuntimeError(f"w4a16_probe_linear: {rc}")
             shapes.append((f"linear: {nwg} workgroups of {waves} waves, {br} loads/lane", launch))
+        for cwb, ns in FLOOR_TILES:
+            nwg = row_bytes // cwb * ns
+            if row_bytes % cwb or KP % ns or nwg not in (256, 512):
+                continue
+            words = nwg * cwb // 4
+            part = torch.empty(words, dtype=torch.float32, device="cuda")
+            out = torch.empty(words, dtype=torch.float32, device="cuda")
+            cnt = torch.zeros(row_bytes // cwb, dtype=torch.int32, device="cuda")
+            # mode 1's in-kernel sums against the host's sum (range order, fp32)
+            # of the mode-0 partials of the same weights
+            st = torch.cuda.current_stream().cuda_stream
+            rc = lib.w4a16_probe_tiles(bufs[0].data_ptr(), KP, row_bytes, cwb, 8, 4, ns, 0,
+                                       part.data_ptr(), cnt.data_ptr(), out.data_ptr(), st)
+            p0 = out.view(-1, ns, cwb // 4).cpu()
+            want = p0[:, 0, :].clone()
+            for k in range(1, ns):
+                want += p0[:, k, :]
+            rc = rc or lib.w4a16_probe_tiles(bufs[0].data_ptr(), KP, row_bytes, cwb, 8, 4, ns, 1,
+                                             part.data_ptr(), cnt.data_ptr(), out.data_ptr(), st)
+            if rc:
+                raise RuntimeError(f"w4a16_probe_tiles: {rc}")
+            got = out[: want.numel()].view_as(want).cpu()
+            same = bool(torch.equal(got, want)) and int(cnt.abs().sum()) == 0
+            for mode, what in TILE_MODES.items():
+                if mode == 1:
+                    what += ", sums " + ("equal to the host's" if same else "DIFFER from the host's")
+                def launch(b, cwb=cwb, ns=ns, mode=mode, part=part, out=out, cnt=cnt):
+                    rc = lib.w4a16_probe_tiles(b.data_ptr(), KP, row_bytes, cwb, 8, 4, ns, mode,
+                                               part.data_ptr(), cnt.data_ptr(), out.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream)
+                    if rc:
+                        raise RuntimeError(f"w4a16_probe_tiles: {rc}")
+                shapes.append((f"tiles: {cwb // 4}-column blocks x {ns} k-ranges ({nwg} "
+                               f"workgroups), 8 waves, 4 rows/lane/batch; {what}", launch))
         for what, launch in shapes:
             us = timed(launch)
             rows.append(f"| {label} | {nbytes / 2**20:.1f} MiB | {what} | {us:.2f} | "

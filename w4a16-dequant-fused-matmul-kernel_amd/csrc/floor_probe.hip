@@ -89,6 +89,106 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(const uint8_t* __res
   out[(size_t)blockIdx.x * blockDim.x + tid] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
 
+// tiles: workgroup -> (column block cb of CWB bytes, k-range ks of S equal
+// ranges), placed like the GEMV's blocks (consecutive (cb, ks) on one XCD); the
+// loads are rows_kernel's over the range's KP / S rows.  Each lane's xor, read
+// as four floats (one per column of its 16 bytes), is summed over the
+// workgroup's row-lanes in LDS into one float per column: the workgroup's
+// partial.  MODE 0: the partial is stored to out[(cb * S + ks) * CW + c] (the
+// access shape alone, no cross-workgroup step).  MODE 1: the k-ranges are summed
+// inside the kernel without a fence: device-coherent partial stores (sc1), a
+// wait for their completion, one device-scope atomic add on the column block's
+// counter; the workgroup that arrives last loads the S partials with
+// device-coherent loads, sums them in range order, stores the block's result to
+// out[cb * CW + c] and resets the counter to zero for the next call (the
+// counters start at zero).  MODE 2: as MODE 1 with plain stores and loads: the
+// cost of the same chain through the L2 alone, which is only coherent when the
+// S workgroups of a block share an XCD (timing only; its sums are not checked).
+template <int CWB, int WAVES, int BR, int MODE>
+__global__ __launch_bounds__(64 * WAVES) void tiles_kernel(const uint8_t* __restrict__ w, int KP,
+                                                           int row_bytes, int S,
+                                                           float* __restrict__ part,
+                                                           uint32_t* __restrict__ cnt,
+                                                           float* __restrict__ out) {
+  constexpr int LPR = CWB / 16;            // lanes per row segment
+  constexpr int RW = 64 / LPR;             // row-lanes per wave
+  constexpr int RL = WAVES * RW;           // row-lanes per workgroup
+  constexpr int CW = CWB / 4;              // columns per block
+  __shared__ float red[RL][CW];
+  __shared__ uint32_t last;
+  const int nb = (int)gridDim.x;
+  int lin = (int)blockIdx.x;
+  if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
+  const int cb = lin / S, ks = lin - cb * S;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rl = wave * RW + lane / LPR;
+  const uint32_t col = (uint32_t)cb * CWB + (uint32_t)(lane % LPR) * 16u;
+  const int rows = KP / S, rb = ks * rows;
+  const __amdgpu_buffer_rsrc_t r = rsrc(w, (uint32_t)KP * (uint32_t)row_bytes);
+  const int nbat = (rows + BR * RL - 1) / (BR * RL);
+  u32x4 a[BR], b[BR];
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  auto load = [&](int bi, u32x4(&d)[BR]) {
+#pragma unroll
+    for (int i = 0; i < BR; ++i) {
+      const int row = (bi * BR + i) * RL + rl;
+      d[i] = load16(r, row < rows ? (uint32_t)(rb + row) * (uint32_t)row_bytes + col : kOob);
+    }
+  };
+  load(0, a);
+  for (int bi = 0; bi < nbat; bi += 2) {
+    load(bi + 1, b);
+#pragma unroll
+    for (int i = 0; i < BR; ++i) acc ^= a[i];
+    if (bi + 1 >= nbat) break;
+    load(bi + 2, a);
+#pragma unroll
+    for (int i = 0; i < BR; ++i) acc ^= b[i];
+  }
+  // finite floats whatever the bits: keep the mantissa, fix the exponent
+  const int c0 = 4 * (lane % LPR);
+  red[rl][c0 + 0] = __uint_as_float((acc.x & 0x007FFFFFu) | 0x3F800000u);
+  red[rl][c0 + 1] = __uint_as_float((acc.y & 0x007FFFFFu) | 0x3F800000u);
+  red[rl][c0 + 2] = __uint_as_float((acc.z & 0x007FFFFFu) | 0x3F800000u);
+  red[rl][c0 + 3] = __uint_as_float((acc.w & 0x007FFFFFu) | 0x3F800000u);
+  __syncthreads();
+  float v = 0.0f;
+  if (tid < CW)
+    for (int i = 0; i < RL; ++i) v += red[i][tid];
+  if constexpr (MODE == 0) {
+    if (tid < CW) out[(size_t)lin * CW + tid] = v;
+    return;
+  } else {
+    if (tid < CW) {
+      if constexpr (MODE == 1)
+        __hip_atomic_store(&part[(size_t)lin * CW + tid], v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      else
+        part[(size_t)lin * CW + tid] = v;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(&cnt[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(S - 1);
+    __syncthreads();
+    if (last) {
+      if (tid < CW) {
+        float s = 0.0f;
+        for (int k = 0; k < S; ++k) {
+          const float* p = &part[((size_t)cb * S + k) * CW + tid];
+          if constexpr (MODE == 1)
+            s += __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            s += *p;
+        }
+        out[(size_t)cb * CW + tid] = s;
+      }
+      if (tid == 0) __hip_atomic_store(&cnt[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 template <int CWB, int WAVES, int BR>
 int launch_rows(const void* w, int KP, int row_bytes, uint32_t* out, hipStream_t st) {
   hipLaunchKernelGGL((rows_kernel<CWB, WAVES, BR>), dim3(row_bytes / CWB), dim3(64 * WAVES), 0, st,
@@ -122,6 +222,38 @@ int w4a16_probe_rows(const void* w, int KP, int row_bytes, int cwb, int waves, i
   if (cwb == 256 && waves == 16 && br == 2) return launch_rows<256, 16, 2>(w, KP, row_bytes, out, st);
   if (cwb == 512 && waves == 8 && br == 4) return launch_rows<512, 8, 4>(w, KP, row_bytes, out, st);
   if (cwb == 512 && waves == 16 && br == 2) return launch_rows<512, 16, 2>(w, KP, row_bytes, out, st);
+  return -1;
+}
+
+// tiles: (cwb, waves, br) in {(128, 8, 4), (256, 8, 4), (512, 8, 4)}, mode 0 / 1 / 2;
+// row_bytes % cwb == 0, KP % s == 0, KP * row_bytes < 2 GiB.  `part` holds
+// (row_bytes / cwb) * s * cwb / 4 floats, `cnt` row_bytes / cwb zeroed words
+// (left zeroed by every mode-1/2 call), `out` as many floats as `part`.
+int w4a16_probe_tiles(const void* w, int KP, int row_bytes, int cwb, int waves, int br, int s,
+                      int mode, float* part, uint32_t* cnt, float* out, hipStream_t st) {
+  if (KP <= 0 || row_bytes <= 0 || cwb <= 0 || row_bytes % cwb != 0 || s <= 0 || KP % s != 0 ||
+      (int64_t)KP * row_bytes >= ((int64_t)1 << 31) || waves != 8 || br != 4 || mode < 0 ||
+      mode > 2)
+    return -1;
+  const dim3 grid((unsigned)(row_bytes / cwb * s)), block(512);
+  const uint8_t* wp = static_cast<const uint8_t*>(w);
+#define W4A16_PROBE_TILES(CWB)                                                                   \
+  if (cwb == CWB) {                                                                              \
+    if (mode == 0)                                                                               \
+      hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 0>), grid, block, 0, st, wp, KP, row_bytes, s, \
+                         part, cnt, out);                                                        \
+    else if (mode == 1)                                                                          \
+      hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 1>), grid, block, 0, st, wp, KP, row_bytes, s, \
+                         part, cnt, out);                                                        \
+    else                                                                                         \
+      hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 2>), grid, block, 0, st, wp, KP, row_bytes, s, \
+                         part, cnt, out);                                                        \
+    return (int)hipGetLastError();                                                               \
+  }
+  W4A16_PROBE_TILES(128)
+  W4A16_PROBE_TILES(256)
+  W4A16_PROBE_TILES(512)
+#undef W4A16_PROBE_TILES
   return -1;
 }
 
