@@ -469,52 +469,35 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 // read by the whole workgroup at once, and the rows a lane processes first are
 // the ones the memory system returns first: the dequant and dot products of
 // the first slots overlap the arrival of the later ones instead of waiting
-// for the lane's whole run (measured on MI355X, C2: 4.81-4.85 -> 4.48-4.57 us
-// with 16 waves and two slots per lane).  Each slot has its own group, so its
-// scale and zero loads are its own.  Slots past `re` load nothing (out-of-range
-// offsets read zeros: a zero activation makes their products exactly zero),
-// so every lane runs the same loads and the same trip count without a branch.
-// Arguments of gemv_direct_kernel: everything the loads need comes first (one
-// batch of scalar loads), the epilogue's arguments follow; the grid size is an
-// argument rather than a read of the dispatch's hidden arguments.
-struct DirectArgs {
-  const f16* X;
-  const uint32_t* QW;
-  const uint16_t* SC;
-  const uint16_t* ZR;
-  int N, K, ldx, rows_per_wg;
-  int nblk, nb;               // column blocks, workgroups (nblk * splits)
-  uint32_t gmagic, bmagic;    // k / G and block / nblk by reciprocal (group_div)
-  int gshift, bshift;
-  // epilogue
-  int S, ldy;
-  const f16* bias;
-  f16* Y;
-  float* part;
-};
-
-// M <= 2 with the activations read directly (no LDS staging): the rows of a
-// workgroup's k-range [rb, re) are dealt to its RL row-lanes in sweeps -- slot
-// j of row-lane rl is packed row rb + j * RL + rl -- and a batch is BR
-// consecutive slots.  So every batch is one contiguous run of BR * RL rows
-// read by the whole workgroup at once, and the rows a lane processes first are
-// the ones the memory system returns first: the dequant and dot products of
-// the first slots overlap the arrival of the later ones instead of waiting
 // for the lane's whole run.  Each slot has its own group, so its scale and
 // zero loads are its own.  Slots past `re` load nothing (out-of-range offsets
 // read zeros: a zero activation makes their products exactly zero), so every
 // lane runs the same loads and the same trip count without a branch.
 //
 // The time to the first weight load is on the critical path of a few-us call
-// (every wave waits for its own), so the set-up is kept short: one batch of
-// argument loads, the column block and k-split from the block index by
-// reciprocal instead of division and without branches, and each slot's
-// loads issued together, weight first (the long pole: cold HBM, most of the
-// bytes).  Measured on MI355X, C2 (16 waves, two slots per lane, one batch),
-// medians of 7 interleaved runs: 4.81-4.85 us with contiguous runs per lane,
-// 4.68-4.70 with sweeps.
-template <int MT, int CWL, int WAVES, bool ONE_BATCH>
-__global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArgs args) {
+// (every wave waits for its own), so the set-up is kept short: the library is
+// built to have the dispatch preload a kernel's leading arguments into SGPRs
+// (-mllvm -amdgpu-kernarg-preload-count; fourteen SGPRs here), and the two
+// entry points below order the arguments so that those SGPRs hold everything
+// the first batch's loads need -- the first weight load then waits for no
+// kernel-argument load at all, and the later arguments are loaded while the
+// weights are in flight (measured on MI355X, C2: 4.69 -> 4.49 us against one
+// batch of argument loads in front of everything).  Unsplit launches
+// (gemv_direct_kernel) preload the operand pointers, N, K, the rows per
+// workgroup, the grid size and the group reciprocal; split launches
+// (gemv_direct_split_kernel) need the reciprocal of the column-block count
+// too (block -> k-split, column block), and take X among the later
+// arguments: its first load comes after the first slot's weight, scale and
+// zero loads.  Each slot's loads are issued together, weight first (the long
+// pole: cold HBM, most of the bytes).  Measured on MI355X, C2 (16 waves, two
+// slots per lane, one batch), medians of 7 interleaved runs: 4.81-4.85 us
+// with contiguous runs per lane, 4.68-4.70 with sweeps.
+template <int MT, int CWL, int WAVES, bool ONE_BATCH, bool SPLIT>
+__device__ __forceinline__ void gemv_direct_body(
+    const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
+    const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
+    int nb, uint32_t gmagic, int gshift, uint32_t bmagic, int bshift, int ldx, int ldy,
+    const f16* __restrict__ bias, f16* __restrict__ Y, float* __restrict__ part) {
   static_assert(MT <= 2, "direct activations are for M <= 2");
   constexpr int BR = GemvShape<WAVES>::kBatch;
   // 32-column and wider blocks: the CWL / 4 lane quads of a packed row each
@@ -530,31 +513,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
   constexpr int CW = 4 * CWL;              // columns per workgroup
   __shared__ float red[WAVES][MT][CW];
 
-  const f16* __restrict__ X = args.X;
-  const uint32_t* __restrict__ QW = args.QW;
-  const uint16_t* __restrict__ SC = args.SC;
-  const uint16_t* __restrict__ ZR = args.ZR;
-  const int N = args.N, K = args.K, ldx = args.ldx, rows_per_wg = args.rows_per_wg;
-  const int nblk = args.nblk, nb = args.nb;
-  const uint32_t gmagic = args.gmagic, bmagic = args.bmagic;
-  const int gshift = args.gshift, bshift = args.bshift;
-  const int S = args.S, ldy = args.ldy;
-  const f16* __restrict__ bias = args.bias;
-  f16* __restrict__ Y = args.Y;
-  float* __restrict__ part = args.part;
-  // every argument in one batch of scalar loads, before anything else: left
-  // to itself the compiler split them into dependent rounds (one more
-  // kernel-argument round trip in front of the first weight load) or loaded
-  // the output pointer after the reduction's barrier
-  asm volatile("" ::"s"(X), "s"(QW), "s"(SC), "s"(ZR), "s"(N), "s"(K), "s"(ldx),
-               "s"(rows_per_wg), "s"(nblk), "s"(nb), "s"(gmagic), "s"(bmagic), "s"(gshift),
-               "s"(bshift), "s"(S), "s"(ldy), "s"(bias), "s"(Y), "s"(part));
-
   // XCD-aware block order (gemv_kernel), then block -> (k-split, column block)
   const int b0 = (int)blockIdx.x;
   const int lin = (nb & 7) == 0 ? (b0 & 7) * (nb >> 3) + (b0 >> 3) : b0;
-  const int sk = (int)((__umulhi((uint32_t)lin, bmagic) + (uint32_t)lin) >> bshift);
+  const int nblk = (N + CW - 1) / CW;
+  // split launches (nb = nblk * splits): lin = sk * nblk + cb
+  const int sk = SPLIT ? (int)((__umulhi((uint32_t)lin, bmagic) + (uint32_t)lin) >> bshift) : 0;
   const int cb = lin - sk * nblk;
+  constexpr int S = SPLIT ? 2 : 1;   // the epilogue only asks whether the launch is split
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -681,6 +647,32 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(const DirectArg
   gemv_reduce_store<MT, CWL, WAVES>(acc, red, tid, cb, sk, S, N, ldy, bias, Y, part);
 }
 
+// Unsplit launches: the first fourteen SGPRs of arguments (preloaded) are what
+// the first batch's loads need.
+template <int MT, int CWL, int WAVES, bool ONE_BATCH>
+__global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(
+    const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
+    const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
+    int nb, uint32_t gmagic, int gshift, int ldx, int ldy, const f16* __restrict__ bias,
+    f16* __restrict__ Y) {
+  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, false>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
+                                                     gmagic, gshift, 0u, 0, ldx, ldy, bias, Y,
+                                                     nullptr);
+}
+
+// Split launches: the block reciprocal joins the preloaded arguments, X
+// follows them.
+template <int MT, int CWL, int WAVES, bool ONE_BATCH>
+__global__ __launch_bounds__(64 * WAVES) void gemv_direct_split_kernel(
+    const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
+    const uint16_t* __restrict__ ZR, int N, int K, int rows_per_wg, int nb, uint32_t bmagic,
+    int bshift, uint32_t gmagic, int gshift, const f16* __restrict__ X, int ldx,
+    float* __restrict__ part) {
+  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, true>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
+                                                    gmagic, gshift, bmagic, bshift, ldx, 0,
+                                                    nullptr, nullptr, part);
+}
+
 template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false, int QPL = 1>
 hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL * QPL;
@@ -691,30 +683,25 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   if constexpr (MT <= 2 && !STAGE) {
     // every split's rows fit one batch of BR slots per row-lane
     constexpr int kRowsPerBatch = GemvShape<WAVES>::kBatch * WAVES * (64 / CWL);
-    auto kern = rows <= kRowsPerBatch ? gemv_direct_kernel<MT, CWL, WAVES, true>
-                                      : gemv_direct_kernel<MT, CWL, WAVES, false>;
-    const GroupDiv bd = group_div(nblk);
-    DirectArgs da{};
-    da.X = static_cast<const f16*>(a.x);
-    da.QW = reinterpret_cast<const uint32_t*>(a.qw);
-    da.SC = static_cast<const uint16_t*>(a.sc);
-    da.ZR = static_cast<const uint16_t*>(a.zr);
-    da.N = a.N;
-    da.K = a.K;
-    da.ldx = a.ldx;
-    da.rows_per_wg = rows;
-    da.nblk = nblk;
-    da.nb = nblk * split;
-    da.gmagic = gd.magic;
-    da.bmagic = bd.magic;
-    da.gshift = gd.shift;
-    da.bshift = bd.shift;
-    da.S = split;
-    da.ldy = a.ldy;
-    da.bias = static_cast<const f16*>(a.bias);
-    da.Y = static_cast<f16*>(a.y);
-    da.part = part;
-    hipLaunchKernelGGL(kern, dim3(nblk * split), dim3(GemvShape<WAVES>::kThreads), 0, st, da);
+    const bool one = rows <= kRowsPerBatch;
+    const dim3 grid(nblk * split), block(GemvShape<WAVES>::kThreads);
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(a.qw);
+    const uint16_t* sc = static_cast<const uint16_t*>(a.sc);
+    const uint16_t* zr = static_cast<const uint16_t*>(a.zr);
+    const f16* x = static_cast<const f16*>(a.x);
+    if (split == 1) {
+      auto kern = one ? gemv_direct_kernel<MT, CWL, WAVES, true>
+                      : gemv_direct_kernel<MT, CWL, WAVES, false>;
+      hipLaunchKernelGGL(kern, grid, block, 0, st, qw, sc, zr, x, a.N, a.K, rows, nblk, gd.magic,
+                         gd.shift, a.ldx, a.ldy, static_cast<const f16*>(a.bias),
+                         static_cast<f16*>(a.y));
+    } else {
+      auto kern = one ? gemv_direct_split_kernel<MT, CWL, WAVES, true>
+                      : gemv_direct_split_kernel<MT, CWL, WAVES, false>;
+      const GroupDiv bd = group_div(nblk);
+      hipLaunchKernelGGL(kern, grid, block, 0, st, qw, sc, zr, a.N, a.K, rows, nblk * split,
+                         bd.magic, bd.shift, gd.magic, gd.shift, x, a.ldx, part);
+    }
   } else
     hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF, QPL>), dim3(nblk * split),
                        dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),

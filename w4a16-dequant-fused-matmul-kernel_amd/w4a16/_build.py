@@ -33,7 +33,8 @@ ARCH = "gfx950"
 
 def source_hash() -> str:
     """sha256 over the names and contents of every file the library is built
-    from (the csrc sources and headers, and the public header).  Compiled into
+    from (the csrc sources and headers, and the public header) and over the
+    compiler flags.  Compiled into
     the library (w4a16_build_id) and compared by the loader, so a library
     built from other sources is refused rather than silently run."""
     h = hashlib.sha256()
@@ -43,6 +44,7 @@ def source_hash() -> str:
         with open(path, "rb") as f:
             data = f.read()
         h.update(name.encode() + b"\0" + len(data).to_bytes(8, "little") + data)
+    h.update(repr((COMMON_FLAGS, sorted(SOURCE_FLAGS.items()))).encode())
     return h.hexdigest()
 
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU ops.
@@ -55,6 +57,12 @@ COMMON_FLAGS = [
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per source: the decode GEMV's leading kernel arguments preloaded into SGPRs
+# by the dispatch (its first loads then wait for no kernel-argument load;
+# firmware without the feature runs the compiler's load prologue instead).
+SOURCE_FLAGS = {
+    "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+}
 
 
 def hipcc() -> str:
@@ -66,7 +74,8 @@ def hipcc() -> str:
 
 def _compile(src: str, verbose: bool, defines: list[str]) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *defines, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *defines, "-x", "hip", "-c",
+           os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
