@@ -57,16 +57,25 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // the lane's two adjacent columns come in one 8-byte word load and one 4-byte
 // scale / zero load each, and its activation fragment feeds both n-tiles, so a
 // CU streams X once for 32 columns instead of once per 16).
+//
+// Arguments: the first fourteen SGPRs' worth are what the first loads need
+// (operand pointers, M, N, K, G, the row groups, ldx); the library is built
+// to have the dispatch preload them into SGPRs (-mllvm
+// -amdgpu-kernarg-preload-count), so the first loads wait for no
+// kernel-argument load, and the epilogue's arguments are loaded meanwhile.
+// mgs_rpg = row groups per column block | rows per group << 16; the grid size
+// is nblk * mgs (no read of the dispatch packet).
 template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
-    const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
-    int N, int K, int G, int mgs, int rpg, int ldx, int ldy) {
+    const uint16_t* __restrict__ ZR, int M, int N, int K, int G, int mgs_rpg, int ldx, int ldy,
+    const f16* __restrict__ bias, f16* __restrict__ Y) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four columns per lane");
   constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][NT][64];
 
-  const int nb = (int)gridDim.x;
+  const int mgs = mgs_rpg & 0xFFFF, rpg = mgs_rpg >> 16;
+  const int nb = (N + 16 * NT - 1) / (16 * NT) * mgs;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
   // The workgroup owns rows [row0, row0 + rpg) of its column block: all of
@@ -304,9 +313,9 @@ hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
   const int waves = ks <= 4 * kBatch ? 4 : ks <= 8 * kBatch ? 8 : ks <= k16 * kBatch ? k16 : 4;
   hipLaunchKernelGGL(k, dim3(nblk * mgs), dim3(64 * waves), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
-                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr),
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), a.M, a.N, a.K,
-                     a.G, mgs, rpg, a.ldx, a.ldy);
+                     static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr), a.M,
+                     a.N, a.K, a.G, mgs | (rpg << 16), a.ldx, a.ldy,
+                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y));
   return hipGetLastError();
 }
 

@@ -159,12 +159,15 @@ __device__ __forceinline__ void gemv_sum_waves_store(float (&red)[WAVES][MT][4 *
   }
 }
 
+// Arguments: the first fourteen SGPRs' worth (preloaded by the dispatch, as for
+// gemv_direct_kernel) are what the first loads need; the grid size is
+// nblk * S, computed rather than read from the dispatch packet.
 template <int MT, int CWL, int WAVES, bool STAGE, bool MF, int QPL>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
-    const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
-    const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y,
-    float* __restrict__ part, int N, int K, int ldx, int ldy, uint32_t gmagic, int gshift,
-    int rows_per_wg, int S, int nblk) {
+    const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
+    const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
+    int S, uint32_t gmagic, int gshift, int ldx, int ldy, const f16* __restrict__ bias,
+    f16* __restrict__ Y, float* __restrict__ part) {
   constexpr int kThreads = GemvShape<WAVES>::kThreads;
   constexpr int BR = GemvShape<WAVES>::kBatch;
   constexpr int RH = BR < 4 ? BR : 4;      // rows per half (a half lies in one group)
@@ -212,18 +215,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   __shared__ uint4 xs[MT * XS];
   __shared__ float red[WAVES][MT][CW];
 
-  // 16-column blocks: every kernel argument in one batch of scalar loads up
-  // front (left to the compiler, the pointers are read only after the
-  // block-order branches, a second and third dependent kernarg round trip
-  // before the first weight load).  Measured on MI355X: C2 5.01 -> 4.86 us,
-  // M = 2 5.50 -> 5.29 us, but K = 14336 N = 4096 12.96 -> 13.24 us; the
-  // 32-column kernel measured 2-3 % slower with it, so it keeps the compiler's
-  // order.
-  const int nb = (int)gridDim.x;
-  if constexpr (CWL <= 4)
-    asm volatile("" ::"s"(X), "s"(QW), "s"(SC), "s"(ZR), "s"(bias), "s"(Y), "s"(part), "s"(N),
-                 "s"(K), "s"(ldx), "s"(ldy), "s"(gmagic), "s"(gshift), "s"(rows_per_wg), "s"(S),
-                 "s"(nblk), "s"(nb));
+  const int nblk = (N + CW - 1) / CW;
+  const int nb = nblk * S;
 
   // XCD-aware block order (see header comment).
   int lin = (int)blockIdx.x;
@@ -704,11 +697,11 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
     }
   } else
     hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF, QPL>), dim3(nblk * split),
-                       dim3(GemvShape<WAVES>::kThreads), 0, st, static_cast<const f16*>(a.x),
+                       dim3(GemvShape<WAVES>::kThreads), 0, st,
                        reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
-                       static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
-                       static_cast<f16*>(a.y), part, a.N, a.K, a.ldx, a.ldy, gd.magic, gd.shift,
-                       rows, split, nblk);
+                       static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.x), a.N, a.K,
+                       rows, split, gd.magic, gd.shift, a.ldx, a.ldy,
+                       static_cast<const f16*>(a.bias), static_cast<f16*>(a.y), part);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, split, st);

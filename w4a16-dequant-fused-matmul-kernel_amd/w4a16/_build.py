@@ -57,11 +57,14 @@ COMMON_FLAGS = [
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-# Per source: the decode GEMV's leading kernel arguments preloaded into SGPRs
-# by the dispatch (its first loads then wait for no kernel-argument load;
-# firmware without the feature runs the compiler's load prologue instead).
+# Per source: the decode kernels' leading kernel arguments preloaded into
+# SGPRs by the dispatch (their first loads then wait for no kernel-argument
+# load; firmware without the feature runs the compiler's load prologue
+# instead).
+_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 SOURCE_FLAGS = {
-    "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "gemv.hip": _PRELOAD,
+    "gemm_skinny.hip": _PRELOAD,
 }
 
 
