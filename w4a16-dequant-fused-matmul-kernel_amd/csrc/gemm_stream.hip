@@ -114,13 +114,20 @@ __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t 
 // kernel it avoids.  Both slices run the same number of steps (a slice's
 // steps past its range load zeros and add exactly 0), so every wave reaches
 // every barrier.
+//
+// Arguments: the first fourteen SGPRs' worth are what the prologue's
+// activation, weight and group computations need (X, QW, the tile and split
+// geometry, the grid size nb, SZ and the group reciprocal); the library is
+// built to have the dispatch preload them into SGPRs (-mllvm
+// -amdgpu-kernarg-preload-count), so those loads wait for no kernel-argument
+// load, and the rest are loaded meanwhile.  The grid size is an argument
+// rather than a read of the dispatch packet.
 template <int kMT, bool kSZ1, int kKS = 1>
 __global__ __launch_bounds__(kNT * kKS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
-                   const char* __restrict__ SZ, uint32_t sc_off, uint32_t zr_off,
-                   uint32_t sz_bytes, const f16* __restrict__ bias, f16* __restrict__ Y,
-                   float* __restrict__ part, int M, int N, int K, int G, int KTS, int ldx,
-                   int ldy, uint32_t gmagic, int gshift) {
+void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW, int M, int N,
+                   int K, int KTS, int ldx, int nb, const char* __restrict__ SZ, uint32_t gmagic,
+                   int gshift, uint32_t sc_off, uint32_t zr_off, uint32_t sz_bytes, int G, int ldy,
+                   const f16* __restrict__ bias, f16* __restrict__ Y, float* __restrict__ part) {
   static_assert(kStages == 4, "stage arrays below are written out for four stages");
   static_assert(kMT == 2 || kMT == 4 || kMT == 8, "8-row activation loads per wave");
   static_assert(kKS == 1 || (kKS == 2 && kMT == 8), "two k-slices: 128-row tiles");
@@ -156,7 +163,6 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
   const int ntn = (N + kBN - 1) / kBN;
   const int ntm = (M + kBM - 1) / kBM;
   const int total = ntn * ntm;
-  const int nb = (int)gridDim.x;
   int B = (int)blockIdx.x;
   if ((nb & 7) == 0) B = (B & 7) * (nb >> 3) + (B >> 3);
   const int sp = B / total;
@@ -496,11 +502,11 @@ hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t 
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
   const GroupDiv gd = group_div(a.G);
   hipLaunchKernelGGL((stream_kernel<kMT, kSZ1, kKS>), dim3(tiles * nsplit), dim3(kNT * kKS), 0, st,
-                     static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), base,
-                     (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes,
+                     static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), a.M, a.N,
+                     a.K, nsplit > 1 ? kts : kts1, a.ldx, tiles * nsplit, base, gd.magic, gd.shift,
+                     (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes, a.G, a.ldy,
                      static_cast<const f16*>(a.bias), static_cast<f16*>(a.y),
-                     nsplit > 1 ? part : nullptr, a.M, a.N, a.K, a.G, nsplit > 1 ? kts : kts1, a.ldx,
-                     a.ldy, gd.magic, gd.shift);
+                     nsplit > 1 ? part : nullptr);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);

@@ -57,7 +57,7 @@ COMMON_FLAGS = [
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-# Per source: the decode kernels' leading kernel arguments preloaded into
+# Per source: the kernels' leading kernel arguments preloaded into
 # SGPRs by the dispatch (their first loads then wait for no kernel-argument
 # load; firmware without the feature runs the compiler's load prologue
 # instead).
@@ -65,6 +65,8 @@ _PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 SOURCE_FLAGS = {
     "gemv.hip": _PRELOAD,
     "gemm_skinny.hip": _PRELOAD,
+    "gemm_stream.hip": _PRELOAD,
+    "gemm_occ2.hip": _PRELOAD,   # and the split-K reduction kernel
 }
 
 
