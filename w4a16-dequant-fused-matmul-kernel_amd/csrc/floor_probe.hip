@@ -33,11 +33,11 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 template <int CWB, int WAVES, int BR>
 __global__ __launch_bounds__(64 * WAVES) void rows_kernel(const uint8_t* __restrict__ w, int KP,
-                                                          int row_bytes, uint32_t* __restrict__ out) {
+                                                          int row_bytes, int nb,
+                                                          uint32_t* __restrict__ out) {
   constexpr int LPR = CWB / 16;            // lanes per row segment
   constexpr int RW = 64 / LPR;             // row-lanes per wave
   constexpr int RL = WAVES * RW;           // row-lanes per workgroup
-  const int nb = (int)gridDim.x;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64 * WAVES) void linear_kernel(const uint8_t* __res
 // S workgroups of a block share an XCD (timing only; its sums are not checked).
 template <int CWB, int WAVES, int BR, int MODE>
 __global__ __launch_bounds__(64 * WAVES) void tiles_kernel(const uint8_t* __restrict__ w, int KP,
-                                                           int row_bytes, int S,
+                                                           int row_bytes, int S, int nb,
                                                            float* __restrict__ part,
                                                            uint32_t* __restrict__ cnt,
                                                            float* __restrict__ out) {
@@ -116,7 +116,6 @@ __global__ __launch_bounds__(64 * WAVES) void tiles_kernel(const uint8_t* __rest
   constexpr int CW = CWB / 4;              // columns per block
   __shared__ float red[RL][CW];
   __shared__ uint32_t last;
-  const int nb = (int)gridDim.x;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
   const int cb = lin / S, ks = lin - cb * S;
@@ -192,7 +191,7 @@ __global__ __launch_bounds__(64 * WAVES) void tiles_kernel(const uint8_t* __rest
 template <int CWB, int WAVES, int BR>
 int launch_rows(const void* w, int KP, int row_bytes, uint32_t* out, hipStream_t st) {
   hipLaunchKernelGGL((rows_kernel<CWB, WAVES, BR>), dim3(row_bytes / CWB), dim3(64 * WAVES), 0, st,
-                     static_cast<const uint8_t*>(w), KP, row_bytes, out);
+                     static_cast<const uint8_t*>(w), KP, row_bytes, row_bytes / CWB, out);
   return (int)hipGetLastError();
 }
 
@@ -241,13 +240,13 @@ int w4a16_probe_tiles(const void* w, int KP, int row_bytes, int cwb, int waves, 
   if (cwb == CWB) {                                                                              \
     if (mode == 0)                                                                               \
       hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 0>), grid, block, 0, st, wp, KP, row_bytes, s, \
-                         part, cnt, out);                                                        \
+                         (int)grid.x, part, cnt, out);                                           \
     else if (mode == 1)                                                                          \
       hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 1>), grid, block, 0, st, wp, KP, row_bytes, s, \
-                         part, cnt, out);                                                        \
+                         (int)grid.x, part, cnt, out);                                           \
     else                                                                                         \
       hipLaunchKernelGGL((tiles_kernel<CWB, 8, 4, 2>), grid, block, 0, st, wp, KP, row_bytes, s, \
-                         part, cnt, out);                                                        \
+                         (int)grid.x, part, cnt, out);                                           \
     return (int)hipGetLastError();                                                               \
   }
   W4A16_PROBE_TILES(128)

@@ -67,6 +67,7 @@ SOURCE_FLAGS = {
     "gemm_skinny.hip": _PRELOAD,
     "gemm_stream.hip": _PRELOAD,
     "gemm_occ2.hip": _PRELOAD,   # and the split-K reduction kernel
+    "floor_probe.hip": _PRELOAD,  # the probe's floors start like the kernels they bound
 }
 
 
