@@ -59,22 +59,25 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // CU streams X once for 32 columns instead of once per 16).
 //
 // Arguments: the first fourteen SGPRs' worth are what the first loads need
-// (operand pointers, M, N, K, G, the row groups, ldx); the library is built
-// to have the dispatch preload them into SGPRs (-mllvm
+// (operand pointers, M, N, K, the group reciprocal, the row groups, ldx); the
+// library is built to have the dispatch preload them into SGPRs (-mllvm
 // -amdgpu-kernarg-preload-count), so the first loads wait for no
 // kernel-argument load, and the epilogue's arguments are loaded meanwhile.
-// mgs_rpg = row groups per column block | rows per group << 16; the grid size
-// is nblk * mgs (no read of the dispatch packet).
+// geo = row groups per column block | rows per group << 8 | group shift << 16;
+// k / G is (umulhi(k, gmagic) + k) >> shift (group_div), no division; the
+// grid size is nblk * mgs (no read of the dispatch packet).
 template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
-    const uint16_t* __restrict__ ZR, int M, int N, int K, int G, int mgs_rpg, int ldx, int ldy,
-    const f16* __restrict__ bias, f16* __restrict__ Y) {
+    const uint16_t* __restrict__ ZR, int M, int N, int K, uint32_t gmagic, uint32_t geo, int ldx,
+    int ldy, const f16* __restrict__ bias, f16* __restrict__ Y) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four columns per lane");
   constexpr int kWaves = WAVES;
   __shared__ f32x4 red[kWaves][MT][NT][64];
 
-  const int mgs = mgs_rpg & 0xFFFF, rpg = mgs_rpg >> 16;
+  const int mgs = (int)(geo & 0xFFu), rpg = (int)((geo >> 8) & 0xFFu);
+  const int gshift = (int)(geo >> 16);
+  auto group_of = [&](uint32_t k) { return div_group(k, gmagic, gshift); };
   const int nb = (N + 16 * NT - 1) / (16 * NT) * mgs;
   int lin = (int)blockIdx.x;
   if ((nb & 7) == 0) lin = (lin & 7) * (nb >> 3) + (lin >> 3);
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const bool nv = col < N;                   // (N even for NT = 2: so is col + 1)
   const int KP = K >> 3;
   const int KS = K >> 5;         // 32-k steps
-  const int NG = K / G;
+  const int NG = (int)group_of((uint32_t)K);
 
   const MagicRegs mg = make_magic();
   // rows of X lie ldx elements apart; the range ends after row M - 1's K
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
         }
         if (j % GSTEP == 0) {
           const uint32_t gk =
-              uniform(in ? (uint32_t)((ks * 32) / G) * (uint32_t)N * 2u : kOobOffset);
+              uniform(in ? group_of((uint32_t)(ks * 32)) * (uint32_t)N * 2u : kOobOffset);
           if constexpr (NT == 1) {
             const uint32_t sv =
                 (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)s_off, (int)gk, 0);
@@ -311,11 +314,13 @@ hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
            : ks <= k16 * kBatch ? skinny_kernel<MT, GSTEP, (k16 ? k16 : 4), NT, true>
                                 : skinny_kernel<MT, GSTEP, 4, NT, false>;
   const int waves = ks <= 4 * kBatch ? 4 : ks <= 8 * kBatch ? 8 : ks <= k16 * kBatch ? k16 : 4;
+  const GroupDiv gd = group_div(a.G);
+  const uint32_t geo = (uint32_t)mgs | ((uint32_t)rpg << 8) | ((uint32_t)gd.shift << 16);
   hipLaunchKernelGGL(k, dim3(nblk * mgs), dim3(64 * waves), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw),
                      static_cast<const uint16_t*>(a.sc), static_cast<const uint16_t*>(a.zr), a.M,
-                     a.N, a.K, a.G, mgs | (rpg << 16), a.ldx, a.ldy,
-                     static_cast<const f16*>(a.bias), static_cast<f16*>(a.y));
+                     a.N, a.K, gd.magic, geo, a.ldx, a.ldy, static_cast<const f16*>(a.bias),
+                     static_cast<f16*>(a.y));
   return hipGetLastError();
 }
 
