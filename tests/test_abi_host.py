@@ -579,6 +579,24 @@ def test_planner_skinny_row_groups():
     assert (p.tile_cfg, p.tile_m) == (2, 16)
 
 
+def test_empty_shapes_plan_simt_for_every_family():
+    """M, N or K = 0 plans the SIMT kernel whatever family is forced (nothing is
+    launched for M = 0 / N = 0; K = 0 writes zeros with it).  Forcing the
+    MFMA family on an empty shape once divided by its zero tile count
+    (SIGFPE in the planner, found by the host-side AddressSanitizer run)."""
+    from w4a16 import _lib
+
+    for M, N, K in ((0, 0, 0), (0, 64, 64), (4, 0, 64), (4, 64, 0), (300, 0, 4096)):
+        for kernel in (0, _lib.KERNEL_GEMV, _lib.KERNEL_MFMA, _lib.KERNEL_SIMT,
+                       _lib.KERNEL_SKINNY):
+            for split in (0, 1, 4):
+                p = _lib.plan(M, N, K, 32, kernel, split)
+                assert p.kernel == _lib.KERNEL_SIMT and p.split_k == 1, (M, N, K, kernel, split)
+                assert p.workspace_bytes == 0
+    with pytest.raises(RuntimeError):
+        _lib.plan(4, 64, 64, 32, 9, 0)       # no such family
+
+
 def test_planner_prefill_split_k():
     from w4a16 import _lib
 

@@ -447,6 +447,7 @@ SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus
 // M = 256, K = 3584, N = 37888, 296 tiles: 97.3 us at 2 splits, 84.8 unsplit;
 // M = 64, 148 64-row tiles: 44.2 at 4, 39.4 at 2).
 int stream_split_for(int64_t tiles, int64_t K, int cus) {
+  if (tiles <= 0) return 1;
   const int64_t kt = K / 64;
   int64_t s = (448 + tiles - 1) / tiles;
   if (s * tiles > 2 * (int64_t)cus) s = 2 * (int64_t)cus / tiles;
@@ -538,7 +539,14 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
               w4a16_plan* p) {
   const int cus = device_cu_count();
   *p = w4a16_plan{};
-  if (kernel == W4A16_KERNEL_AUTO && (M == 0 || N == 0 || K == 0)) kernel = W4A16_KERNEL_SIMT;
+  // Empty shapes (forced families included) plan the SIMT kernel: nothing is
+  // launched for M = 0 or N = 0, and K = 0 writes y = 0 with it.  (The tile
+  // and block counts of the other families would be zero, and their split
+  // rules divide by them.)
+  if (kernel != W4A16_KERNEL_AUTO && kernel != W4A16_KERNEL_GEMV && kernel != W4A16_KERNEL_MFMA &&
+      kernel != W4A16_KERNEL_SIMT && kernel != W4A16_KERNEL_SKINNY)
+    return W4A16_ERR_BAD_PLAN;
+  if (M == 0 || N == 0 || K == 0) kernel = W4A16_KERNEL_SIMT;
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;
