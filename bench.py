@@ -85,9 +85,14 @@ def _args():
                     help="write profiles/traffic.json from the counter_collection.csv files "
                          "of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "--traffic-probe")
-    ap.add_argument("--floor-probe", action="store_true",
-                    help="time the decode GEMV's weight-access shapes loads-only "
-                         "(csrc/floor_probe.hip) beside the GEMV itself; markdown table")
+    ap.add_argument("--empty-kernels", action="store_true",
+                    help="time K calls of two near-empty kernels exactly as the headline's "
+                         "calls are timed (eager, behind the spin, HIP events): the per-dispatch "
+                         "cost of the queue itself, untraced or under a tracer")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="markdown table of a rocprofv3 --kernel-trace CSV of bench.py: per "
+                         "kernel, the durations of its last --steps dispatches (the timed "
+                         "calls) and the gaps between them")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="markdown table of every counter in rocprofv3 --pmc runs of "
                          "--traffic-probe, per workload and kernel")
@@ -154,6 +159,50 @@ def _time_calls(fns, steps: int, warmup: int, graph: bool) -> dict:
             break
     return {"ms": start.elapsed_time(end) / steps, "queued_before_start": queued,
             "host_us_per_call": host_us, "spin_us": spin_us}
+
+
+def empty_kernels(steps: int, warmup: int) -> dict:
+    """Per-call time of near-empty kernels queued and timed like the headline's
+    calls: torch.cuda._sleep(0) (one thread, no work) and a fill of 128 Ki fp16
+    (torch's elementwise kernel over a grid of workgroups).  What the queue
+    costs per dispatch; run under rocprofv3 --kernel-trace as well, it shows
+    what the tracer adds to each dispatch."""
+    import torch
+
+    buf = torch.empty(256 * 512, dtype=torch.float16, device="cuda")
+    out = {}
+    for name, fn in (("sleep0", lambda: torch.cuda._sleep(0)), ("fill_128Ki_f16", lambda: buf.fill_(1.0))):
+        t = _time_calls([fn], steps, warmup, False)
+        out[name] = {"us_per_call": round(t["ms"] * 1e3, 4),
+                     "queued_before_start": t["queued_before_start"]}
+    return {"what": "near-empty kernels, K eager calls behind a spin kernel, HIP events",
+            "steps": steps, "warmup": warmup, "kernels": out}
+
+
+def trace_summary(path: str, last: int) -> str:
+    """Markdown table from a rocprofv3 kernel-trace CSV: per kernel, the
+    number of dispatches, and over its last `last` dispatches (bench.py's timed
+    calls are each kernel's last ones) the mean / median / min / max duration
+    and the mean gap from one dispatch's end to the next one's start."""
+    import csv
+    import statistics
+
+    by = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            by.setdefault(r["Kernel_Name"], []).append(
+                (int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    lines = [f"| kernel | dispatches | last {last}: mean ns | median ns | min ns | max ns | "
+             "mean gap ns |", "|---|---|---|---|---|---|---|"]
+    for name, ds in sorted(by.items(), key=lambda kv: -len(kv[1])):
+        ds.sort()
+        tail = ds[-last:]
+        dur = [e - s for s, e in tail]
+        gaps = [tail[i + 1][0] - tail[i][1] for i in range(len(tail) - 1)]
+        gap = f"{statistics.mean(gaps):.0f}" if gaps else ""
+        lines.append(f"| `{_kernel_short(name)}` | {len(ds)} | {statistics.mean(dur):.0f} | "
+                     f"{statistics.median(dur):.0f} | {min(dur)} | {max(dur)} | {gap} |")
+    return "\n".join(lines)
 
 
 def _prepare(case, copies_for_cold: bool):
@@ -343,133 +392,6 @@ def to_markdown_table(results: list[dict]) -> str:
     return header + "\n".join(rows) + "\n"
 
 
-# --floor-probe: the decode GEMV's weight-access shapes with the dequant and
-# dot products taken out (csrc/floor_probe.hip).  (label, config, K, N)
-FLOOR_SHAPES = [("C2", "C2", 4096, 4096), ("C3 N=28672", "C3", 4096, 28672),
-                ("C5 K=8192", "C5", 8192, 28672), ("C5 K=28672", "C5", 28672, 8192)]
-# rows: (column-block bytes, waves, rows per lane per batch); linear: (workgroups,
-# waves, loads per lane in flight)
-FLOOR_ROWS = [(64, 16, 2), (64, 8, 4), (128, 16, 2), (256, 8, 4), (256, 16, 2), (512, 8, 4),
-              (512, 16, 2)]
-FLOOR_LINEAR = [(256, 8, 4), (512, 8, 4), (1024, 4, 8)]
-# tiles (K split across workgroups): (column-block bytes, k-ranges); each with
-# mode 0 (partials stored, no cross-workgroup step), 1 (in-kernel reduction over
-# device-coherent stores / loads and a counter) and 2 (the same chain through
-# the L2 alone; timing only).  Kept where they give 256 or 512 workgroups.
-FLOOR_TILES = [(128, 2), (256, 4), (512, 8), (256, 2), (512, 4), (256, 8), (512, 2)]
-TILE_MODES = {0: "partials stored, no reduction", 1: "in-kernel reduction, device-coherent",
-              2: "in-kernel reduction through L2 only (timing only)"}
-
-
-def floor_probe(steps: int, only: tuple[str, ...] | None = None) -> str:
-    """Markdown table: µs per call and GB/s of packed-weight bytes for the
-    loads-only probe's row shapes (a GEMV column block of 64 / 128 / 256 / 512
-    bytes, i.e. 16 / 32 / 64 / 128 columns) and linear reads of the same bytes, cold like
-    the bench (rotating copies), beside the GEMV's default plan on the M = 1,
-    G = 128 case of each shape (its GB/s also counts scales, zeros, x, y)."""
-    import ctypes
-
-    import torch
-    from w4a16 import _build
-    from w4a16 import workloads as wl
-
-    lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
-    vp, i32 = ctypes.c_void_p, ctypes.c_int
-    lib.w4a16_probe_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
-    lib.w4a16_probe_linear.argtypes = [vp, ctypes.c_uint32, i32, i32, i32, vp, vp]
-    lib.w4a16_probe_rows_out_words.restype = ctypes.c_int64
-    lib.w4a16_probe_rows_out_words.argtypes = [i32, i32, i32]
-    lib.w4a16_probe_linear_out_words.restype = ctypes.c_int64
-    lib.w4a16_probe_linear_out_words.argtypes = [i32, i32]
-    lib.w4a16_probe_tiles.argtypes = [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp]
-    rows = ["| shape | packed weights | access | µs | GB/s |", "|---|---|---|---|---|"]
-    for label, cfg, K, N in FLOOR_SHAPES:
-        if only and label not in only:
-            continue
-        KP, row_bytes = K // 8, N * 4
-        nbytes = KP * row_bytes
-        ncopy = max(2, -(-COLD_BYTES // nbytes) + 1)
-        bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
-                for _ in range(ncopy)]
-
-        def timed(launch) -> float:
-            fns = [(lambda b=b: launch(b)) for b in bufs]
-            return _time_calls(fns, steps, 10, False)["ms"] * 1e3
-
-        shapes = []
-        for cwb, waves, br in FLOOR_ROWS:
-            if row_bytes % cwb:
-                continue
-            out = torch.empty(lib.w4a16_probe_rows_out_words(row_bytes, cwb, waves),
-                              dtype=torch.int32, device="cuda")
-
-            def launch(b, cwb=cwb, waves=waves, br=br, out=out):
-                rc = lib.w4a16_probe_rows(b.data_ptr(), KP, row_bytes, cwb, waves, br,
-                                          out.data_ptr(), torch.cuda.current_stream().cuda_stream)
-                if rc:
-                    raise RuntimeError(f"w4a16_probe_rows: {rc}")
-            shapes.append((f"rows: {cwb // 4}-column blocks ({row_bytes // cwb} workgroups), "
-                           f"{waves} waves, {br} rows/lane/batch", launch))
-        for nwg, waves, br in FLOOR_LINEAR:
-            out = torch.empty(lib.w4a16_probe_linear_out_words(nwg, waves), dtype=torch.int32,
-                              device="cuda")
-
-            def launch(b, nwg=nwg, waves=waves, br=br, out=out):
-                rc = lib.w4a16_probe_linear(b.data_ptr(), nbytes, nwg, waves, br, out.data_ptr(),
-                                            torch.cuda.current_stream().cuda_stream)
-                if rc:
-                    raise RuntimeError(f"w4a16_probe_linear: {rc}")
-            shapes.append((f"linear: {nwg} workgroups of {waves} waves, {br} loads/lane", launch))
-        for cwb, ns in FLOOR_TILES:
-            nwg = row_bytes // cwb * ns
-            if row_bytes % cwb or KP % ns or nwg not in (256, 512):
-                continue
-            words = nwg * cwb // 4
-            part = torch.empty(words, dtype=torch.float32, device="cuda")
-            out = torch.empty(words, dtype=torch.float32, device="cuda")
-            cnt = torch.zeros(row_bytes // cwb, dtype=torch.int32, device="cuda")
-            # mode 1's in-kernel sums against the host's sum (range order, fp32)
-            # of the mode-0 partials of the same weights
-            st = torch.cuda.current_stream().cuda_stream
-            rc = lib.w4a16_probe_tiles(bufs[0].data_ptr(), KP, row_bytes, cwb, 8, 4, ns, 0,
-                                       part.data_ptr(), cnt.data_ptr(), out.data_ptr(), st)
-            p0 = out.view(-1, ns, cwb // 4).cpu()
-            want = p0[:, 0, :].clone()
-            for k in range(1, ns):
-                want += p0[:, k, :]
-            rc = rc or lib.w4a16_probe_tiles(bufs[0].data_ptr(), KP, row_bytes, cwb, 8, 4, ns, 1,
-                                             part.data_ptr(), cnt.data_ptr(), out.data_ptr(), st)
-            if rc:
-                raise RuntimeError(f"w4a16_probe_tiles: {rc}")
-            got = out[: want.numel()].view_as(want).cpu()
-            same = bool(torch.equal(got, want)) and int(cnt.abs().sum()) == 0
-            for mode, what in TILE_MODES.items():
-                if mode == 1:
-                    what += ", sums " + ("equal to the host's" if same else "DIFFER from the host's")
-                def launch(b, cwb=cwb, ns=ns, mode=mode, part=part, out=out, cnt=cnt):
-                    rc = lib.w4a16_probe_tiles(b.data_ptr(), KP, row_bytes, cwb, 8, 4, ns, mode,
-                                               part.data_ptr(), cnt.data_ptr(), out.data_ptr(),
-                                               torch.cuda.current_stream().cuda_stream)
-                    if rc:
-                        raise RuntimeError(f"w4a16_probe_tiles: {rc}")
-                shapes.append((f"tiles: {cwb // 4}-column blocks x {ns} k-ranges ({nwg} "
-                               f"workgroups), 8 waves, 4 rows/lane/batch; {what}", launch))
-        for what, launch in shapes:
-            us = timed(launch)
-            rows.append(f"| {label} | {nbytes / 2**20:.1f} MiB | {what} | {us:.2f} | "
-                        f"{nbytes / us / 1e3:.0f} |")
-            print(rows[-1], file=sys.stderr, flush=True)
-        del bufs
-        torch.cuda.empty_cache()
-        case = [c for c in wl.CONFIGS[cfg] if (c.M, c.K, c.N, c.G) == (1, K, N, 128)][0]
-        r = bench_case(case, steps, 10, cold=True)
-        rows.append(f"| {label} | {nbytes / 2**20:.1f} MiB | GEMV as planned ({r['kernel']} "
-                    f"{r['tile'][1]}-column blocks, cfg {r['tile_cfg']}), with dequant and dot "
-                    f"products | {r['us']:.2f} | {r['GB/s']:.0f} (all bytes) |")
-        print(rows[-1], file=sys.stderr, flush=True)
-    return "\n".join(rows)
-
-
 def reference_table(json_path: str | None) -> dict:
     from w4a16 import workloads as wl
 
@@ -619,7 +541,7 @@ def _kernel_short(mangled: str) -> str:
 
     m = re.match(r"_ZN5w4a1612_GLOBAL__N_1(\d+)", mangled)
     if not m:                                    # already demangled by the profiler
-        short = mangled.replace("w4a16::(anonymous namespace)::", "")
+        short = mangled.replace("w4a16::", "").replace("(anonymous namespace)::", "")
         return short.split("(")[0].replace("void ", "")
     n = int(m.group(1))
     at = m.end()
@@ -673,6 +595,9 @@ def main() -> int:
     if args.pmc_summary:
         print(pmc_summary(args.pmc_summary))
         return 0
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.steps))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build targets a single MI355X: columns would shard with no "
@@ -687,11 +612,11 @@ def main() -> int:
     if args.traffic_probe:
         traffic_probe()
         return 0
+    if args.empty_kernels:
+        print(json.dumps(empty_kernels(args.steps, args.warmup)), flush=True)
+        return 0
     if args.reference_table:
         print(json.dumps(reference_table(args.reference_json)), flush=True)
-        return 0
-    if args.floor_probe:
-        print(floor_probe(max(20, args.steps // 4)), flush=True)
         return 0
     from w4a16 import workloads as wl
 

@@ -19,10 +19,17 @@
  *   qweight int32 [K/8, N]      word (i, n) holds rows 8i..8i+7, row 8i+j in
  *                               bits [4j, 4j+4), unsigned codes 0..15
  *   scales  fp16  [K/G, N]
- *   zeros   fp16  [K/G, N]      integer zero-points (the fused GEMM kernels
- *                               require integers in [-63, 63]; quantize_weight
- *                               produces 0..15)
+ *   zeros   fp16  [K/G, N]      zero-points; W = fp16(fp16(fp16(q) - z) * s)
  *   y       fp16  [M, N]        Y = fp16(fp32-accumulated X @ dequant(W)) (row stride ldy)
+ *
+ * Zero-points: quantize_weight produces integers 0..15.  By default the fused
+ * kernels assume integer zeros with |z| <= 1024, which lets them dequantise
+ * with one subtract and one multiply per pair of weights.  Any other zeros
+ * (fractions, larger magnitudes, NaN, infinities) need a plan with
+ * W4A16_PLAN_ANY_ZEROS set, which runs the same kernels with one more packed
+ * subtract per pair and gives the reference's rounding for every fp16 zero;
+ * w4a16_zeros_check_f16 tells which a tensor needs.  (The Python layer checks
+ * each zeros tensor once and sets the flag itself.)
  */
 #ifndef W4A16_H_
 #define W4A16_H_
@@ -34,7 +41,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 1
+#define W4A16_ABI_VERSION 2
 
 enum w4a16_status {
   W4A16_OK = 0,
@@ -54,6 +61,9 @@ enum w4a16_kernel {
   W4A16_KERNEL_SIMT = 3, /* sequential-k, one thread per output, any shape           */
   W4A16_KERNEL_SKINNY = 4 /* small batch: v_mfma_f32_16x16x32_f16, weights streamed   */
 };
+
+/* w4a16_plan.flags */
+#define W4A16_PLAN_ANY_ZEROS 1 /* zeros may be any fp16 value (see above)     */
 
 /* The launch a GEMM call will make.  Filled by w4a16_gemm_plan(). */
 typedef struct w4a16_plan {
@@ -82,6 +92,9 @@ typedef struct w4a16_plan {
                               64-column blocks) x columns                    */
   int64_t grid_x, grid_y;  /* workgroups launched                              */
   int64_t workspace_bytes; /* device workspace the call needs (0 = none)        */
+  int32_t flags;           /* W4A16_PLAN_ANY_ZEROS or 0 (w4a16_gemm_plan sets
+                              0; the caller may set it); other bits are
+                              refused (W4A16_ERR_BAD_PLAN)                    */
 } w4a16_plan;
 
 /* Version of this ABI (W4A16_ABI_VERSION). */
@@ -107,6 +120,16 @@ const char* w4a16_status_string(int status);
 int w4a16_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t group_size, int32_t kernel,
                     int32_t split_k, w4a16_plan* plan);
 
+/*
+ * Whether `zeros` (count fp16 values on the device) need W4A16_PLAN_ANY_ZEROS:
+ * sets *flag (a device int32 the caller zero-fills) to 1 if any zero is not
+ * an integer in [-1024, 1024].  Asynchronous on `stream`.  No reference
+ * counterpart: the reference's kernels dequantise every zero alike
+ * (triton_kernel.py:117-119, cuda/w4a16_gemm.cu:51-58); here a caller checks a
+ * zeros tensor once, when it is made or loaded, not on every GEMM.
+ */
+int w4a16_zeros_check_f16(const void* zeros, int64_t count, int32_t* flag, void* stream);
+
 /* Workspace bytes the automatic plan for this shape needs (0 = none). */
 size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size);
 
@@ -117,8 +140,9 @@ size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group
  * w4a16_gemm_cuda (w4a16-kernel/src/w4a16/cuda/w4a16_gemm.cu:76-115).
  * `workspace` (256-byte aligned) must hold w4a16_gemm_workspace_bytes() bytes
  * of fp32 split-K partials; its contents need no initialisation and are
- * overwritten by every call.  Calls that share one workspace must be ordered
- * (same stream).  M = 0 or N = 0 launches nothing;
+ * overwritten by every call.  Integer zeros with |z| <= 1024 only (any other
+ * zeros: a plan with W4A16_PLAN_ANY_ZEROS, w4a16_gemm_f16_strided).  Calls
+ * that share one workspace must be ordered (same stream).  M = 0 or N = 0 launches nothing;
  * K = 0 writes y = 0 (x, qweight, scales and zeros may then be NULL).  The
  * library issues kernel launches only (no memset or copy), so calls can be
  * captured into a HIP graph.
@@ -182,7 +206,9 @@ int w4a16_gemm_f16_strided(const w4a16_plan* plan, const void* x, int64_t ldx,
  * (nothing needs to start zeroed: a call writes its partials before it reads
  * them), so calls that overlap on one GPU -- different streams, or graphs
  * replayed concurrently -- race and must be ordered by the caller.  Results
- * equal w4a16_gemm_f16_strided's for the same plan.
+ * equal w4a16_gemm_f16_strided's for the same plan.  The scratch address a
+ * device's first call resolves is kept for the life of the process: do not
+ * call this entry point on a device after hipDeviceReset.
  */
 int w4a16_gemm_f16_noalloc(const w4a16_plan* plan, const void* x, int64_t ldx,
                            const int32_t* qweight, const void* scales, const void* zeros,

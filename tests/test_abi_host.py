@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.w4a16_abi_version() == 1
+    assert lib.w4a16_abi_version() == 2
     for code in (0, -1, -2, -3, -4, -5, -6):
         s = lib.w4a16_status_string(code)
         assert s and isinstance(s, bytes)
@@ -110,6 +110,29 @@ def test_split_k_gemv_requires_workspace(lib):
     code = lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096, 128,
                                       a, 1 << 30, NULL)
     assert code == -5
+
+
+def test_plan_flags_and_zeros_check_arguments(lib):
+    """Plans start with no flags; a flag bit other than W4A16_PLAN_ANY_ZEROS is
+    refused before any launch; the zeros check validates its arguments and
+    launches nothing for an empty tensor."""
+    from w4a16 import _lib
+
+    p = _lib.plan(1, 1024, 4096, 128)
+    assert p.flags == 0
+    a = ctypes.c_void_p(1 << 12)   # aligned fake pointers: never dereferenced
+    for bad in (2, 4, 1 | 8, -1):
+        p.flags = bad
+        assert lib.w4a16_gemm_f16_planned(ctypes.byref(p), a, a, a, a, NULL, a, 1, 1024, 4096,
+                                          128, NULL, 0, NULL) == -5
+        assert lib.w4a16_gemm_f16_strided(ctypes.byref(p), a, 4096, a, a, a, NULL, a, 1024, 1,
+                                          1024, 4096, 128, NULL, 0, NULL) == -5
+        assert lib.w4a16_gemm_f16_noalloc(ctypes.byref(p), a, 4096, a, a, a, NULL, a, 1024, 1,
+                                          1024, 4096, 128, NULL) == -5
+    assert lib.w4a16_zeros_check_f16(a, -1, a, NULL) == -2
+    assert lib.w4a16_zeros_check_f16(NULL, 8, a, NULL) == -1
+    assert lib.w4a16_zeros_check_f16(a, 8, NULL, NULL) == -1
+    assert lib.w4a16_zeros_check_f16(NULL, 0, NULL, NULL) == 0
 
 
 def test_retired_configurations_refused(lib):
@@ -803,25 +826,3 @@ def test_stale_library_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_sources_hash", lambda: "0" * 64)
     with pytest.raises(ImportError, match="other sources"):
         _lib.load()
-
-
-def test_floor_probe_library_exports():
-    """bench.py --floor-probe's loads-only library is built beside libw4a16.so,
-    exports its entry points, sizes its output and refuses shapes it has no
-    kernel for before any launch (no GPU call here)."""
-    import ctypes
-
-    from w4a16 import _build
-
-    lib = ctypes.CDLL(_build.PROBE_LIB_PATH)
-    for name in ("w4a16_probe_rows", "w4a16_probe_linear", "w4a16_probe_rows_out_words",
-                 "w4a16_probe_linear_out_words"):
-        assert hasattr(lib, name), name
-    lib.w4a16_probe_rows_out_words.restype = ctypes.c_int64
-    assert lib.w4a16_probe_rows_out_words(114688, 512, 8) == 224 * 512
-    vp, i32 = ctypes.c_void_p, ctypes.c_int
-    lib.w4a16_probe_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
-    lib.w4a16_probe_linear.argtypes = [vp, ctypes.c_uint32, i32, i32, i32, vp, vp]
-    assert lib.w4a16_probe_rows(None, 512, 16384, 48, 8, 4, None, None) == -1   # 16384 % 48
-    assert lib.w4a16_probe_rows(None, 1 << 20, 16384, 64, 8, 4, None, None) == -1  # >= 2 GiB
-    assert lib.w4a16_probe_linear(None, 1000, 3, 8, 4, None, None) == -1       # 1000 % 48

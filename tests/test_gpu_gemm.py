@@ -508,3 +508,32 @@ def test_baselines_on_gpu():
     # CPU inputs come back on the CPU
     y4 = fp16_matmul(X.cpu(), W.cpu())
     assert y4.device.type == "cpu" and torch.equal(y4, y3.cpu())
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("cfg", [4, 5, 6, 7])
+def test_gemv_staged_nonfinite_activations(M, cfg):
+    """An inf in X on the staged GEMV blocks whose runs take an odd number of
+    batches (K = 5120: five 4-row batches per row-lane on 64-column blocks):
+    the batch after a run's end holds the next row-lane's rows, and its zero
+    weights must meet the zero row of X, not that row-lane's inf.  Y must give
+    the oracle's inf / NaN pattern: +-inf where the weight under the inf is
+    non-zero, NaN where it dequantises to zero."""
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+
+    K, N, G = 5120, 13824, 64
+    X, qw, s, z = _build_case(M, K, N, G, seed=17, std=0.02)
+    X[0, 777] = float("inf")
+    if M == 2:
+        X[1, 4100] = float("-inf")
+    cols = sample_cols(N, 256)
+    ref = oracle_cols(X, qw, s, z, G, cols)
+    assert np.isinf(ref).any() and np.isnan(ref).any(), "the case must hold both inf and NaN"
+    for cols_per_wg in (64, 128):
+        if cfg in (4, 5) and cols_per_wg == 128:
+            continue
+        p = plan_for(M, N, K, G, "gemv", 1)
+        p.tile_n, p.tile_cfg = cols_per_wg, cfg
+        log(f"gemv inf M={M} K={K} N={N} G={G} cfg={cfg} cols={cols_per_wg}")
+        out = w4a16_matmul_planned(X, qw, s, z, G, p)
+        assert_gemm_close(out[:, cols], ref, f"gemv inf cfg={cfg} cols={cols_per_wg}")

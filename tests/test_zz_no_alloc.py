@@ -170,3 +170,78 @@ def test_noalloc_rejects_plan_beyond_scratch():
     assert rc == ERR_WORKSPACE
     assert lib.w4a16_gemm_f16_noalloc(None, None, 64, None, None, None, None, None, N,
                                       M, N, 64, 48, None) == -3     # G does not divide K
+
+
+# A fresh process whose first call into the library is a split-K noalloc call
+# made while torch captures a HIP graph: the library's code object, and with
+# it the static scratch, is loaded and the scratch's address resolved inside
+# the capture.  The inputs are made with torch alone (no library kernel runs
+# before the capture).
+_CAPTURE_CHILD = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import torch
+from w4a16 import _lib
+lib = _lib.load()
+dev = "cuda"
+M, K, N, G = 1, 14336, 1024, 128          # automatic plan: GEMV, 4-way split
+gen = torch.Generator(device=dev).manual_seed(0)
+X = torch.randn(M, K, device=dev, generator=gen).half()
+qw = torch.randint(-2**31, 2**31 - 1, (K // 8, N), dtype=torch.int32, device=dev, generator=gen)
+s = (torch.rand(K // G, N, device=dev, generator=gen) * 0.01 + 0.001).half()
+z = torch.randint(0, 16, (K // G, N), device=dev, generator=gen).half()
+p = _lib.plan(M, N, K, G)
+assert p.split_k > 1, p.as_dict()
+
+def call(x, w, sc, zr, y, m, n, k):
+    return lib.w4a16_gemm_f16_noalloc(None, x.data_ptr(), k, w.data_ptr(), sc.data_ptr(),
+                                      zr.data_ptr(), None, y.data_ptr(), n, m, n, k, G,
+                                      torch.cuda.current_stream().cuda_stream)
+
+y_cap = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream()
+with torch.cuda.graph(graph, stream=side):
+    rc = call(X, qw, s, z, y_cap, M, N, K)
+assert rc == 0, ("capture", rc)
+# eager result, and a smaller split call that leaves other partials in the scratch
+y_eager = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+before = torch.cuda.memory_allocated()
+assert call(X, qw, s, z, y_eager, M, N, K) == 0
+assert torch.cuda.memory_allocated() == before, "the call allocated through torch"
+K2, N2 = 8192, 512
+X2 = torch.randn(M, K2, device=dev, generator=gen).half()
+qw2 = torch.randint(-2**31, 2**31 - 1, (K2 // 8, N2), dtype=torch.int32, device=dev, generator=gen)
+s2 = (torch.rand(K2 // G, N2, device=dev, generator=gen) * 0.01).half()
+z2 = torch.randint(0, 16, (K2 // G, N2), device=dev, generator=gen).half()
+y2 = torch.empty(M, N2, dtype=torch.float16, device=dev)
+torch.cuda.synchronize()
+assert bool(torch.isfinite(y_eager).all())
+for rep in range(3):
+    y_cap.fill_(float("nan"))
+    assert call(X2, qw2, s2, z2, y2, M, N2, K2) == 0
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y_cap, y_eager), ("replay", rep)
+print("CAPTURE-CHILD-OK", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_inside_graph_capture():
+    """In a fresh process, the library's first call is a split-K noalloc call
+    under HIP-graph capture; three replays, each after an eager split call of
+    another shape, equal the eager result bit for bit, and an eager call
+    leaves torch's allocation counter unchanged."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+    pkg = os.path.join(root, "w4a16-dequant-fused-matmul-kernel_amd")
+    log("noalloc: first call inside graph capture (child process)")
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root, pkg], capture_output=True,
+                         text=True, timeout=150)
+    assert res.returncode == 0 and "CAPTURE-CHILD-OK" in res.stdout, (
+        f"rc={res.returncode}\n{res.stdout[-2000:]}\n{res.stderr[-3000:]}")

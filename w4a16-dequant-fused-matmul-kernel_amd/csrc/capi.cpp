@@ -682,8 +682,10 @@ int run_planned(const w4a16_plan* p, const void* x, int64_t ldx, const int32_t* 
   if (int st = check_strides(M, N, K, ldx, ldy)) return st;
   if (M == 0 || N == 0) return W4A16_OK;
   if (!y || (K > 0 && (!x || !qw || !sc || !zr))) return W4A16_ERR_NULL_POINTER;
+  if (p->flags & ~W4A16_PLAN_ANY_ZEROS) return W4A16_ERR_BAD_PLAN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy};
+  GemmArgs a{x, qw, sc, zr, bias, y, (int)M, (int)N, (int)K, (int)G, (int)ldx, (int)ldy,
+             (p->flags & W4A16_PLAN_ANY_ZEROS) != 0};
   // K = 0: Y = 0 (+ bias).  A kernel rather than a memset, so that the call
   // can be captured into a HIP graph; the SIMT kernel reads no operand then.
   if (K == 0) return to_status(launch_simt(a, s));
@@ -848,6 +850,13 @@ int w4a16_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t group_size, int32_t
   return make_plan(M, N, K, group_size, kernel, split_k, plan);
 }
 
+int w4a16_zeros_check_f16(const void* zeros, int64_t count, int32_t* flag, void* stream) {
+  if (count < 0) return W4A16_ERR_BAD_SHAPE;
+  if (count == 0) return W4A16_OK;
+  if (!zeros || !flag) return W4A16_ERR_NULL_POINTER;
+  return to_status(launch_zeros_check(zeros, count, flag, static_cast<hipStream_t>(stream)));
+}
+
 size_t w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {
   w4a16_plan p;
   if (check_gemm_shape(M, N, K, group_size) != W4A16_OK) return 0;
@@ -901,14 +910,17 @@ int w4a16_gemm_f16_noalloc(const w4a16_plan* plan, const void* x, int64_t ldx,
   if (plan) {
     // an explicit plan whose partials do not fit the scratch is refused
     p = *plan;
+    if (p.flags & ~W4A16_PLAN_ANY_ZEROS) return W4A16_ERR_BAD_PLAN;
     if (plan_scratch_bytes(p, M, N, K) > kMax) return W4A16_ERR_WORKSPACE;
   } else {
     if (int st = auto_plan(x, ldx, qweight, scales, zeros, bias, y, ldy, M, N, K, group_size, &p))
       return st;
     // the automatic plan takes the most k-splits whose partials fit (a plan
     // with one split needs no scratch at all)
+    const int32_t flags = p.flags;
     for (int s = p.split_k - 1; plan_scratch_bytes(p, M, N, K) > kMax && s >= 1; --s)
       if (int st = make_plan(M, N, K, group_size, p.kernel, s, &p)) return st;
+    p.flags = flags;
     if (plan_scratch_bytes(p, M, N, K) > kMax) return W4A16_ERR_WORKSPACE;
   }
   void* ws = nullptr;

@@ -47,7 +47,7 @@ constexpr int kBK = 64;
 constexpr int kLdsRow = 9;  // uint4 per LDS row: 8 octets + 1 pad
 constexpr int kGroupM = 4;  // M-tiles per group of the tile order
 
-template <int WMT, int WAVES_M, int WAVES_N, bool KTAIL>
+template <int WMT, int WAVES_M, int WAVES_N, bool KTAIL, bool AZ>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ bias, f16* __restrict__ Y, int M,
@@ -165,8 +165,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
     ColQ cq[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const ColQ2 p01 = make_colq2(st.sc[h].x, st.zr[h].x);
-      const ColQ2 p23 = make_colq2(st.sc[h].y, st.zr[h].y);
+      const ColQ2 p01 = make_colq2<AZ>(st.sc[h].x, st.zr[h].x);
+      const ColQ2 p23 = make_colq2<AZ>(st.sc[h].y, st.zr[h].y);
       cq[h][0] = colq_of<0>(p01);
       cq[h][1] = colq_of<1>(p01);
       cq[h][2] = colq_of<0>(p23);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         f16x2 d[4];
-        dq_word_fast(words[c], cq[s >> 1][c], mg, d);
+        dq_word_fast<AZ>(words[c], cq[s >> 1][c], mg, d);
         bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
       }
     };
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void mfma_kernel(
 // MFMAs.  B lane l of n-tile j is column 2*(l%32) + j of the wave's 64; the
 // epilogue stores 2 consecutive columns per lane.  One A register stage and two
 // B register stages; K must be a multiple of 128 (two steps per iteration).
-template <int WMT, int WAVES_M, int WAVES_N>
+template <int WMT, int WAVES_M, int WAVES_N, bool AZ>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                       const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
@@ -390,7 +390,7 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
     ColQ cq[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const ColQ2 q2 = make_colq2(st.sc[h], st.zr[h]);
+      const ColQ2 q2 = make_colq2<AZ>(st.sc[h], st.zr[h]);
       cq[h][0] = colq_of<0>(q2);
       cq[h][1] = colq_of<1>(q2);
     }
@@ -400,7 +400,7 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         f16x2 d[4];
-        dq_word_fast(words[c], cq[s >> 1][c], mg, d);
+        dq_word_fast<AZ>(words[c], cq[s >> 1][c], mg, d);
         bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
       }
     };
@@ -485,12 +485,12 @@ void mfma_occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW
   }
 }
 
-template <int WMT, int WAVES_M, int WAVES_N>
+template <int WMT, int WAVES_M, int WAVES_N, bool AZ>
 hipError_t launch_occ2(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 64 * WAVES_N;
   dim3 grid(((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((mfma_occ2_kernel<WMT, WAVES_M, WAVES_N>), grid,
+  hipLaunchKernelGGL((mfma_occ2_kernel<WMT, WAVES_M, WAVES_N, AZ>), grid,
                      dim3(64 * WAVES_M * WAVES_N), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
@@ -498,7 +498,7 @@ hipError_t launch_occ2(const GemmArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int WMT, int WAVES_M, int WAVES_N>
+template <int WMT, int WAVES_M, int WAVES_N, bool AZ>
 hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = 32 * WMT * WAVES_M;
   constexpr int BN = 128 * WAVES_N;
@@ -511,10 +511,10 @@ hipError_t launch_cfg(const GemmArgs& a, hipStream_t st) {
   const f16* bias = static_cast<const f16*>(a.bias);
   f16* y = static_cast<f16*>(a.y);
   if (a.K % kBK == 0)
-    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, false>), grid, block, 0, st, x, qw, sc,
+    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, false, AZ>), grid, block, 0, st, x, qw, sc,
                        zr, bias, y, a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   else
-    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, true>), grid, block, 0, st, x, qw, sc,
+    hipLaunchKernelGGL((mfma_kernel<WMT, WAVES_M, WAVES_N, true, AZ>), grid, block, 0, st, x, qw, sc,
                        zr, bias, y, a.M, a.N, a.K, a.G, a.ldx, a.ldy);
   return hipGetLastError();
 }
@@ -574,11 +574,13 @@ bool mfma_fits(int M, int N, int K, int G) { return operands_fit(M, N, K, G); }
 hipError_t launch_mfma(const GemmArgs& a, int cfg, int split, float* part, hipStream_t st) {
   if (split > 1 && !mfma_cfg_splits(cfg)) return hipErrorInvalidValue;
   switch (cfg) {
-    case 1: return launch_cfg<2, 2, 2>(a, st);
-    case 2: return launch_cfg<1, 1, 4>(a, st);
+    case 1:
+      return a.any_zeros ? launch_cfg<2, 2, 2, true>(a, st) : launch_cfg<2, 2, 2, false>(a, st);
+    case 2:
+      return a.any_zeros ? launch_cfg<1, 1, 4, true>(a, st) : launch_cfg<1, 1, 4, false>(a, st);
     case 6:
       if (a.K % (2 * kBK) != 0) return hipErrorInvalidValue;
-      return launch_occ2<4, 1, 4>(a, st);
+      return a.any_zeros ? launch_occ2<4, 1, 4, true>(a, st) : launch_occ2<4, 1, 4, false>(a, st);
     case 7: return launch_occ2_gemm(a, split, part, st);
     case 11: return launch_stream_gemm(a, 128, split, part, st);
     case 12: return launch_stream_gemm(a, 32, split, part, st);

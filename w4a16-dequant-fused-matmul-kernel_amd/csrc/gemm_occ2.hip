@@ -44,7 +44,7 @@ constexpr int kGroupM = 4;    // M-tiles per group of the tile order
 constexpr int kMT = 8;        // 16-row MFMA tiles per wave (128 rows)
 constexpr int kNTiles = 4;    // 16-column MFMA tiles per wave (64 columns)
 
-template <int WAVES_M, int WAVES_N, bool G64>
+template <int WAVES_M, int WAVES_N, bool G64, bool AZ>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
                  const uint16_t* __restrict__ SC, const uint16_t* __restrict__ ZR,
@@ -156,8 +156,8 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
     ColQ cq[NH][4];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
-      const ColQ2 p01 = make_colq2(st.sc[h].x, st.zr[h].x);
-      const ColQ2 p23 = make_colq2(st.sc[h].y, st.zr[h].y);
+      const ColQ2 p01 = make_colq2<AZ>(st.sc[h].x, st.zr[h].x);
+      const ColQ2 p23 = make_colq2<AZ>(st.sc[h].y, st.zr[h].y);
       cq[h][0] = colq_of<0>(p01);
       cq[h][1] = colq_of<1>(p01);
       cq[h][2] = colq_of<0>(p23);
@@ -176,7 +176,7 @@ void occ2_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW,
 #pragma unroll
       for (int c = 0; c < kNTiles; ++c) {
         f16x2 d[4];
-        dq_word_fast(words[c], c4[c], mg, d);
+        dq_word_fast<AZ>(words[c], c4[c], mg, d);
         bf[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
       }
       if (more) load_w(kt + 1, h, st);
@@ -297,15 +297,15 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
   *reinterpret_cast<f16x4*>(Y + row * (size_t)ldy + col) = o;
 }
 
-template <int WAVES_M, int WAVES_N, bool G64>
-hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
+template <int WAVES_M, int WAVES_N, bool G64, bool AZ>
+hipError_t launch_wgz(const GemmArgs& a, int split, float* part, hipStream_t st) {
   constexpr int BM = 16 * kMT * WAVES_M;
   constexpr int BN = 16 * kNTiles * WAVES_N;
   const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   const int KT = a.K / kBK;
   const int kts = (KT + split - 1) / split;
   const int nsplit = split > 1 ? (KT + kts - 1) / kts : 1;   // every split non-empty
-  hipLaunchKernelGGL((occ2_kernel<WAVES_M, WAVES_N, G64>), dim3(tiles * nsplit),
+  hipLaunchKernelGGL((occ2_kernel<WAVES_M, WAVES_N, G64, AZ>), dim3(tiles * nsplit),
                      dim3(64 * WAVES_M * WAVES_N), 0, st, static_cast<const f16*>(a.x),
                      reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                      static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.bias),
@@ -314,6 +314,13 @@ hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) 
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
+}
+
+// Zero-point form by the call (w4a16_device.h).
+template <int WAVES_M, int WAVES_N, bool G64>
+hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
+  return a.any_zeros ? launch_wgz<WAVES_M, WAVES_N, G64, true>(a, split, part, st)
+                     : launch_wgz<WAVES_M, WAVES_N, G64, false>(a, split, part, st);
 }
 
 }  // namespace

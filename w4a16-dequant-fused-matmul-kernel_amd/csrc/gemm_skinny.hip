@@ -66,7 +66,7 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // geo = row groups per column block | rows per group << 8 | group shift << 16;
 // k / G is (umulhi(k, gmagic) + k) >> shift (group_div), no division; the
 // grid size is nblk * mgs (no read of the dispatch packet).
-template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH>
+template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH, bool AZ>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, int M, int N, int K, uint32_t gmagic, uint32_t geo, int ldx,
@@ -220,9 +220,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
       for (int mt = 0; mt < MT; ++mt) xa[mt] = kXPerm ? perm_pairs(b.x[j][mt]) : b.x[j][mt];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const ColQ cq = make_colq(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
+        const ColQ cq = make_colq<AZ>(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
         f16x2 d[4];
-        dq_word_fast(b.w[j][t], cq, mg, d);
+        dq_word_fast<AZ>(b.w[j][t], cq, mg, d);
         // kXPerm: the words in pair order (w0 w4 w1 w5 w2 w6 w3 w7), the
         // activations permuted to match; else natural k order:
         // w0..w7 = d0.x d1.x d2.x d3.x d0.y d1.y d2.y d3.y
@@ -301,18 +301,18 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 // against 4 waves in the loop: K = N = 4096 M = 4 / 8 / 16: 6.40 / 6.78 /
 // 7.85 us -> 5.74 / 6.29 / 7.49; M = 16, N = 28672 (64 columns): 22.6 ->
 // 21.1; M = 8, K = 2048, N = 4096: 4.99 -> 4.55 with 8 waves.
-template <int MT, int GSTEP, int NT>
-hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
+template <int MT, int GSTEP, int NT, bool AZ>
+hipError_t launch_ntz(const GemmArgs& a, int rpg, hipStream_t st) {
   const int mgs = (a.M + rpg - 1) / rpg;
   const int nblk = (a.N + 16 * NT - 1) / (16 * NT);
   const int ks = a.K >> 5;
   // 16 waves hold 128 registers each: 64 rows with a scale / zero load per
   // step would spill there, and take the loop instead
   constexpr int k16 = MT == 4 && GSTEP == 1 ? 0 : 16;
-  auto k = ks <= 4 * kBatch     ? skinny_kernel<MT, GSTEP, 4, NT, true>
-           : ks <= 8 * kBatch   ? skinny_kernel<MT, GSTEP, 8, NT, true>
-           : ks <= k16 * kBatch ? skinny_kernel<MT, GSTEP, (k16 ? k16 : 4), NT, true>
-                                : skinny_kernel<MT, GSTEP, 4, NT, false>;
+  auto k = ks <= 4 * kBatch     ? skinny_kernel<MT, GSTEP, 4, NT, true, AZ>
+           : ks <= 8 * kBatch   ? skinny_kernel<MT, GSTEP, 8, NT, true, AZ>
+           : ks <= k16 * kBatch ? skinny_kernel<MT, GSTEP, (k16 ? k16 : 4), NT, true, AZ>
+                                : skinny_kernel<MT, GSTEP, 4, NT, false, AZ>;
   const int waves = ks <= 4 * kBatch ? 4 : ks <= 8 * kBatch ? 8 : ks <= k16 * kBatch ? k16 : 4;
   const GroupDiv gd = group_div(a.G);
   const uint32_t geo = (uint32_t)mgs | ((uint32_t)rpg << 8) | ((uint32_t)gd.shift << 16);
@@ -322,6 +322,14 @@ hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
                      a.N, a.K, gd.magic, geo, a.ldx, a.ldy, static_cast<const f16*>(a.bias),
                      static_cast<f16*>(a.y));
   return hipGetLastError();
+}
+
+// Zero-point form by the call (w4a16_device.h): the kernels for integer zeros
+// or those for any fp16 zero.
+template <int MT, int GSTEP, int NT>
+hipError_t launch_nt(const GemmArgs& a, int rpg, hipStream_t st) {
+  return a.any_zeros ? launch_ntz<MT, GSTEP, NT, true>(a, rpg, st)
+                     : launch_ntz<MT, GSTEP, NT, false>(a, rpg, st);
 }
 
 template <int MT, int GSTEP>

@@ -80,7 +80,8 @@ __device__ __forceinline__ void tile_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Per column: zz = (1024 + zero, 64 + zero) as (low, high) halves, s = scale.
+// Per column: zz = (1024 + zero, 64 + zero) as (low, high) halves, s = scale
+// (AZ: zz = (zero, zero)).
 struct ColN {
   f16x2 zz;
   f16 s;
@@ -90,15 +91,23 @@ struct ColN {
 // v_perm_b32 copies byte i (nibbles 2i, 2i+1) into bytes 0 and 2; the mask
 // keeps nibble 2i in bits [0,4) and nibble 2i+1 in bits [20,24), which the
 // magic word 0x54006400 turns into the fp16 pair (1024 + q_2i, 64 + q_2i+1).
-// Subtracting zz is exact for integer zero-points in [-63, 63], so the result
-// is fp16(q - z) * s with one RNE rounding, as in the reference.
+// Subtracting zz is exact for integer zero-points with |z| <= 1024, so the
+// result is fp16(q - z) * s with one RNE rounding, as in the reference.  AZ
+// (any fp16 zero): the magic word, which is also the fp16 pair (1024, 64), is
+// subtracted first (exact: the codes), then the zero with the reference's
+// rounding of fp16(q) - z.
+template <bool AZ>
 __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t magic_mix,
                                             f16x2 d[4]) {
   const f16x2 s2 = f16x2{c.s, c.s};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t t = __builtin_amdgcn_perm(w, w, 0x01010101u * (uint32_t)i);
-    d[i] = (as_h2(and_or(t, 0x00F0000Fu, magic_mix)) - c.zz) * s2;
+    const f16x2 p = as_h2(and_or(t, 0x00F0000Fu, magic_mix));
+    if constexpr (AZ)
+      d[i] = ((p - as_h2(magic_mix)) - c.zz) * s2;
+    else
+      d[i] = (p - c.zz) * s2;
   }
 }
 
@@ -122,7 +131,7 @@ __device__ __forceinline__ void dq_word_nat(uint32_t w, const ColN& c, uint32_t 
 // -amdgpu-kernarg-preload-count), so those loads wait for no kernel-argument
 // load, and the rest are loaded meanwhile.  The grid size is an argument
 // rather than a read of the dispatch packet.
-template <int kMT, bool kSZ1, int kKS = 1>
+template <int kMT, bool kSZ1, int kKS = 1, bool AZ = false>
 __global__ __launch_bounds__(kNT * kKS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW, int M, int N,
                    int K, int KTS, int ldx, int nb, const char* __restrict__ SZ, uint32_t gmagic,
@@ -283,16 +292,18 @@ void stream_kernel(const f16* __restrict__ X, const uint32_t* __restrict__ QW, i
     in.z = make_uint2(c.z, c.w);
   };
   auto dequant = [&](const In& in, f16x8 (&b)[kNTiles]) {
-    const f16x2 zm = f16x2{(f16)1024.0f, (f16)64.0f};
+    const f16x2 zm = AZ ? f16x2{} : f16x2{(f16)1024.0f, (f16)64.0f};
     const f16x2 z01 = as_h2(in.z.x), z23 = as_h2(in.z.y);
     const f16x2 s01 = as_h2(in.s.x), s23 = as_h2(in.s.y);
-    const ColN cn[4] = {{f16x2{z01.x, z01.x} + zm, s01.x}, {f16x2{z01.y, z01.y} + zm, s01.y},
-                        {f16x2{z23.x, z23.x} + zm, s23.x}, {f16x2{z23.y, z23.y} + zm, s23.y}};
+    const f16x2 zz[4] = {f16x2{z01.x, z01.x}, f16x2{z01.y, z01.y}, f16x2{z23.x, z23.x},
+                         f16x2{z23.y, z23.y}};
+    const ColN cn[4] = {{AZ ? zz[0] : zz[0] + zm, s01.x}, {AZ ? zz[1] : zz[1] + zm, s01.y},
+                        {AZ ? zz[2] : zz[2] + zm, s23.x}, {AZ ? zz[3] : zz[3] + zm, s23.y}};
     const uint32_t words[4] = {in.w.x, in.w.y, in.w.z, in.w.w};
 #pragma unroll
     for (int c = 0; c < kNTiles; ++c) {
       f16x2 d[4];
-      dq_word_nat(words[c], cn[c], magic_mix, d);
+      dq_word_nat<AZ>(words[c], cn[c], magic_mix, d);
       b[c] = f16x8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
     }
   };
@@ -483,7 +494,7 @@ int split_steps(int K, int split, int slices) {
   return ((KT + split - 1) / split + unit - 1) / unit * unit;
 }
 
-template <int kMT, bool kSZ1, int kKS>
+template <int kMT, bool kSZ1, int kKS, bool AZ>
 hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t st) {
   constexpr int kBM = 16 * kMT;
   const int tiles = ((a.N + kBN - 1) / kBN) * ((a.M + kBM - 1) / kBM);
@@ -501,7 +512,7 @@ hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t 
   const uint32_t sz_bytes = (uint32_t)((sc < zr ? zr : sc) - base) +
                             (uint32_t)(a.K / a.G) * (uint32_t)a.N * 2u;
   const GroupDiv gd = group_div(a.G);
-  hipLaunchKernelGGL((stream_kernel<kMT, kSZ1, kKS>), dim3(tiles * nsplit), dim3(kNT * kKS), 0, st,
+  hipLaunchKernelGGL((stream_kernel<kMT, kSZ1, kKS, AZ>), dim3(tiles * nsplit), dim3(kNT * kKS), 0, st,
                      static_cast<const f16*>(a.x), reinterpret_cast<const uint32_t*>(a.qw), a.M, a.N,
                      a.K, nsplit > 1 ? kts : kts1, a.ldx, tiles * nsplit, base, gd.magic, gd.shift,
                      (uint32_t)(sc - base), (uint32_t)(zr - base), sz_bytes, a.G, a.ldy,
@@ -512,10 +523,16 @@ hipError_t launch_kernel(const GemmArgs& a, int split, float* part, hipStream_t 
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, nsplit, st);
 }
 
+template <int kMT, int kKS, bool AZ>
+hipError_t launch_wz(const GemmArgs& a, int split, float* part, hipStream_t st) {
+  return a.G % (2 * 32) == 0 ? launch_kernel<kMT, true, kKS, AZ>(a, split, part, st)
+                             : launch_kernel<kMT, false, kKS, AZ>(a, split, part, st);
+}
+
 template <int kMT, int kKS = 1>
 hipError_t launch_wg(const GemmArgs& a, int split, float* part, hipStream_t st) {
-  return a.G % (2 * 32) == 0 ? launch_kernel<kMT, true, kKS>(a, split, part, st)
-                             : launch_kernel<kMT, false, kKS>(a, split, part, st);
+  return a.any_zeros ? launch_wz<kMT, kKS, true>(a, split, part, st)
+                     : launch_wz<kMT, kKS, false>(a, split, part, st);
 }
 
 }  // namespace

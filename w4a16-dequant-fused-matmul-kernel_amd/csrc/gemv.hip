@@ -162,7 +162,7 @@ __device__ __forceinline__ void gemv_sum_waves_store(float (&red)[WAVES][MT][4 *
 // Arguments: the first fourteen SGPRs' worth (preloaded by the dispatch, as for
 // gemv_direct_kernel) are what the first loads need; the grid size is
 // nblk * S, computed rather than read from the dispatch packet.
-template <int MT, int CWL, int WAVES, bool STAGE, bool MF, int QPL>
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF, int QPL, bool AZ>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
@@ -203,15 +203,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   // batch (K % 32 == 0, splits and chunks in whole batches), so a batch is
   // wholly inside or wholly past it, and a batch past it loads zero words,
   // scales and zeros (out-of-range offsets): its weights dequantise to exactly
-  // 0, and its activation index is clamped to a zero row (so 0 * x never
-  // meets an inf or NaN of another row).  The per-row branch had put every
+  // 0, and its rows read BR zero rows of X (so 0 * x never meets an inf or
+  // NaN of another row; a run of an odd number of batches above one also
+  // processes the batch after its end, whose rows belong to the next
+  // row-lane).  The batch's first row picks its LDS rows, so each row's read
+  // keeps the row offset in the instruction's immediate.  The per-row branch had put every
   // row's dequant under an exec mask and the next batch's loads between them:
   // measured on MI355X without it, M = 1, K = 8192, N = 28672 on 128-column
   // blocks 27.0 -> 25.6 us, K = 4096 16.0 -> 15.4, M = 2 30.2 -> 29.2, N = 16384
   // on 64-column blocks 10.4 -> 9.8; on 16-column blocks (never staged by the
-  // planner) it measured slower.  XS: per m, CHUNK staged rows and that zero row.
+  // planner) it measured slower.  XS: per m, CHUNK staged rows and BR zero rows.
   constexpr bool kBranchFree = MT <= 2 && CWL >= 16;
-  constexpr int XS = kBranchFree ? CHUNK + 1 : CHUNK;
+  constexpr int XS = kBranchFree ? CHUNK + BR : CHUNK;
   __shared__ uint4 xs[MT * XS];
   __shared__ float red[WAVES][MT][CW];
 
@@ -301,26 +304,28 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   };
 
   auto process = [&](const Batch& b, int r0, int le, int c0) {
+    // LDS row of the batch's first row: the zero rows for a batch past `le`
+    const int xb = kBranchFree && r0 >= le ? CHUNK : r0 - c0;
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       if constexpr (MF) {
 #pragma unroll
         for (int q = 0; q < QPL; ++q) {
-          const ColQ2 p01 = make_colq2(b.s[h][q].x, b.z[h][q].x);
-          const ColQ2 p23 = make_colq2(b.s[h][q].y, b.z[h][q].y);
+          const ColQ2 p01 = make_colq2<AZ>(b.s[h][q].x, b.z[h][q].x);
+          const ColQ2 p23 = make_colq2<AZ>(b.s[h][q].y, b.z[h][q].y);
           const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
 #pragma unroll
           for (int uu = 0; uu < RH; ++uu) {
             const int u = h * RH + uu;
-            const int r = r0 + u;
+
             f16x2 d[4][4];
-            dq_word_fast(b.w[u][q].x, cq4[0], mg, d[0]);
-            dq_word_fast(b.w[u][q].y, cq4[1], mg, d[1]);
-            dq_word_fast(b.w[u][q].z, cq4[2], mg, d[2]);
-            dq_word_fast(b.w[u][q].w, cq4[3], mg, d[3]);
+            dq_word_fast<AZ>(b.w[u][q].x, cq4[0], mg, d[0]);
+            dq_word_fast<AZ>(b.w[u][q].y, cq4[1], mg, d[1]);
+            dq_word_fast<AZ>(b.w[u][q].z, cq4[2], mg, d[2]);
+            dq_word_fast<AZ>(b.w[u][q].w, cq4[3], mg, d[3]);
             // both operands in pair order: (w0 w4 w1 w5 w2 w6 w3 w7) against
             // the activations permuted the same way when they were staged
-            const uint4 xp = xs[xrow * XS + min(r - c0, CHUNK)];
+            const uint4 xp = xs[xrow * XS + xb + u];
 #pragma unroll
             for (int c = 0; c < 4; ++c)
               macc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -332,8 +337,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         }
         continue;
       }
-      const ColQ2 p01 = make_colq2(b.s[h][0].x, b.z[h][0].x);
-      const ColQ2 p23 = make_colq2(b.s[h][0].y, b.z[h][0].y);
+      const ColQ2 p01 = make_colq2<AZ>(b.s[h][0].x, b.z[h][0].x);
+      const ColQ2 p23 = make_colq2<AZ>(b.s[h][0].y, b.z[h][0].y);
       const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
 #pragma unroll
       for (int uu = 0; uu < RH; ++uu) {
@@ -341,13 +346,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         const int r = r0 + u;
         if (!kBranchFree && r >= le) break;
         f16x2 d[4][4];
-        dq_word_fast(b.w[u][0].x, cq4[0], mg, d[0]);
-        dq_word_fast(b.w[u][0].y, cq4[1], mg, d[1]);
-        dq_word_fast(b.w[u][0].z, cq4[2], mg, d[2]);
-        dq_word_fast(b.w[u][0].w, cq4[3], mg, d[3]);
+        dq_word_fast<AZ>(b.w[u][0].x, cq4[0], mg, d[0]);
+        dq_word_fast<AZ>(b.w[u][0].y, cq4[1], mg, d[1]);
+        dq_word_fast<AZ>(b.w[u][0].z, cq4[2], mg, d[2]);
+        dq_word_fast<AZ>(b.w[u][0].w, cq4[3], mg, d[3]);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const uint4 xp = xs[m * XS + (kBranchFree ? min(r - c0, CHUNK) : r - c0)];
+          const uint4 xp = xs[m * XS + xb + u];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             float a = acc[m][c];
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
         if (idx < MT * CHUNK) xs[(idx / CHUNK) * XS + idx % CHUNK] = perm_pairs(xv[i]);
       }
       if constexpr (XS > CHUNK) {
-        if (tid < MT) xs[tid * XS + CHUNK] = make_uint4(0u, 0u, 0u, 0u);
+        if (tid < MT * BR) xs[(tid / BR) * XS + CHUNK + tid % BR] = make_uint4(0u, 0u, 0u, 0u);
       }
       __syncthreads();
     }
@@ -485,7 +490,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
 // pole: cold HBM, most of the bytes).  Measured on MI355X, C2 (16 waves, two
 // slots per lane, one batch), medians of 7 interleaved runs: 4.81-4.85 us
 // with contiguous runs per lane, 4.68-4.70 with sweeps.
-template <int MT, int CWL, int WAVES, bool ONE_BATCH, bool SPLIT>
+template <int MT, int CWL, int WAVES, bool ONE_BATCH, bool SPLIT, bool AZ>
 __device__ __forceinline__ void gemv_direct_body(
     const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
@@ -587,13 +592,14 @@ __device__ __forceinline__ void gemv_direct_body(
   auto process = [&](const Batch& bt) {
 #pragma unroll
     for (int i = 0; i < BR; ++i) {
-      const ColQ2 p01 = make_colq2(bt.s[i].x, bt.z[i].x), p23 = make_colq2(bt.s[i].y, bt.z[i].y);
+      const ColQ2 p01 = make_colq2<AZ>(bt.s[i].x, bt.z[i].x);
+      const ColQ2 p23 = make_colq2<AZ>(bt.s[i].y, bt.z[i].y);
       const ColQ cq4[4] = {colq_of<0>(p01), colq_of<1>(p01), colq_of<0>(p23), colq_of<1>(p23)};
       f16x2 d[4][4];
-      dq_word_fast(bt.w[i].x, cq4[0], mg, d[0]);
-      dq_word_fast(bt.w[i].y, cq4[1], mg, d[1]);
-      dq_word_fast(bt.w[i].z, cq4[2], mg, d[2]);
-      dq_word_fast(bt.w[i].w, cq4[3], mg, d[3]);
+      dq_word_fast<AZ>(bt.w[i].x, cq4[0], mg, d[0]);
+      dq_word_fast<AZ>(bt.w[i].y, cq4[1], mg, d[1]);
+      dq_word_fast<AZ>(bt.w[i].z, cq4[2], mg, d[2]);
+      dq_word_fast<AZ>(bt.w[i].w, cq4[3], mg, d[3]);
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         uint4 xo4 = bt.x[m * BR + i];
@@ -642,32 +648,32 @@ __device__ __forceinline__ void gemv_direct_body(
 
 // Unsplit launches: the first fourteen SGPRs of arguments (preloaded) are what
 // the first batch's loads need.
-template <int MT, int CWL, int WAVES, bool ONE_BATCH>
+template <int MT, int CWL, int WAVES, bool ONE_BATCH, bool AZ>
 __global__ __launch_bounds__(64 * WAVES) void gemv_direct_kernel(
     const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, const f16* __restrict__ X, int N, int K, int rows_per_wg,
     int nb, uint32_t gmagic, int gshift, int ldx, int ldy, const f16* __restrict__ bias,
     f16* __restrict__ Y) {
-  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, false>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
+  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, false, AZ>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
                                                      gmagic, gshift, 0u, 0, ldx, ldy, bias, Y,
                                                      nullptr);
 }
 
 // Split launches: the block reciprocal joins the preloaded arguments, X
 // follows them.
-template <int MT, int CWL, int WAVES, bool ONE_BATCH>
+template <int MT, int CWL, int WAVES, bool ONE_BATCH, bool AZ>
 __global__ __launch_bounds__(64 * WAVES) void gemv_direct_split_kernel(
     const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, int N, int K, int rows_per_wg, int nb, uint32_t bmagic,
     int bshift, uint32_t gmagic, int gshift, const f16* __restrict__ X, int ldx,
     float* __restrict__ part) {
-  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, true>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
+  gemv_direct_body<MT, CWL, WAVES, ONE_BATCH, true, AZ>(QW, SC, ZR, X, N, K, rows_per_wg, nb,
                                                     gmagic, gshift, bmagic, bshift, ldx, 0,
                                                     nullptr, nullptr, part);
 }
 
-template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false, int QPL = 1>
-hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF, int QPL, bool AZ>
+hipError_t launch_cwlz(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   constexpr int CW = 4 * CWL * QPL;
   const int nblk = (a.N + CW - 1) / CW;
   const int rows = gemv_rows_per_split(a.K, split);
@@ -683,20 +689,20 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
     const uint16_t* zr = static_cast<const uint16_t*>(a.zr);
     const f16* x = static_cast<const f16*>(a.x);
     if (split == 1) {
-      auto kern = one ? gemv_direct_kernel<MT, CWL, WAVES, true>
-                      : gemv_direct_kernel<MT, CWL, WAVES, false>;
+      auto kern = one ? gemv_direct_kernel<MT, CWL, WAVES, true, AZ>
+                      : gemv_direct_kernel<MT, CWL, WAVES, false, AZ>;
       hipLaunchKernelGGL(kern, grid, block, 0, st, qw, sc, zr, x, a.N, a.K, rows, nblk, gd.magic,
                          gd.shift, a.ldx, a.ldy, static_cast<const f16*>(a.bias),
                          static_cast<f16*>(a.y));
     } else {
-      auto kern = one ? gemv_direct_split_kernel<MT, CWL, WAVES, true>
-                      : gemv_direct_split_kernel<MT, CWL, WAVES, false>;
+      auto kern = one ? gemv_direct_split_kernel<MT, CWL, WAVES, true, AZ>
+                      : gemv_direct_split_kernel<MT, CWL, WAVES, false, AZ>;
       const GroupDiv bd = group_div(nblk);
       hipLaunchKernelGGL(kern, grid, block, 0, st, qw, sc, zr, a.N, a.K, rows, nblk * split,
                          bd.magic, bd.shift, gd.magic, gd.shift, x, a.ldx, part);
     }
   } else
-    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF, QPL>), dim3(nblk * split),
+    hipLaunchKernelGGL((gemv_kernel<MT, CWL, WAVES, STAGE, MF, QPL, AZ>), dim3(nblk * split),
                        dim3(GemvShape<WAVES>::kThreads), 0, st,
                        reinterpret_cast<const uint32_t*>(a.qw), static_cast<const uint16_t*>(a.sc),
                        static_cast<const uint16_t*>(a.zr), static_cast<const f16*>(a.x), a.N, a.K,
@@ -705,6 +711,14 @@ hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
   return launch_splitk_reduce(part, a.bias, a.y, a.M, a.N, a.ldy, split, st);
+}
+
+// Zero-point form by the call (w4a16_device.h): the kernels for integer zeros
+// or those for any fp16 zero.
+template <int MT, int CWL, int WAVES, bool STAGE, bool MF = false, int QPL = 1>
+hipError_t launch_cwl(const GemmArgs& a, int split, void* ws, hipStream_t st) {
+  return a.any_zeros ? launch_cwlz<MT, CWL, WAVES, STAGE, MF, QPL, true>(a, split, ws, st)
+                     : launch_cwlz<MT, CWL, WAVES, STAGE, MF, QPL, false>(a, split, ws, st);
 }
 
 template <int MT, int WAVES, bool STAGE>

@@ -298,6 +298,20 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
   }
 }
 
+// Zero-points outside the integer-zero kernels' domain (w4a16_device.h): any
+// zero that is not an integer in [-1024, 1024] (NaN and infinities included)
+// sets *flag.  Grid-stride over the n halves; every offending lane stores 1.
+__global__ __launch_bounds__(256) void zeros_check_kernel(const f16* __restrict__ Z, int64_t n,
+                                                          int32_t* __restrict__ flag) {
+  bool bad = false;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const float z = (float)Z[i];
+    bad |= !(z == __builtin_rintf(z) && __builtin_fabsf(z) <= 1024.0f);
+  }
+  if (bad) *flag = 1;
+}
+
 template <class IN>
 hipError_t quantize_launch(const void* W, int32_t* qw, void* sc, void* zr, int K, int N, int G,
                            int32_t* flag, hipStream_t st) {
@@ -347,6 +361,13 @@ hipError_t launch_unpack(const int32_t* qw, int32_t* q, int K, int N, hipStream_
   dim3 grid(K / 8, (N + 255) / 256);
   hipLaunchKernelGGL(unpack_kernel, grid, dim3(256), 0, st,
                      reinterpret_cast<const uint32_t*>(qw), q, K, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_zeros_check(const void* zr, int64_t n, int32_t* flag, hipStream_t st) {
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(zeros_check_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256),
+                     0, st, static_cast<const f16*>(zr), n, flag);
   return hipGetLastError();
 }
 

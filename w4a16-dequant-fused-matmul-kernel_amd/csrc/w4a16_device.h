@@ -3,8 +3,19 @@
 // Storage format (reference w4a16-kernel/src/w4a16/quant.py:1-30, W4A16_SPEC.md:109-171):
 //   qweight int32 [K/8, N]: word (i, n) holds codes for rows k = 8i + j, j = 0..7,
 //                           code j in bits [4j, 4j+4), unsigned.
-//   scales  fp16  [K/G, N], zeros fp16 [K/G, N] (integer zero-points).
-//   W_dq[k, n] = fp16((fp16(q) - z) * s)  (quant.py:173-177).
+//   scales  fp16  [K/G, N], zeros fp16 [K/G, N].
+//   W_dq[k, n] = fp16(fp16(fp16(q) - z) * s)  (quant.py:173-177).
+//
+// Zero-points.  The fused kernels are instantiated twice over a template flag
+// AZ ("any zero"):
+//   AZ = false: every zero is an integer with |z| <= 1024 (quantize_weight
+//     makes 0..15).  Then 1024 + z and 64 + z are fp16 numbers, so one
+//     subtract of the magic-biased zero from the magic-biased code gives q - z
+//     exactly and one multiply rounds once, as the reference's two roundings
+//     do when q - z is exact.
+//   AZ = true: any fp16 zero.  The magic is subtracted first (exact: the code
+//     q as fp16), then z with the reference's own RNE rounding of fp16(q) - z,
+//     then the multiply: one more packed subtract per pair of weights.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,18 +39,20 @@ __device__ __forceinline__ uint16_t as_u16(f16 h) { return __builtin_bit_cast(ui
 //   s  = (scale, scale)
 //   z0 = (1024 + zero, 1024 + zero)   pairs built from nibbles at bits [0,4) of a half
 //   z1 = (  64 + zero,   64 + zero)   pairs built from nibbles at bits [4,8) of a half
+//   (AZ: z0 = z1 = (zero, zero))
 // OR-ing a nibble q into the mantissa of fp16 1024 (0x6400) gives exactly 1024 + q;
 // OR-ing q << 4 into fp16 64 (0x5400) gives exactly 64 + q.  Subtracting 1024 + z
-// (or 64 + z) is then exact for integer zero-points in [-63, 63], so
+// (or 64 + z) is then exact for integer zero-points with |z| <= 1024, so
 // (p - z0) * s == fp16(q - z) * s with a single RNE rounding, as in the reference.
 struct ColQ {
   f16x2 s, z0, z1;
 };
 
+template <bool AZ = false>
 __device__ __forceinline__ ColQ make_colq(uint16_t sbits, uint16_t zbits) {
   const f16 s = as_h(sbits), z = as_h(zbits);
-  const f16 a = (f16)1024.0f + z;
-  const f16 b = (f16)64.0f + z;
+  const f16 a = AZ ? z : (f16)1024.0f + z;
+  const f16 b = AZ ? z : (f16)64.0f + z;
   ColQ c;
   c.s = f16x2{s, s};
   c.z0 = f16x2{a, a};
@@ -50,15 +63,21 @@ __device__ __forceinline__ ColQ make_colq(uint16_t sbits, uint16_t zbits) {
 // Two columns' scale/zero state, packed: lane c of each pair is column c.
 // Used through colq_of<c>(), whose broadcasts fold into the packed ops' op_sel.
 struct ColQ2 {
-  f16x2 s, za, zb;   // scales, 1024 + zeros, 64 + zeros
+  f16x2 s, za, zb;   // scales, 1024 + zeros, 64 + zeros (AZ: zeros, zeros)
 };
 
+template <bool AZ = false>
 __device__ __forceinline__ ColQ2 make_colq2(uint32_t sbits2, uint32_t zbits2) {
   const f16x2 z = as_h2(zbits2);
   ColQ2 q;
   q.s = as_h2(sbits2);
-  q.za = z + f16x2{(f16)1024.0f, (f16)1024.0f};
-  q.zb = z + f16x2{(f16)64.0f, (f16)64.0f};
+  if constexpr (AZ) {
+    q.za = z;
+    q.zb = z;
+  } else {
+    q.za = z + f16x2{(f16)1024.0f, (f16)1024.0f};
+    q.zb = z + f16x2{(f16)64.0f, (f16)64.0f};
+  }
   return q;
 }
 
@@ -92,31 +111,28 @@ __device__ __forceinline__ MagicRegs make_magic() {
   return m;
 }
 
-// As dq_word with the unpack done in five instructions (one shift, four
-// v_and_or_b32); same results bit for bit.
-__device__ __forceinline__ void dq_word_fast(uint32_t w, const ColQ& c, const MagicRegs& mg,
-                                             f16x2 d[4]) {
-  const uint32_t t = w >> 8;
-  d[0] = (as_h2(and_or(w, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
-  d[1] = (as_h2(and_or(w, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
-  d[2] = (as_h2(and_or(t, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
-  d[3] = (as_h2(and_or(t, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
-}
-
 // Dequantise one packed word into four fp16 pairs in "pair order":
 //   d[0] = (w0, w4), d[1] = (w1, w5), d[2] = (w2, w6), d[3] = (w3, w7)
 // where w_j is the weight of row 8i + j.  Consumers permute the activations the
-// same way, so the dot products see matching k.
-__device__ __forceinline__ void dq_word(uint32_t w, const ColQ& c, f16x2 d[4]) {
+// same way, so the dot products see matching k.  The unpack takes five
+// instructions (one shift, four v_and_or_b32); the magic words are also the
+// fp16 pairs (1024, 1024) and (64, 64) that AZ subtracts first.
+template <bool AZ = false>
+__device__ __forceinline__ void dq_word_fast(uint32_t w, const ColQ& c, const MagicRegs& mg,
+                                             f16x2 d[4]) {
   const uint32_t t = w >> 8;
-  const uint32_t p0 = (w & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p1 = (w & 0x00F000F0u) | 0x54005400u;
-  const uint32_t p2 = (t & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p3 = (t & 0x00F000F0u) | 0x54005400u;
-  d[0] = (as_h2(p0) - c.z0) * c.s;
-  d[1] = (as_h2(p1) - c.z1) * c.s;
-  d[2] = (as_h2(p2) - c.z0) * c.s;
-  d[3] = (as_h2(p3) - c.z1) * c.s;
+  if constexpr (AZ) {
+    const f16x2 a = as_h2(mg.m1024), b = as_h2(mg.m64);
+    d[0] = ((as_h2(and_or(w, 0x000F000Fu, mg.m1024)) - a) - c.z0) * c.s;
+    d[1] = ((as_h2(and_or(w, 0x00F000F0u, mg.m64)) - b) - c.z1) * c.s;
+    d[2] = ((as_h2(and_or(t, 0x000F000Fu, mg.m1024)) - a) - c.z0) * c.s;
+    d[3] = ((as_h2(and_or(t, 0x00F000F0u, mg.m64)) - b) - c.z1) * c.s;
+  } else {
+    d[0] = (as_h2(and_or(w, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
+    d[1] = (as_h2(and_or(w, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
+    d[2] = (as_h2(and_or(t, 0x000F000Fu, mg.m1024)) - c.z0) * c.s;
+    d[3] = (as_h2(and_or(t, 0x00F000F0u, mg.m64)) - c.z1) * c.s;
+  }
 }
 
 // Permute eight consecutive fp16 activations x0..x7 (four dwords, natural order)

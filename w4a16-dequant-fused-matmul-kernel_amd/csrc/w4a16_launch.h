@@ -33,6 +33,9 @@ struct GemmArgs {
   int M, N, K, G;
   int ldx, ldy;         // row strides (>= K, >= N); the vector kernels need
                         // ldx % 8 == 0 and ldy % 4 == 0 (16- / 8-byte rows)
+  bool any_zeros = false;   // zeros may be any fp16 value: the fused kernels'
+                            // AZ forms (w4a16_device.h); else integers with
+                            // |z| <= 1024
 };
 
 // Bytes from the first element of x to one past its last: (M - 1) ldx + K
@@ -131,5 +134,7 @@ hipError_t launch_pack(const int32_t* q, int32_t* qw, int K, int N, int32_t* fla
 hipError_t launch_unpack(const int32_t* qw, int32_t* q, int K, int N, hipStream_t st);
 hipError_t launch_dequant(const int32_t* qw, const void* sc, const void* zr, void* w, int K,
                           int N, int G, hipStream_t st);
+// flag <- 1 if any of the n fp16 zeros is not an integer in [-1024, 1024].
+hipError_t launch_zeros_check(const void* zr, int64_t n, int32_t* flag, hipStream_t st);
 
 }  // namespace w4a16

@@ -4,9 +4,6 @@
 
 The library's sources under ``csrc/`` are compiled for gfx950 only, then linked
 into ``w4a16/libw4a16.so`` next to this file, where :mod:`w4a16._lib` loads it.
-``csrc/floor_probe.hip`` (bench.py's loads-only probe of the decode GEMV's
-access shapes) is linked on its own into ``w4a16/libw4a16_floor_probe.so``;
-nothing in the library uses it.
 """
 from __future__ import annotations
 
@@ -22,8 +19,6 @@ ROOT_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT_DIR, "csrc")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libw4a16.so")
-PROBE_SOURCE = "floor_probe.hip"
-PROBE_LIB_PATH = os.path.join(PKG_DIR, "libw4a16_floor_probe.so")
 SOURCES = ["gemv.hip", "gemm_mfma.hip", "gemm_occ2.hip", "gemm_stream.hip", "gemm_skinny.hip",
            "simt.hip", "quant.hip", "capi.cpp"]
 HEADERS = ["w4a16_device.h", "w4a16_launch.h"]
@@ -67,7 +62,6 @@ SOURCE_FLAGS = {
     "gemm_skinny.hip": _PRELOAD,
     "gemm_stream.hip": _PRELOAD,
     "gemm_occ2.hip": _PRELOAD,   # and the split-K reduction kernel
-    "floor_probe.hip": _PRELOAD,  # the probe's floors start like the kernels they bound
 }
 
 
@@ -106,17 +100,13 @@ def _link(objs: list[str], path: str, verbose: bool) -> None:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every source and link libw4a16.so (and the floor probe's
-    library); returns the library path."""
+    """Compile every source and link libw4a16.so; returns the library path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    jobs = jobs or min(len(SOURCES) + 1, os.cpu_count() or 1, 8)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
     defines = [f'-DW4A16_SOURCE_HASH="{source_hash()}"']
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        probe = ex.submit(_compile, PROBE_SOURCE, verbose, [])
         objs = list(ex.map(lambda s: _compile(s, verbose, defines), SOURCES))
-        probe_obj = probe.result()
     _link(objs, LIB_PATH, verbose)
-    _link([probe_obj], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

@@ -14,7 +14,7 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a16.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum w4a16_kernel
 KERNEL_AUTO, KERNEL_GEMV, KERNEL_MFMA, KERNEL_SIMT, KERNEL_SKINNY = 0, 1, 2, 3, 4
@@ -26,6 +26,8 @@ MFMA_SPLIT_CONFIGS = (7, 11, 12, 13, 14)
 GEMV_CONFIGS = (1, 2, 4, 5)          # 8 / 16 waves, + LDS-staged activations (M <= 2)
 GEMV_MFMA_CONFIGS = (6, 7)           # 16 / 8 waves, staged, MFMA dot products (M <= 2, 64 / 128 columns)
 SKINNY_CONFIGS = (0, 2, 3)           # 16 / 32 / 64-column blocks
+# w4a16_plan.flags: W4A16_PLAN_ANY_ZEROS (zeros other than integers in [-1024, 1024])
+PLAN_ANY_ZEROS = 1
 # W4A16_NOALLOC_SCRATCH_BYTES: the static scratch of w4a16_gemm_f16_noalloc
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
@@ -53,6 +55,7 @@ class Plan(ctypes.Structure):
         ("grid_x", ctypes.c_int64),
         ("grid_y", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_int64),
+        ("flags", ctypes.c_int32),
     ]
 
     def as_dict(self) -> dict:
@@ -74,6 +77,7 @@ SIGNATURES = {
     "w4a16_status_string": (ctypes.c_char_p, [_int]),
     "w4a16_gemm_plan": (_int, [_i64, _i64, _i64, _i64, _i32, _i32, ctypes.POINTER(Plan)]),
     "w4a16_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "w4a16_zeros_check_f16": (_int, [_vp, _i64, _vp, _vp]),
     "w4a16_gemm_f16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
     "w4a16_linear_f16": (
         _int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),

@@ -24,6 +24,13 @@ wrapper asserts contiguity (:170-173); any other layout raises the same
 Group size: the reference's Triton path needs every autotune BLOCK_K to divide
 G (:177-182), i.e. G % 64 == 0.  These kernels need G % 32 == 0, so G = 32 works
 here as well; G = 8 still raises AssertionError like the reference.
+
+Zero-points: the reference dequantises ``(q - z) * s`` in fp16 for any fp16
+zero (:117-119).  The fused kernels have two forms: one for integer zeros
+with |z| <= 1024 (what quantize_weight makes, 0..15) and one for any zero (one
+more fp16 subtract per pair of weights).  Each zeros tensor is checked once on
+the GPU (``w4a16_zeros_check_f16``); the result is kept on the tensor with
+its version counter, so an in-place change is checked again.
 """
 from __future__ import annotations
 
@@ -35,7 +42,7 @@ from torch import Tensor
 from . import _lib
 from . import _runtime as rt
 
-__all__ = ["w4a16_matmul", "w4a16_linear", "plan_for", "GROUP_MULTIPLE"]
+__all__ = ["w4a16_matmul", "w4a16_linear", "plan_for", "GROUP_MULTIPLE", "zeros_need_any_form"]
 
 GROUP_MULTIPLE = 32
 
@@ -80,9 +87,50 @@ def _row_stride(t: Tensor) -> int:
     return t.stride(0) if t.shape[0] > 1 else t.shape[1]
 
 
+_ZKEY = "_w4a16_zeros_checked"
+
+
+def zeros_need_any_form(zeros: Tensor) -> bool:
+    """Whether `zeros` holds a value the integer-zero kernels cannot take (not an
+    integer in [-1024, 1024]).  Checked on the GPU once per tensor version and
+    kept on the tensor; under HIP-graph capture, where the answer cannot be read
+    back, an unchecked tensor is taken to need the any-zero form (exact for
+    every zero)."""
+    key = (zeros._version, zeros.data_ptr(), zeros.numel(), zeros.device)
+    hit = getattr(zeros, _ZKEY, None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    if zeros.numel() == 0:
+        return False
+    if torch.cuda.is_current_stream_capturing():
+        return True
+    with rt.on_device(zeros.device):
+        flag = torch.zeros(1, dtype=torch.int32, device=zeros.device)
+        _lib.check(rt.lib().w4a16_zeros_check_f16(zeros.data_ptr(), zeros.numel(),
+                                                   flag.data_ptr(), rt.stream_ptr(zeros.device)),
+                   "w4a16 zeros check")
+        need = bool(flag.item())
+    setattr(zeros, _ZKEY, (key, need))
+    return need
+
+
+def mark_integer_zeros(zeros: Tensor) -> None:
+    """Record that `zeros` (as it is now) holds integers in [0, 15], as made by
+    quantize_weight, so its first GEMM needs no check."""
+    setattr(zeros, _ZKEY, ((zeros._version, zeros.data_ptr(), zeros.numel(), zeros.device),
+                           False))
+
+
 def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | None"):
     dev = x.device
     with rt.on_device(dev):
+        if zeros_need_any_form(zeros):
+            # the any-zero kernels, through a plan carrying the flag
+            if plan is None:
+                plan = _lib.plan(M, N, K, G)
+            else:
+                plan = _lib.Plan.from_buffer_copy(plan)
+            plan.flags |= _lib.PLAN_ANY_ZEROS
         if plan is None:
             ws_bytes = rt.lib().w4a16_gemm_workspace_bytes(M, N, K, G)
         else:

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor, nn
 
-from .hip_kernel import w4a16_linear
+from .hip_kernel import mark_integer_zeros, w4a16_linear
 from .quant import quantize_weight
 
 __all__ = ["W4A16Linear"]
@@ -84,6 +84,7 @@ class W4A16Linear(nn.Module):
         self.qweight.copy_(qweight.to(self.qweight.device))
         self.scales.copy_(scales.to(self.scales.device))
         self.zeros.copy_(zeros.to(self.zeros.device))
+        mark_integer_zeros(self.zeros)
 
     def forward(self, x: Tensor) -> Tensor:
         """y = (x @ dequant(W)) + bias over the last dim (linear.py:82-92)."""

@@ -24,6 +24,7 @@ from torch import Tensor
 
 from . import _lib
 from . import _runtime as rt
+from .hip_kernel import mark_integer_zeros
 
 __all__ = ["quantize_weight", "dequantize_weight", "pack_int4", "unpack_int4"]
 
@@ -112,7 +113,9 @@ def quantize_weight(W: Tensor, group_size: int = 128) -> tuple[Tensor, Tensor, T
             if int(flag.item()) != 0:
                 raise AssertionError(
                     "uint4 values must be in [0,15]: W holds a non-finite value")
-    return qweight.to(home), scales.to(home), zeros.to(home)
+    zeros = zeros.to(home)
+    mark_integer_zeros(zeros)   # zero-points 0..15: the integer-zero kernels take them
+    return qweight.to(home), scales.to(home), zeros
 
 
 def dequantize_weight(qweight: Tensor, scales: Tensor, zeros: Tensor, group_size: int) -> Tensor:
