@@ -243,6 +243,39 @@ def bench_case(case, steps: int, warmup: int, graph: bool = False, cold: bool = 
             "bytes": case.bytes(), "flops": case.flops()}
 
 
+def bench_quantize(case, steps: int, warmup: int) -> dict:
+    """quantize_weight's kernel (w4a16_quantize_pack_f16) on the case's fp16 W,
+    outputs preallocated, calls queued behind the spin and timed with HIP
+    events like the GEMM cases; GB/s of W read plus qweight, scales and zeros
+    written.  W (K x N fp16) is far larger than the caches only at C4 / C5
+    sizes; at C2 (32 MiB) consecutive calls may find part of it in the 256 MiB
+    Infinity Cache."""
+    import torch
+    from w4a16 import _lib
+    from w4a16 import workloads as wl
+
+    _, W = wl.make_inputs(case)
+    Wd = W.cuda()
+    K, N, G = case.K, case.N, case.G
+    qw = torch.empty(K // 8, N, dtype=torch.int32, device="cuda")
+    sc = torch.empty(K // G, N, dtype=torch.float16, device="cuda")
+    zr = torch.empty(K // G, N, dtype=torch.float16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lib = _lib.load()
+
+    def call():
+        rc = lib.w4a16_quantize_pack_f16(Wd.data_ptr(), qw.data_ptr(), sc.data_ptr(),
+                                         zr.data_ptr(), K, N, G, flag.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"w4a16_quantize_pack_f16: {rc}")
+    t = _time_calls([call], steps, warmup, False)
+    nbytes = 2 * K * N + 4 * (K // 8) * N + 2 * 2 * (K // G) * N
+    us = t["ms"] * 1e3
+    return {"case": "quantize " + case.name, "K": K, "N": N, "G": G, "us": us,
+            "GB/s": nbytes / us / 1e3, "bytes": nbytes, "flag": int(flag.item())}
+
+
 def _cold_note(r: dict) -> str:
     if r["weight_copies"] <= 1:
         return "warm: one copy of the weights"
@@ -429,13 +462,24 @@ def _device_name() -> str:
 # --------------------------------------------------------------------------- #
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 
-# --traffic-probe's workloads, in order: (key, config, M, K, N, calls, cold)
-PROBE = [("C2", "C2", 1, 4096, 4096, 8, True),
-         ("C3_M8_K4096_N4096", "C3", 8, 4096, 4096, 4, True),
-         ("C3_M32_K4096_N4096", "C3", 32, 4096, 4096, 4, True),
-         ("C3_M16_K4096_N28672", "C3", 16, 4096, 28672, 4, True),
-         ("C3_M32_K4096_N28672", "C3", 32, 4096, 28672, 4, True),
-         ("C4_M4096", "C4", 4096, 4096, 14336, 3, False)]
+# --traffic-probe's workloads, in order: (key, config, M, K, N, G, calls, cold);
+# config "X": a shape outside the BASELINE configs (C3-style weights).  The
+# M <= 2 rows cover every kernel the planner picks there: the direct GEMV with
+# 8 / 16 waves (C2, K = 14336), the skinny kernel's 32-column blocks (N =
+# 6144), and the MFMA-dot GEMV on 128-column blocks and, split, on 64-column
+# blocks with its reduction pass (N = 28672, C5, M = 2 at K = 14336).
+PROBE = [("C2", "C2", 1, 4096, 4096, 128, 8, True),
+         ("C3_M1_K4096_N6144", "C3", 1, 4096, 6144, 128, 4, True),
+         ("C3_M1_K14336_N4096", "C3", 1, 14336, 4096, 128, 4, True),
+         ("C3_M1_K4096_N28672", "C3", 1, 4096, 28672, 128, 4, True),
+         ("C5_M1_K8192_N28672_G128", "C5", 1, 8192, 28672, 128, 4, True),
+         ("C5_M1_K28672_N8192_G128", "C5", 1, 28672, 8192, 128, 4, True),
+         ("M2_K14336_N4096", "X", 2, 14336, 4096, 128, 4, True),
+         ("C3_M8_K4096_N4096", "C3", 8, 4096, 4096, 128, 4, True),
+         ("C3_M32_K4096_N4096", "C3", 32, 4096, 4096, 128, 4, True),
+         ("C3_M16_K4096_N28672", "C3", 16, 4096, 28672, 128, 4, True),
+         ("C3_M32_K4096_N28672", "C3", 32, 4096, 28672, 128, 4, True),
+         ("C4_M4096", "C4", 4096, 4096, 14336, 128, 3, False)]
 
 
 def traffic_probe() -> None:
@@ -454,8 +498,9 @@ def traffic_probe() -> None:
     torch.cuda.synchronize()
     del a, b
     print("copy 256 MiB x3", flush=True)
-    for key, cfg, M, K, N, calls, cold in PROBE:
-        case = [c for c in wl.CONFIGS[cfg] if (c.M, c.K, c.N) == (M, K, N)][0]
+    for key, cfg, M, K, N, G, calls, cold in PROBE:
+        case = (wl.Case("X", M, K, N, G, 2) if cfg == "X" else
+                [c for c in wl.CONFIGS[cfg] if (c.M, c.K, c.N, c.G) == (M, K, N, G)][0])
         X, W, Xd, layers, y, _, _ = _prepare(case, cold)
         torch.cuda.synchronize()
         torch.cuda._sleep(1000)                      # group marker
@@ -678,6 +723,15 @@ def main() -> int:
             print(f"{r['case']:<32} {r['kernel']:>6} cfg={r['tile_cfg']:<2} "
                   f"split={r['split_k']:<3} {r['us']:9.2f} us {r['GB/s']:8.1f} GB/s "
                   f"{r['TFLOP/s']:8.2f} TFLOP/s", file=sys.stderr, flush=True)
+        seen = set()
+        for case in wl.cases("C2", "C4", "C5"):
+            if (case.K, case.N, case.G) in seen:
+                continue
+            seen.add((case.K, case.N, case.G))
+            r = bench_quantize(case, max(20, args.steps // 4), 3)
+            rows.append(r)
+            print(f"{r['case']:<32} {r['us']:9.2f} us {r['GB/s']:8.1f} GB/s (W read + packed "
+                  "written)", file=sys.stderr, flush=True)
         if args.sweep_json:
             with open(args.sweep_json, "w") as f:
                 json.dump(rows, f, indent=1)

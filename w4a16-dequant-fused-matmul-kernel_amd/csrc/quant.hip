@@ -191,6 +191,155 @@ __global__ __launch_bounds__(256) void quantize_kernel(const typename IN::T* __r
   }
 }
 
+// Four adjacent columns' weights of one row: 8 (fp16) or 16 (fp32) bytes.
+template <class IN>
+struct Row4;
+template <>
+struct Row4<InF16> {
+  uint2 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ uint16_t bits(int c) const {
+    return (uint16_t)(((c < 2 ? v.x : v.y) >> (16 * (c & 1))) & 0xFFFFu);
+  }
+  __device__ __forceinline__ float val(int c) const { return InF16::val(bits(c)); }
+  __device__ __forceinline__ bool nonfinite(int c) const { return InF16::nonfinite(bits(c)); }
+};
+template <>
+struct Row4<InF32> {
+  float4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ float val(int c) const {
+    return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+  }
+  __device__ __forceinline__ bool nonfinite(int c) const { return InF32::nonfinite(val(c)); }
+};
+
+// One workgroup quantises one group (G rows, G % 8 == 0) of 256 columns
+// (N % 4 == 0): lane l of each wave owns columns 4l..4l+3, and wave w a
+// contiguous quarter of the group's packed rows (octets).  Every lane issues
+// all of its rows' loads at once (the group's min / max no longer waits for
+// one row after another), the waves' minima and maxima meet in LDS in wave
+// (k) order, and the codes come from the rows still in registers (OPW > 0:
+// at most OPW octets per wave) or from a second read of the group (OPW = 0,
+// long groups; the tile is L2-resident).  The running minimum's tie rule
+// (min_step) applied within a wave in k order and across the waves in k order
+// gives the same zero as one scan in k order.  Grid: K / G x N / 256
+// workgroups (512 at K = N = 4096, G = 128, against 128 for one thread per
+// group and 4 columns).
+template <class IN, int OPW>
+__global__ __launch_bounds__(256) void quantize_tile_kernel(const typename IN::T* __restrict__ W,
+                                                            uint32_t* __restrict__ QW,
+                                                            uint16_t* __restrict__ SC,
+                                                            uint16_t* __restrict__ ZR, int K,
+                                                            int N, int G,
+                                                            int32_t* __restrict__ flag) {
+  __shared__ float smn[4][256], smx[4][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = blockIdx.x;
+  const int n = blockIdx.y * 256 + 4 * lane;
+  const bool nv = n < N;
+  const int octs = G / 8;
+  const int per = (octs + 3) / 4;
+  const int o0 = min(octs, wave * per), o1 = min(octs, o0 + per);
+  const bool tie_last = n < 32 * (N / 32);
+  const typename IN::T* src = W + (size_t)g * G * N + n;
+
+  float mn[4], mx[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    mn[c] = __builtin_inff();
+    mx[c] = -__builtin_inff();
+  }
+  bool bad = false;
+  auto scan = [&](const Row4<IN>& r) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bad |= r.nonfinite(c);
+      const float v = r.val(c);
+      mn[c] = min_step(v, mn[c], tie_last);
+      mx[c] = (v >= mx[c]) ? v : mx[c];
+    }
+  };
+  Row4<IN> keep[OPW > 0 ? OPW : 1][8];
+  if constexpr (OPW > 0) {
+#pragma unroll
+    for (int i = 0; i < OPW; ++i)
+      if (nv && o0 + i < o1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) keep[i][j].load(src + (size_t)((o0 + i) * 8 + j) * N);
+      }
+#pragma unroll
+    for (int i = 0; i < OPW; ++i)
+      if (nv && o0 + i < o1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) scan(keep[i][j]);
+      }
+  } else if (nv) {
+    for (int o = o0; o < o1; ++o) {
+      Row4<IN> r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j].load(src + (size_t)(o * 8 + j) * N);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) scan(r[j]);
+    }
+  }
+  if (bad) *flag = 1;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    smn[wave][4 * lane + c] = mn[c];
+    smx[wave][4 * lane + c] = mx[c];
+  }
+  __syncthreads();
+  float sc[4], zr[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float a = smn[0][4 * lane + c], b = smx[0][4 * lane + c];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float v = smn[w][4 * lane + c], u = smx[w][4 * lane + c];
+      a = min_step(v, a, tie_last);
+      b = (u >= b) ? u : b;
+    }
+    float s = (b - a) / 15.0f;
+    s = (s > 0.0f) ? s : 1.0f;
+    sc[c] = s;
+    zr[c] = clamp_q(__builtin_rintf(-a / s));
+  }
+  if (!nv) return;
+  auto codes = [&](const Row4<IN>(&r)[8], int o) {
+    uint32_t word[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float q = clamp_q(__builtin_rintf(r[j].val(c) / sc[c]) + zr[c]);
+        word[c] |= ((uint32_t)(int)q & 0xFu) << (4 * j);
+      }
+    *reinterpret_cast<uint4*>(QW + (size_t)(g * octs + o) * N + n) =
+        make_uint4(word[0], word[1], word[2], word[3]);
+  };
+  if constexpr (OPW > 0) {
+#pragma unroll
+    for (int i = 0; i < OPW; ++i)
+      if (o0 + i < o1) codes(keep[i], o0 + i);
+  } else {
+    for (int o = o0; o < o1; ++o) {
+      Row4<IN> r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j].load(src + (size_t)(o * 8 + j) * N);
+      codes(r, o);
+    }
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      SC[(size_t)g * N + n + c] = as_u16((f16)sc[c]);
+      ZR[(size_t)g * N + n + c] = as_u16((f16)zr[c]);
+    }
+  }
+}
+
 // Any G dividing K (G % 8 != 0 lets a packed word straddle groups): one thread
 // per packed word; each row's group statistics are recomputed from the group's
 // G values, and the thread that owns a group's first row writes its scale/zero.
@@ -330,9 +479,17 @@ hipError_t quantize_launch(const void* W, int32_t* qw, void* sc, void* zr, int K
   const bool vec = (N % 4 == 0) && ((reinterpret_cast<uintptr_t>(W) & (wa - 1)) == 0) &&
                    ((reinterpret_cast<uintptr_t>(qw) & 15) == 0);
   if (vec) {
-    dim3 grid(K / G, (N / 4 + 255) / 256);
-    hipLaunchKernelGGL((quantize_kernel<IN, 4>), grid, dim3(256), 0, st, w, q, s, z, K, N, G,
-                       flag);
+    // octets per wave: kept in registers up to 8 (fp16) / 4 (fp32), beyond
+    // that read twice
+    const int per = (G / 8 + 3) / 4;
+    constexpr int kMaxKeep = sizeof(T) == 2 ? 8 : 4;
+    auto k = per <= 1 ? quantize_tile_kernel<IN, 1>
+             : per <= 2 ? quantize_tile_kernel<IN, 2>
+             : per <= 4 ? quantize_tile_kernel<IN, 4>
+             : per <= kMaxKeep ? quantize_tile_kernel<IN, kMaxKeep>
+                              : quantize_tile_kernel<IN, 0>;
+    dim3 grid(K / G, (N + 255) / 256);
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, st, w, q, s, z, K, N, G, flag);
   } else {
     dim3 grid(K / G, (N + 255) / 256);
     hipLaunchKernelGGL((quantize_kernel<IN, 1>), grid, dim3(256), 0, st, w, q, s, z, K, N, G,
