@@ -89,6 +89,19 @@ def _args():
                     help="time K calls of two near-empty kernels exactly as the headline's "
                          "calls are timed (eager, behind the spin, HIP events): the per-dispatch "
                          "cost of the queue itself, untraced or under a tracer")
+    ap.add_argument("--planner-audit", action="store_true",
+                    help="planner regret: the static plan against every other plan the "
+                         "library has (w4a16.autotune.candidates) over LLM layer shapes x M "
+                         "(AUDIT_SHAPES, AUDIT_MS); markdown table")
+    ap.add_argument("--audit-shapes", default=None,
+                    help="comma list of KxN (default: AUDIT_SHAPES)")
+    ap.add_argument("--audit-ms", default=None, help="comma list of M (default: AUDIT_MS)")
+    ap.add_argument("--decode-scan", metavar="OUT_JSON",
+                    help="time every GEMV and skinny plan for M = 1, 2 (G = 128) over the "
+                         "DECODE_KS x DECODE_NS grid, cold weights; JSON for --decode-table")
+    ap.add_argument("--decode-table", metavar="SCAN_JSON",
+                    help="write csrc/decode_table.inc (the planner's measured M <= 2 table) "
+                         "from a --decode-scan file")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="markdown table of a rocprofv3 --kernel-trace CSV of bench.py: per "
                          "kernel, the durations of its last --steps dispatches (the timed "
@@ -274,6 +287,177 @@ def bench_quantize(case, steps: int, warmup: int) -> dict:
     us = t["ms"] * 1e3
     return {"case": "quantize " + case.name, "K": K, "N": N, "G": G, "us": us,
             "GB/s": nbytes / us / 1e3, "bytes": nbytes, "flag": int(flag.item())}
+
+
+# --planner-audit: (label, K, N) of Llama-style layers: fused QKV, out-proj,
+# fused gate+up, down-proj of 7B (Llama-2), 8B (Llama-3), 13B and 70B.
+AUDIT_SHAPES = [("7B qkv", 4096, 12288), ("7B o", 4096, 4096), ("7B gate+up", 4096, 22016),
+                ("7B down", 11008, 4096), ("8B qkv", 4096, 6144), ("8B gate+up", 4096, 28672),
+                ("8B down", 14336, 4096), ("13B qkv", 5120, 15360), ("13B o", 5120, 5120),
+                ("13B gate+up", 5120, 27648), ("13B down", 13824, 5120),
+                ("70B qkv", 8192, 10240), ("70B o", 8192, 8192), ("70B gate+up", 8192, 57344),
+                ("70B down", 28672, 8192)]
+AUDIT_MS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024]
+
+
+def planner_audit(shapes, ms, G: int = 128, steps: int = 30, reps: int = 3) -> str:
+    """Markdown table: per shape and M, the static plan's µs against the fastest
+    of the other plans (timed the bench's way: cold weights and eager calls for
+    M < 64, warm weights in a graph replay from M = 64; repetitions interleaved
+    across plans; median).  The static plan is timed twice (its two medians
+    give the run's noise).  Regret = static / best - 1."""
+    import torch
+    from w4a16 import autotune, quantize_weight
+    from w4a16.hip_kernel import w4a16_matmul_planned
+
+    lines = ["| layer | K | N | M | static plan | static µs | static µs (again) | best plan | "
+             "best µs | regret |", "|---|---|---|---|---|---|---|---|---|---|"]
+    worst = []
+    for label, K, N in shapes:
+        g = torch.Generator(device="cuda").manual_seed(K * 7 + N)
+        W = (torch.randn(K, N, device="cuda", generator=g) * 0.02).to(torch.float16)
+        qw, sc, zr = quantize_weight(W, G)
+        del W
+        per = qw.numel() * 4 + sc.numel() * 4
+        for M in ms:
+            X = torch.randn(M, K, device="cuda", generator=g).to(torch.float16)
+            cold = M < 64
+            ncopy = max(2, -(-COLD_BYTES // per) + 1) if cold else 1
+            layers = [(qw, sc, zr)] + [(qw.clone(), sc.clone(), zr.clone())
+                                       for _ in range(ncopy - 1)]
+            y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+            cands = autotune.candidates(M, N, K, G)
+            cands = [cands[0], ("static (again)", cands[0][1])] + cands[1:]
+            live = []
+            for name, p in cands:
+                try:
+                    w4a16_matmul_planned(X, qw, sc, zr, G, p, out=y)
+                except RuntimeError:
+                    continue
+                fns = [(lambda l=l, p=p: w4a16_matmul_planned(X, l[0], l[1], l[2], G, p, out=y))
+                       for l in layers]
+                live.append((name, fns))
+            torch.cuda.synchronize()
+            times = {name: [] for name, _ in live}
+            best_first = float("inf")
+            for r in range(reps):
+                for name, fns in live:
+                    if r > 0 and times[name][0] > 1.5 * best_first and not name.startswith("static"):
+                        continue
+                    t = _time_calls(fns, steps, 5, not cold)["ms"] * 1e3
+                    times[name].append(t)
+                    if r == 0:
+                        best_first = min(best_first, t)
+            import statistics
+            med = {n: statistics.median(v) for n, v in times.items()}
+            st, st2 = med[cands[0][0]], med["static (again)"]
+            others = {n: v for n, v in med.items() if not n.startswith("static")}
+            bname = min(others, key=others.get) if others else cands[0][0]
+            best = min(others.get(bname, st), st, st2)
+            if best >= min(st, st2):
+                bname = "static"
+            regret = st / best - 1.0
+            worst.append((regret, label, M, bname))
+            lines.append(f"| {label} | {K} | {N} | {M} | {cands[0][1].as_dict()['kernel_name']} "
+                         f"cfg {cands[0][1].tile_cfg} split {cands[0][1].split_k} "
+                         f"tile {cands[0][1].tile_m}x{cands[0][1].tile_n} | {st:.2f} | {st2:.2f} | "
+                         f"{bname} | {best:.2f} | {100 * regret:+.1f} % |")
+            print(lines[-1], file=sys.stderr, flush=True)
+            del layers, X, y
+        del qw, sc, zr
+        torch.cuda.empty_cache()
+    worst.sort(reverse=True)
+    n3 = sum(1 for w in worst if w[0] > 0.03)
+    lines.append("")
+    lines.append(f"{len(worst)} shapes x M; static plan more than 3 % behind the best other plan "
+                 f"on {n3}; largest regrets: " +
+                 "; ".join(f"{l} M={m} {100 * r:+.1f} % ({b})" for r, l, m, b in worst[:5]))
+    return "\n".join(lines)
+
+
+# --decode-scan grid: the planner's measured table for M <= 2, G % 128 == 0
+# covers K in [DECODE_KS[0], DECODE_KS[-1]] and N in [DECODE_NS[0], DECODE_NS[-1]]
+DECODE_KS = [3584, 4096, 5120, 6144, 8192, 11008, 13824, 14336, 16384, 20480, 28672]
+DECODE_NS = [4096, 5120, 6144, 8192, 10240, 11008, 12288, 14336, 15360, 16384, 20480, 22016,
+             24576, 27648, 28672, 32768, 40960, 57344]
+DECODE_TABLE = os.path.join(PKG_DIR, "csrc", "decode_table.inc")
+
+
+def decode_scan(out_path: str, ks=None, ns=None, ms=(1, 2), G: int = 128) -> None:
+    """Median µs of every GEMV and skinny plan (w4a16.autotune.candidates) at each
+    (M, K, N) of the grid, timed the bench's way (cold weights, eager calls
+    behind the spin, 3 interleaved repetitions); written as JSON after every
+    (K, N)."""
+    import statistics
+
+    import torch
+    from w4a16 import _lib, autotune, quantize_weight
+    from w4a16.hip_kernel import w4a16_matmul_planned
+
+    res = []
+    for K in ks or DECODE_KS:
+        for N in ns or DECODE_NS:
+            g = torch.Generator(device="cuda").manual_seed(K + N)
+            W = (torch.randn(K, N, device="cuda", generator=g) * 0.02).to(torch.float16)
+            qw, sc, zr = quantize_weight(W, G)
+            del W
+            per = qw.numel() * 4 + sc.numel() * 4
+            ncopy = max(2, -(-COLD_BYTES // per) + 1)
+            layers = [(qw, sc, zr)] + [(qw.clone(), sc.clone(), zr.clone())
+                                       for _ in range(ncopy - 1)]
+            for M in ms:
+                X = torch.randn(M, K, device="cuda", generator=g).to(torch.float16)
+                y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+                live = []
+                for name, p in autotune.candidates(M, N, K, G):
+                    if name != "static" and p.kernel not in (_lib.KERNEL_GEMV, _lib.KERNEL_SKINNY):
+                        continue
+                    try:
+                        w4a16_matmul_planned(X, qw, sc, zr, G, p, out=y)
+                    except RuntimeError:
+                        continue
+                    fns = [(lambda l=l, p=p: w4a16_matmul_planned(X, l[0], l[1], l[2], G, p,
+                                                                  out=y)) for l in layers]
+                    live.append((name, p, fns))
+                t = {name: [] for name, _, _ in live}
+                for _ in range(3):
+                    for name, p, fns in live:
+                        t[name].append(_time_calls(fns, 30, 5, False)["ms"] * 1e3)
+                res.append({"M": M, "K": K, "N": N, "G": G,
+                            "plans": {name: p.as_dict() for name, p, _ in live},
+                            "us": {name: statistics.median(v) for name, v in t.items()}})
+                best = min(res[-1]["us"], key=res[-1]["us"].get)
+                print(f"M={M} K={K} N={N} static {res[-1]['us']['static']:.2f} best {best} "
+                      f"{res[-1]['us'][best]:.2f}", file=sys.stderr, flush=True)
+                del X, y
+            del layers, qw, sc, zr
+            torch.cuda.empty_cache()
+            with open(out_path, "w") as f:
+                json.dump(res, f)
+
+
+def decode_table(scan_path: str) -> str:
+    """C source of the planner's M <= 2 table from a --decode-scan file: per
+    measured (M, K, N) the fastest plan (family, configuration, column block or
+    row group, k-split)."""
+    with open(scan_path) as f:
+        rows = json.load(f)
+    lines = ["// Generated by `python bench.py --decode-table <scan.json>` from",
+             "// `python bench.py --decode-scan <scan.json>` on one MI355X (256 CUs): per",
+             "// (M, K, N) of the grid, G = 128, cold weights, the fastest GEMV / skinny",
+             "// plan.  Fields: M, K, N, kernel (1 GEMV, 4 skinny), tile_cfg, tile_n,",
+             "// tile_m (skinny rows), split_k, µs x 100 of the fastest, of the plan",
+             "// the rules gave.",
+             "// clang-format off"]
+    for r in sorted(rows, key=lambda r: (r["M"], r["K"], r["N"])):
+        us = r["us"]
+        best = min(us, key=us.get)
+        p = r["plans"][best]
+        lines.append(f"{{{r['M']}, {r['K']}, {r['N']}, {p['kernel']}, {p['tile_cfg']}, "
+                     f"{p['tile_n']}, {p['tile_m']}, {p['split_k']}, {round(100 * us[best])}, "
+                     f"{round(100 * us['static'])}}},")
+    lines.append("// clang-format on")
+    return "\n".join(lines) + "\n"
 
 
 def _cold_note(r: dict) -> str:
@@ -643,6 +827,12 @@ def main() -> int:
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.steps))
         return 0
+    if args.decode_table:
+        src = decode_table(args.decode_table)
+        with open(DECODE_TABLE, "w") as f:
+            f.write(src)
+        print(f"wrote {DECODE_TABLE} ({src.count(chr(10)) - 8} entries)")
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build targets a single MI355X: columns would shard with no "
@@ -659,6 +849,19 @@ def main() -> int:
         return 0
     if args.empty_kernels:
         print(json.dumps(empty_kernels(args.steps, args.warmup)), flush=True)
+        return 0
+    if args.decode_scan:
+        decode_scan(args.decode_scan)
+        return 0
+    if args.planner_audit:
+        shapes = AUDIT_SHAPES
+        if args.audit_shapes:
+            want = [tuple(map(int, s.split("x"))) for s in args.audit_shapes.split(",")]
+            shapes = [a for a in AUDIT_SHAPES if (a[1], a[2]) in want] + [
+                (f"{k}x{n}", k, n) for k, n in want if (k, n) not in
+                {(a[1], a[2]) for a in AUDIT_SHAPES}]
+        ms = [int(m) for m in args.audit_ms.split(",")] if args.audit_ms else AUDIT_MS
+        print(planner_audit(shapes, ms), flush=True)
         return 0
     if args.reference_table:
         print(json.dumps(reference_table(args.reference_json)), flush=True)

@@ -318,7 +318,6 @@ def test_quant_entry_points_reject_bad_args(lib):
     (4, 28672, 4096, 128, "skinny"),
     (2, 6144, 4096, 128, "skinny"),   # M <= 2, 4096 < N <= 8192: the skinny kernel's 32-column blocks
     (2, 6144, 4096, 32, "skinny"),    # ... at any G up to K = 4096
-    (2, 6144, 8192, 128, "skinny"),   # ... at M = 2 up to K = 8192 with G % 128 == 0
     (2, 6144, 8192, 64, "gemv"),
     (2, 6144, 2048, 128, "gemv"),     # ... not for K <= 2048
     (3, 4096, 14336, 128, "skinny"),  # 3 <= M <= 8 up to N = 16384: MFMA skinny
@@ -392,16 +391,16 @@ def test_planner_decode_64_column_band():
     from w4a16 import _lib
 
     for M, N, K, G, kern, cfg in ((1, 11008, 4096, 128, "skinny", 3), (2, 14336, 4096, 128, "skinny", 3),
-                                  (1, 11008, 4096, 32, "gemv", 7), (1, 10240, 8192, 128, "gemv", 7),
+                                  (1, 11008, 4096, 32, "gemv", 7), (1, 10240, 8192, 64, "gemv", 7),
                                   (2, 11008, 8192, 64, "gemv", 7)):
         p = _lib.plan(M, N, K, G)
         assert (_lib.KERNEL_NAMES[p.kernel], p.tile_cfg, p.tile_n, p.split_k) == (kern, cfg, 64, 1), (M, N, K, G)
-    p = _lib.plan(1, 11008, 2048, 128)          # K <= 2048: the skinny kernel's blocks
+    p = _lib.plan(1, 11008, 2048, 64)          # K <= 2048: the skinny kernel's blocks
     assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n) == ("skinny", 64)
     # at the band's edges: N = 8192 (256 32-column blocks) and N = 16384 (256
     # 64-column blocks) keep their plans
-    assert _lib.plan(1, 8192, 8192, 128).tile_n == 32
-    assert (_lib.plan(1, 16384, 4096, 128).tile_n, _lib.plan(1, 16384, 4096, 128).tile_cfg) == (64, 7)
+    assert _lib.plan(1, 8192, 8192, 64).tile_n == 32
+    assert (_lib.plan(1, 16384, 4096, 64).tile_n, _lib.plan(1, 16384, 4096, 64).tile_cfg) == (64, 7)
 
 
 def test_planner_gemv_split_rule():
@@ -419,7 +418,7 @@ def test_planner_gemv_split_rule():
         assert p.tile_n in (16, 32, 64, 128, 256)
         assert p.tile_cfg in (1, 2, 4, 5, 7)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
-    assert _lib.plan(1, 28672, 4096, 128).tile_n == 128
+    assert _lib.plan(1, 28672, 4096, 64).tile_n == 128
     for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 1024, 28672)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
@@ -434,10 +433,10 @@ def test_planner_gemv_split_rule():
         assert p.workspace_bytes == split * M * N * 4
         assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
     for M, N, K in ((1, 4096, 14336), (1, 8192, 8192), (1, 1024, 28672), (3, 8192, 28672)):
-        p = _lib.plan(M, N, K, 128)                  # shorter rows, too few blocks, M > 2
+        p = _lib.plan(M, N, K, 64)                   # shorter rows, too few blocks, M > 2
         assert p.tile_cfg != 7 or p.split_k == 1, (M, N, K)
-    assert _lib.plan(1, 28672, 14336, 128).split_k == 1   # enough column blocks
-    assert _lib.plan(1, 4096, 14336, 128).split_k == 1    # one block per CU
+    assert _lib.plan(1, 28672, 14336, 64).split_k == 1   # enough column blocks
+    assert _lib.plan(1, 4096, 14336, 64).split_k == 1    # one block per CU
     for split in (2, 3, 7, 600):
         p = _lib.plan(2, 1024, 4096, 128, _lib.KERNEL_GEMV, split)
         rows = -(-512 // p.split_k)
@@ -460,55 +459,115 @@ def test_planner_gemv_blocks_and_waves():
     4), one chunk, no split."""
     from w4a16 import _lib
 
-    p = _lib.plan(1, 4096, 4096, 128)            # C2: 256 blocks of 16 (256 CUs), 8 waves
+    p = _lib.plan(1, 4096, 4096, 64)            # C2: 256 blocks of 16 (256 CUs), 8 waves
     assert (p.tile_n, p.tile_cfg) == (16, 1)
-    p = _lib.plan(2, 4096, 4096, 128)            # ... 16 at M = 2
+    p = _lib.plan(2, 4096, 4096, 64)            # ... 16 at M = 2
     assert (p.tile_n, p.tile_cfg) == (16, 2)
     p = _lib.plan(1, 4096, 2048, 128, _lib.KERNEL_GEMV, 0)   # ... and at K = 2048
     assert (p.tile_n, p.tile_cfg) == (16, 2)
-    assert _lib.KERNEL_NAMES[_lib.plan(1, 4096, 2048, 128).kernel] == "skinny"   # (planned there)
+    assert _lib.KERNEL_NAMES[_lib.plan(1, 4096, 2048, 64).kernel] == "skinny"   # (planned there)
     p = _lib.plan(1, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)   # 384 blocks of 16 -> 192 of 32
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(2, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)
     assert (p.tile_n, p.tile_cfg) == (32, 2)
-    p = _lib.plan(1, 6144, 14336, 128)           # ... at any K, unsplit, 16 waves
+    p = _lib.plan(1, 6144, 14336, 64)            # ... at any K, unsplit, 16 waves
     assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n, p.tile_cfg, p.split_k) == ("gemv", 32, 2, 1)
-    p = _lib.plan(1, 6144, 28672, 128)           # ... even past the long-row split's K
+    p = _lib.plan(1, 6144, 28672, 64)            # ... even past the long-row split's K
     assert (p.tile_n, p.tile_cfg, p.split_k) == (32, 2, 1)
-    p = _lib.plan(1, 8192, 28672, 128)           # not at N = 8192 (256 blocks of 32)
+    p = _lib.plan(1, 8192, 28672, 64)           # not at N = 8192 (256 blocks of 32)
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
     # 128-column blocks, unsplit, where 64-column ones would take more than one
     # round (N > 16384) and 128-column ones not; N = 16384 keeps one round of 64
     for N, K in ((16896, 4096), (20480, 8192), (20480, 28672), (32768, 4096)):
-        p = _lib.plan(1, N, K, 128)
+        p = _lib.plan(1, N, K, 64)
         assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1), (N, K)
-    assert _lib.plan(1, 16384, 4096, 128).tile_n == 64
-    p = _lib.plan(2, 4096, 10240, 128)           # long rows at M = 2: 8 waves
+    assert _lib.plan(1, 16384, 4096, 64).tile_n == 64
+    p = _lib.plan(2, 4096, 10240, 64)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
-    p = _lib.plan(2, 4096, 14336, 128)           # ... longer: MFMA dots, split K
+    p = _lib.plan(2, 4096, 14336, 64)           # ... longer: MFMA dots, split K
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 4)
-    p = _lib.plan(1, 4096, 14336, 128)           # ... 16 at M = 1, direct
+    p = _lib.plan(1, 4096, 14336, 64)           # ... 16 at M = 1, direct
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 16384, 4096, 128)           # 64-column blocks: 8 waves, staged, MFMA dots
+    p = _lib.plan(1, 16384, 4096, 64)           # 64-column blocks: 8 waves, staged, MFMA dots
     assert (p.tile_n, p.tile_cfg) == (64, 7)
-    p = _lib.plan(1, 28672, 4096, 128)           # 224 blocks of 128: 8 waves, MFMA dots
+    p = _lib.plan(1, 28672, 4096, 64)           # 224 blocks of 128: 8 waves, MFMA dots
     assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
-    p = _lib.plan(2, 28672, 8192, 128)
+    p = _lib.plan(2, 28672, 8192, 64)
     assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
-    p = _lib.plan(1, 65536, 4096, 128)           # 256-column blocks: dot2, staged
+    p = _lib.plan(1, 65536, 4096, 64)           # 256-column blocks: dot2, staged
     assert (p.tile_n, p.tile_cfg) == (256, 4)
     p = _lib.plan(3, 28672, 8192, 128, _lib.KERNEL_GEMV, 0)   # M > 2 keeps 64-column blocks
     assert (p.tile_n, p.tile_cfg) == (64, 1)
-    p = _lib.plan(1, 4096, 8192, 128)            # shorter rows: direct reads
+    p = _lib.plan(1, 4096, 8192, 64)            # shorter rows: direct reads
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 8192, 28672, 128)           # C5 down-proj: MFMA dots, split 2
+    p = _lib.plan(1, 8192, 28672, 64)           # C5 down-proj: MFMA dots, split 2
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
     p = _lib.plan(1, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # unsplit: 16 waves, direct
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(2, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # ... 8 waves at M = 2
     assert (p.tile_n, p.tile_cfg) == (32, 1)
-    p = _lib.plan(2, 1024, 8192, 128)            # split 4: 2048 rows per split
+    p = _lib.plan(2, 1024, 8192, 64)            # split 4: 2048 rows per split
     assert p.split_k == 4 and p.tile_cfg == 2
+
+
+def _decode_table():
+    """Entries of csrc/decode_table.inc: (M, K, N, kernel, cfg, cols, rows, split)."""
+    path = os.path.join(ROOT, "w4a16-dequant-fused-matmul-kernel_amd", "csrc", "decode_table.inc")
+    rows = []
+    for line in open(path):
+        m = re.match(r"\{(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\},", line)
+        if m:
+            rows.append(tuple(int(v) for v in m.groups()[:8]))
+    return rows
+
+
+def test_planner_decode_table():
+    """M <= 2 with G % 128 == 0 inside the measured grid's K and N range: the
+    automatic plan is the grid's fastest plan (csrc/decode_table.inc) at every
+    grid point and the nearest grid point's (log2 K, log2 N) between them;
+    other group sizes and shapes outside the range follow the rules."""
+    import math
+
+    from w4a16 import _lib
+
+    table = _decode_table()
+    assert len(table) >= 300
+    assert {r[0] for r in table} == {1, 2}
+    kmin, kmax = min(r[1] for r in table), max(r[1] for r in table)
+    nmin, nmax = min(r[2] for r in table), max(r[2] for r in table)
+
+    def expect(M, K, N):
+        best = min((r for r in table if r[0] == M),
+                   key=lambda r: math.log2(K / r[1]) ** 2 + math.log2(N / r[2]) ** 2)
+        return best
+
+    def check(M, K, N, G=128):
+        p = _lib.plan(M, N, K, G)
+        e = expect(M, K, N)
+        kern, cfg, cols, rows, split = e[3:8]
+        assert p.kernel == kern and p.tile_cfg == cfg, (M, K, N, e, p.as_dict())
+        if kern == _lib.KERNEL_GEMV:
+            assert (p.tile_n, p.split_k) == (cols, split), (M, K, N, e, p.as_dict())
+            assert p.workspace_bytes == (split * M * N * 4 if split > 1 else 0)
+            assert p.grid_x == -(-N // cols) * split
+        else:
+            assert (p.tile_n, p.tile_m, p.split_k) == (cols, rows, 1), (M, K, N, e, p.as_dict())
+
+    for r in table:
+        check(r[0], r[1], r[2])
+    rng = np.random.default_rng(5)
+    for _ in range(300):
+        M = int(rng.integers(1, 3))
+        K = int(rng.integers(-(-kmin // 128), kmax // 128 + 1)) * 128
+        N = int(rng.integers(nmin // 4, nmax // 4 + 1)) * 4
+        check(M, K, N)
+    # outside the table's domain the rules decide alike for every group size:
+    # N or K outside the grid
+    for M, N, K in ((1, nmin // 2, kmax), (2, nmin, 2 * kmax), (1, 2 * nmax, kmin), (2, nmin, kmin // 2)):
+        a, b = _lib.plan(M, N, K, 128).as_dict(), _lib.plan(M, N, K, 64).as_dict()
+        assert a == b, (M, N, K, a, b)
+    # inside it, a smaller group size follows the rules (here unlike the table)
+    assert _lib.plan(1, 10240, 8192, 64).as_dict() != _lib.plan(1, 10240, 8192, 128).as_dict()
 
 
 def test_planner_small_batch_wide_weights_stream():

@@ -8,6 +8,7 @@
 
 #include <atomic>
 #include <climits>
+#include <cmath>
 #include <mutex>
 
 #include "../../include/w4a16.h"
@@ -477,9 +478,16 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // 32.0 (4 splits); M = 512, K = N = 4096 38.8 -> 36.0; M = 256, K = 14336,
   // N = 4096 48.5 -> 46.2 (8 splits); ties at M = 128 / 256, K = N = 4096.
   // More tiles than CUs (M = 1024, N = 14336: 131.0 vs 119.4) keep cfg 11.
-  if (c11 && G % 64 == 0 && t6 <= cus) {
-    int64_t s = cus / t6;
-    if (s > K / 512) s = K / 512;
+  // Unsplit, only where its tiles fill 7/10 of the CUs: with 160 tiles for
+  // 256 CUs (one workgroup each, the rest idle) cfg 11 split three ways for
+  // about two workgroups per CU wins instead (measured on MI355X, µs:
+  // M = 1024, K = 13824, N = 5120 174.9 -> 138.9; M = 512, K = 8192,
+  // N = 10240 108.1 -> 92.1; M = 1024, K = N = 5120 70.7 -> 66.6; 192 tiles,
+  // M = 512, K = 4096, N = 12288: cfg 14 within 2 %; split two ways it keeps
+  // winning below that: 86 tiles, M = 128, K = 4096, N = 22016).
+  const int64_t s14 = t6 > 0 ? (cus / t6 < K / 512 ? cus / t6 : K / 512) : 1;
+  if (c11 && G % 64 == 0 && t6 <= cus && (s14 > 1 || t6 * 10 >= 7 * (int64_t)cus)) {
+    int64_t s = s14;
     if (s < 1) s = 1;
     // 64 < M <= 256 on small layers: the 64-row streamed tiles (cfg 13, one
     // k-slice) instead, where the two-slice split would leave each slice at
@@ -506,6 +514,12 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     }
     return {14, s > 1 ? stream_splits((int)K, (int)s, 2) : 1};
   }
+  // M >= 1024 with more tiles than CUs but fewer than two per CU: split K
+  // three ways where that packs the tiles into two full rounds of two
+  // workgroups per CU instead of one partly filled round (320 tiles: M = 1024,
+  // K = 8192, N = 10240 188.6 -> 179.6 us on MI355X); else unsplit.
+  if (M >= 1024 && c11 && t6 > cus && 3 * t6 <= 4 * (int64_t)cus && K / 64 >= 24)
+    return {11, stream_splits((int)K, 3)};
   if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
   // cfg 11 on fewer than ~448 tiles: split K for about two workgroups per CU
   // (measured on MI355X: M = 128, K = 8192, N = 28672: 77.7 us at 4 splits vs
@@ -531,6 +545,46 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   return {1, 1};
 }
 
+// Measured decode plans (M <= 2, G % 128 == 0, 256 CUs): per (M, K, N) of a
+// grid the fastest GEMV or skinny plan, timed on MI355X with cold weights by
+// bench.py --decode-scan and written into decode_table.inc by bench.py
+// --decode-table.  A shape inside the grid's K and N range takes the plan of
+// the nearest grid point in (log2 K, log2 N).  The rules below cover
+// everything else (other M, smaller groups, other CU counts, shapes outside
+// the grid).  Measured against those rules on the same grid: 71 of 168 shapes
+// had been more than 3 % slower than the grid's best (up to 61 %: M = 2,
+// K = 28672, N = 14336, 66.0 against 41.1 us on 64-column MFMA-dot blocks).
+struct DecodeEntry {
+  int M, K, N, kernel, cfg, cols, rows, split, us100, rule_us100;
+};
+const DecodeEntry kDecodeTable[] = {
+#include "decode_table.inc"
+    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+
+const DecodeEntry* decode_table_entry(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  if (M < 1 || M > 2 || G % 128 != 0 || cus != 256) return nullptr;
+  int64_t kmin = INT64_MAX, kmax = 0, nmin = INT64_MAX, nmax = 0;
+  for (const DecodeEntry* e = kDecodeTable; e->M; ++e) {
+    kmin = e->K < kmin ? e->K : kmin;
+    kmax = e->K > kmax ? e->K : kmax;
+    nmin = e->N < nmin ? e->N : nmin;
+    nmax = e->N > nmax ? e->N : nmax;
+  }
+  if (K < kmin || K > kmax || N < nmin || N > nmax) return nullptr;
+  const DecodeEntry* best = nullptr;
+  double bd = 1e30;
+  for (const DecodeEntry* e = kDecodeTable; e->M; ++e) {
+    if (e->M != M) continue;
+    const double dk = std::log2((double)K / e->K), dn = std::log2((double)N / e->N);
+    const double d = dk * dk + dn * dn;
+    if (d < bd) {
+      bd = d;
+      best = e;
+    }
+  }
+  return best;
+}
+
 size_t mfma_workspace_bytes(int64_t M, int64_t N, int64_t K, int split) {
   return occ2_workspace_bytes((int)M, (int)N, (int)K, split);
 }
@@ -547,6 +601,38 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       kernel != W4A16_KERNEL_SIMT && kernel != W4A16_KERNEL_SKINNY)
     return W4A16_ERR_BAD_PLAN;
   if (M == 0 || N == 0 || K == 0) kernel = W4A16_KERNEL_SIMT;
+  if (kernel == W4A16_KERNEL_AUTO && fits(M, N, K, G)) {
+    if (const DecodeEntry* e = decode_table_entry(M, N, K, G, cus)) {
+      if (e->kernel == W4A16_KERNEL_GEMV && gemv_applicable(M, N, G) &&
+          gemv_cfg_valid(e->cfg, (int)M, e->cols) && gemv_cols_valid(e->cols)) {
+        int S = e->split < K / 8 ? e->split : (int)(K / 8);
+        if (S > 1) {
+          const int64_t KP = K / 8, rows = (KP + S - 1) / S;
+          S = (int)((KP + rows - 1) / rows);
+        }
+        p->kernel = W4A16_KERNEL_GEMV;
+        p->split_k = S < 1 ? 1 : S;
+        p->tile_cfg = e->cfg;
+        p->tile_m = 0;
+        p->tile_n = e->cols;
+        p->grid_x = ((N + e->cols - 1) / e->cols) * p->split_k;
+        p->grid_y = 1;
+        p->workspace_bytes = (int64_t)gemv_workspace_bytes((int)M, (int)N, (int)K, p->split_k);
+        return W4A16_OK;
+      }
+      if (e->kernel == W4A16_KERNEL_SKINNY && skinny_applicable(M, G) &&
+          skinny_plan_valid(e->cfg, (int)M, (int)N, e->rows)) {
+        p->kernel = W4A16_KERNEL_SKINNY;
+        p->split_k = 1;
+        p->tile_cfg = e->cfg;
+        p->tile_m = e->rows;
+        p->tile_n = e->cfg == 3 ? 64 : e->cfg == 2 ? 32 : 16;
+        p->grid_x = (N + p->tile_n - 1) / p->tile_n * ((M + p->tile_m - 1) / p->tile_m);
+        p->grid_y = 1;
+        return W4A16_OK;
+      }
+    }
+  }
   if (kernel == W4A16_KERNEL_AUTO) {
     if (!fits(M, N, K, G))
       kernel = W4A16_KERNEL_SIMT;

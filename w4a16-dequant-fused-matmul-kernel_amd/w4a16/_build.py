@@ -21,7 +21,7 @@ BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libw4a16.so")
 SOURCES = ["gemv.hip", "gemm_mfma.hip", "gemm_occ2.hip", "gemm_stream.hip", "gemm_skinny.hip",
            "simt.hip", "quant.hip", "capi.cpp"]
-HEADERS = ["w4a16_device.h", "w4a16_launch.h"]
+HEADERS = ["w4a16_device.h", "w4a16_launch.h", "decode_table.inc"]
 PUBLIC_HEADER = os.path.join(os.path.dirname(ROOT_DIR), "include", "w4a16.h")
 ARCH = "gfx950"
 

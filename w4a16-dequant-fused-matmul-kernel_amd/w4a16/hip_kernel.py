@@ -41,6 +41,7 @@ from torch import Tensor
 
 from . import _lib
 from . import _runtime as rt
+from . import autotune
 
 __all__ = ["w4a16_matmul", "w4a16_linear", "plan_for", "GROUP_MULTIPLE", "zeros_need_any_form"]
 
@@ -124,7 +125,11 @@ def mark_integer_zeros(zeros: Tensor) -> None:
 def _launch(x, qweight, scales, zeros, bias, y, M, N, K, G, plan: "_lib.Plan | None"):
     dev = x.device
     with rt.on_device(dev):
-        if zeros_need_any_form(zeros):
+        any_zeros = zeros_need_any_form(zeros)
+        if plan is None and autotune.enabled():
+            plan = autotune.plan_for_call(x, qweight, scales, zeros, G, M, N, K, _row_stride(x),
+                                          _row_stride(y), any_zeros)
+        if any_zeros:
             # the any-zero kernels, through a plan carrying the flag
             if plan is None:
                 plan = _lib.plan(M, N, K, G)
