@@ -478,15 +478,18 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // 32.0 (4 splits); M = 512, K = N = 4096 38.8 -> 36.0; M = 256, K = 14336,
   // N = 4096 48.5 -> 46.2 (8 splits); ties at M = 128 / 256, K = N = 4096.
   // More tiles than CUs (M = 1024, N = 14336: 131.0 vs 119.4) keep cfg 11.
-  // Unsplit, only where its tiles fill 7/10 of the CUs: with 160 tiles for
-  // 256 CUs (one workgroup each, the rest idle) cfg 11 split three ways for
-  // about two workgroups per CU wins instead (measured on MI355X, µs:
-  // M = 1024, K = 13824, N = 5120 174.9 -> 138.9; M = 512, K = 8192,
-  // N = 10240 108.1 -> 92.1; M = 1024, K = N = 5120 70.7 -> 66.6; 192 tiles,
-  // M = 512, K = 4096, N = 12288: cfg 14 within 2 %; split two ways it keeps
-  // winning below that: 86 tiles, M = 128, K = 4096, N = 22016).
+  // Unsplit it needs its tiles to fill 7/10 of the CUs, or K <= 4096: with
+  // 160 tiles for 256 CUs (one workgroup each, the rest idle) and longer K,
+  // cfg 11 split three ways for about two workgroups per CU wins instead
+  // (measured on MI355X, µs: M = 1024, K = 13824, N = 5120 174.9 -> 138.9;
+  // M = 512, K = 8192, N = 10240 108.1 -> 92.1; M = 1024, K = N = 5120 70.7 ->
+  // 66.6), not at K = 4096 (172 tiles, M = 256, N = 22016: 59.9 unsplit
+  // against 64.8 split two ways); 192 tiles, M = 512, K = 4096, N = 12288:
+  // cfg 14 within 2 %.  Split two ways or more it keeps winning (86 tiles,
+  // M = 128, K = 4096, N = 22016).
   const int64_t s14 = t6 > 0 ? (cus / t6 < K / 512 ? cus / t6 : K / 512) : 1;
-  if (c11 && G % 64 == 0 && t6 <= cus && (s14 > 1 || t6 * 10 >= 7 * (int64_t)cus)) {
+  const bool fills = s14 > 1 || t6 * 10 >= 7 * (int64_t)cus || K <= 4096;
+  if (c11 && G % 64 == 0 && t6 <= cus && fills) {
     int64_t s = s14;
     if (s < 1) s = 1;
     // 64 < M <= 256 on small layers: the 64-row streamed tiles (cfg 13, one
@@ -520,7 +523,7 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // K = 8192, N = 10240 188.6 -> 179.6 us on MI355X); else unsplit.
   if (M >= 1024 && c11 && t6 > cus && 3 * t6 <= 4 * (int64_t)cus && K / 64 >= 24)
     return {11, stream_splits((int)K, 3)};
-  if (M >= 1024 && (c11 || c7)) return {c11 ? 11 : 7, 1};
+  if (M >= 1024 && (c11 || c7) && t6 > cus) return {c11 ? 11 : 7, 1};
   // cfg 11 on fewer than ~448 tiles: split K for about two workgroups per CU
   // (measured on MI355X: M = 128, K = 8192, N = 28672: 77.7 us at 4 splits vs
   // 90.2 at 3; M = 256: 133.2 at 2 vs 149.8 unsplit; M = 256, K = 28672, N =
