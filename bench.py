@@ -256,6 +256,21 @@ def bench_case(case, steps: int, warmup: int, graph: bool = False, cold: bool = 
             "bytes": case.bytes(), "flops": case.flops()}
 
 
+def dense_fp16_case(case, steps: int, warmup: int) -> dict:
+    """Context for the prefill line: torch's fp16 GEMM (hipBLASLt) of the same
+    M x K x N with an fp16 W (4x the weight bytes, no dequant), timed the same
+    way (one graph replay of the calls, HIP events) right after it."""
+    import torch
+    from w4a16 import workloads as wl
+
+    X, W = (t.cuda() for t in wl.make_inputs(case))
+    y = torch.empty(case.M, case.N, dtype=torch.float16, device="cuda")
+    t = _time_calls([lambda: torch.matmul(X, W, out=y)], steps, warmup, True)
+    us = t["ms"] * 1e3
+    return {"what": "torch.matmul fp16 x fp16 (hipBLASLt), same shape and timing",
+            "us": round(us, 2), "TFLOP/s": round(case.flops() / us / 1e6, 2)}
+
+
 def bench_quantize(case, steps: int, warmup: int) -> dict:
     """quantize_weight's kernel (w4a16_quantize_pack_f16) on the case's fp16 W,
     outputs preallocated, calls queued behind the spin and timed with HIP
@@ -912,6 +927,8 @@ def main() -> int:
                          "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
                          "traffic": _traffic_for("C4_M4096")},
+            "dense_fp16": dense_fp16_case(c4, max(50, args.steps // 4),
+                                          max(10, args.warmup // 2)),
         }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c2)

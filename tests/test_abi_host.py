@@ -573,14 +573,16 @@ def test_planner_decode_table():
 def test_planner_small_batch_wide_weights_stream():
     """4 <= M <= 64 on large enough, wide weights takes the streamed prefill
     kernel with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K
-    for about 448 workgroups with >= 8 k-steps per split; narrow N, small
+    (>= 8 k-steps per split) for one workgroup per CU where up to 64 64-row
+    tiles fill 3/4 of the CUs that way, else for close to two per CU; narrow N, small
     weights, or N <= 8192 (16384 for M <= 16) with M <= 32 stay on the skinny
     kernel (or the GEMV for M <= 3)."""
     from w4a16 import _lib
 
     for M, N, K, cfg, s in ((32, 28672, 4096, 12, 4), (24, 28672, 8192, 12, 4),
                             (17, 28672, 8192, 12, 4), (64, 28672, 8192, 13, 4),
-                            (48, 14336, 4096, 13, 8), (64, 4096, 16384, 13, 22)):
+                            (48, 14336, 4096, 13, 4), (64, 4096, 16384, 13, 16),
+                            (32, 22016, 4096, 12, 6), (32, 10240, 8192, 12, 11)):
         p = _lib.plan(M, N, K, 128)
         rows = 32 if cfg == 12 else 64
         assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == cfg, (M, N, K)
@@ -721,8 +723,15 @@ def test_planner_prefill_split_k():
     for M in (128, 192, 256):
         p = _lib.plan(M, 16384, 2048, 128)
         assert (p.tile_cfg, p.split_k, p.workspace_bytes) == (13, 1, 0), M
-    # ... not with longer slices, nor beyond M = 256
-    for M, N, K in ((96, 14336, 4096), (128, 4096, 14336), (128, 8192, 8192), (384, 4096, 4096)):
+    # ... and at M <= 128 with 86..128 64-row tiles (K > 2048), split for
+    # about two workgroups per CU
+    for M, N, K, split in ((128, 12288, 4096, 4), (128, 15360, 5120, 4), (96, 14336, 4096, 4)):
+        p = _lib.plan(M, N, K, 128)
+        assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
+        assert p.grid_x == split * (N // 256) * 2
+    # ... not with longer slices, more or fewer tiles, nor beyond M = 256
+    for M, N, K in ((128, 4096, 14336), (128, 8192, 8192), (384, 4096, 4096), (128, 27648, 5120),
+                    (128, 10240, 8192)):
         assert _lib.plan(M, N, K, 128).tile_cfg == 14, (M, N, K)
     # more tiles than CUs: cfg 11
     p = _lib.plan(1024, 14336, 4096, 128)

@@ -456,11 +456,54 @@ int stream_split_for(int64_t tiles, int64_t K, int cus) {
   return s < 1 ? 1 : (int)s;
 }
 
+// k-splits for the 64-row streamed tiles when they are few (<= 64 tiles):
+// the split whose workgroups (tiles x splits, after the kernel's rounding of
+// splits to whole 4-step blocks of >= 8 steps) come closest to one per CU
+// from below, where that fills 3/4 of the CUs; 0 where it does not.  Found
+// by the planner audit (bench.py --planner-audit: static plan against every
+// other plan), measured on MI355X (µs) against the ~448 workgroups of
+// stream_split_for: M = 64, K = N = 8192 (32 tiles) 25.4 -> 23.3 at 256
+// workgroups; M = 64, K = 14336, N = 4096 (16 tiles) 26.2 -> 23.7 at 224;
+// M = 64, K = 5120, N = 15360 (60 tiles) 26.7 -> 25.5 at 240.  With more
+// tiles, and for the 32-row tiles, two per CU win (stream_split_two).
+int stream_split_one_per_cu(int64_t tiles, int64_t K, int cus) {
+  if (tiles <= 0 || tiles > 64) return 0;
+  const int64_t smax = K / 64 / 8;
+  int one = 0;
+  int64_t u1 = 0;
+  for (int64_t s = 1; s <= smax && s <= 64; ++s) {
+    const int64_t u = tiles * stream_splits((int)K, (int)s);
+    if (u <= cus && u > u1) u1 = u, one = (int)s;
+  }
+  return one && u1 * 4 >= 3 * (int64_t)cus ? one : 0;
+}
+
+// k-splits for the 32-row streamed tiles and for the 64-row ones past 64
+// tiles: the split whose workgroups (after the kernel's rounding) come
+// closest to two per CU from below, 2 % over allowed.  Against
+// stream_split_for, which ignores the rounding (µs on MI355X): M = 32,
+// K = 4096, N = 22016 (86 tiles) 23.5 -> 22.4 at 516 workgroups; M = 32,
+// K = 8192, N = 10240 (40 tiles) 24.1 -> 22.6 at 440; M = 32, K = 4096,
+// N = 28672 (112 tiles) 25.3 at 448 (224: 28.5).
+int stream_split_two(int64_t tiles, int64_t K, int cus) {
+  if (tiles <= 0) return 1;
+  const int64_t smax = K / 64 / 8;
+  int two = 1;
+  int64_t u2 = 0;
+  for (int64_t s = 1; s <= smax && s <= 64; ++s) {
+    const int64_t u = tiles * stream_splits((int)K, (int)s);
+    if (u * 100 <= 2 * (int64_t)cus * 102 && u > u2) u2 = u, two = (int)s;
+  }
+  return two;
+}
+
 MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) {
     if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return {2, 1};
     const int rows = M <= 32 ? 32 : 64;
-    const int s = stream_split_for((N + 255) / 256 * ((M + rows - 1) / rows), K, cus);
+    const int64_t tiles = (N + 255) / 256 * ((M + rows - 1) / rows);
+    const int s1 = rows == 64 ? stream_split_one_per_cu(tiles, K, cus) : 0;
+    const int s = s1 ? s1 : stream_split_two(tiles, K, cus);
     return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
@@ -505,6 +548,19 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     // (K = 4096, N = 14336, M = 96 / 128: 28.0 / 30.3 vs 28.3 / 30.2 at best;
     // K = 14336, N = 4096 and K = N = 8192 ties or slower; unsplit at K = 4096
     // 47 us at every M).
+    // M <= 128 with 86..128 64-row tiles: those, split for about two
+    // workgroups per CU (µs: M = 128, K = 5120, N = 15360, 120 tiles: 34.5 at
+    // 480 workgroups against 37.8 for cfg 14 at 240; K = 4096, N = 12288, 96
+    // tiles: 29.0 against 29.7).  Outside that range cfg 14 is as fast or
+    // faster (K = 5120, N = 27648, 216 tiles; K = 8192, N = 10240, 80 tiles);
+    // K <= 2048 keeps the unsplit 64-row tiles below.
+    if (M <= 128 && K > 2048) {
+      const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
+      if (t13 >= 86 && t13 <= 128) {
+        const int s13 = stream_split_two(t13, K, cus);
+        return {13, s13 > 1 ? stream_splits((int)K, s13) : 1};
+      }
+    }
     if (M <= 256 && s > 1) {
       const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
       if (K <= 2048 && 2 * t13 >= cus) return {13, 1};
