@@ -106,6 +106,9 @@ def _args():
                     help="markdown table of a rocprofv3 --kernel-trace CSV of bench.py: per "
                          "kernel, the durations of its last --steps dispatches (the timed "
                          "calls) and the gaps between them")
+    ap.add_argument("--trace-last", default=None, metavar="NAME=COUNT,...",
+                    help="with --trace-summary: timed-call counts for kernels whose names "
+                         "contain NAME (default --steps for all)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="markdown table of every counter in rocprofv3 --pmc runs of "
                          "--traffic-probe, per workload and kernel")
@@ -192,11 +195,15 @@ def empty_kernels(steps: int, warmup: int) -> dict:
             "steps": steps, "warmup": warmup, "kernels": out}
 
 
-def trace_summary(path: str, last: int) -> str:
+def trace_summary(path: str, last: int, per_kernel: str | None = None) -> str:
     """Markdown table from a rocprofv3 kernel-trace CSV: per kernel, the
     number of dispatches, and over its last `last` dispatches (bench.py's timed
-    calls are each kernel's last ones) the mean / median / min / max duration
-    and the mean gap from one dispatch's end to the next one's start."""
+    calls are each kernel's last ones) the mean / median / min / max duration,
+    the mean gap from one dispatch's end to the next one's start, and the span
+    from the first one's start to the last one's end per dispatch (what HIP
+    events around those calls measure).  `per_kernel` ("name=count,...")
+    gives kernels whose names contain `name` another count (the prefill line
+    times 50 calls: "stream_kernel=50,Cijk=50")."""
     import csv
     import statistics
 
@@ -205,16 +212,24 @@ def trace_summary(path: str, last: int) -> str:
         for r in csv.DictReader(f):
             by.setdefault(r["Kernel_Name"], []).append(
                 (int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
-    lines = [f"| kernel | dispatches | last {last}: mean ns | median ns | min ns | max ns | "
-             "mean gap ns |", "|---|---|---|---|---|---|---|"]
+    counts = {}
+    for item in (per_kernel or "").split(","):
+        if "=" in item:
+            k, v = item.split("=")
+            counts[k.strip()] = int(v)
+    lines = ["| kernel | dispatches | timed (last) | mean ns | median ns | min ns | max ns | "
+             "mean gap ns | span / dispatch ns |", "|---|---|---|---|---|---|---|---|---|"]
     for name, ds in sorted(by.items(), key=lambda kv: -len(kv[1])):
         ds.sort()
-        tail = ds[-last:]
+        n = next((v for k, v in counts.items() if k in name), last)
+        tail = ds[-n:]
         dur = [e - s for s, e in tail]
         gaps = [tail[i + 1][0] - tail[i][1] for i in range(len(tail) - 1)]
         gap = f"{statistics.mean(gaps):.0f}" if gaps else ""
-        lines.append(f"| `{_kernel_short(name)}` | {len(ds)} | {statistics.mean(dur):.0f} | "
-                     f"{statistics.median(dur):.0f} | {min(dur)} | {max(dur)} | {gap} |")
+        span = (tail[-1][1] - tail[0][0]) / len(tail)
+        lines.append(f"| `{_kernel_short(name)}` | {len(ds)} | {len(tail)} | "
+                     f"{statistics.mean(dur):.0f} | {statistics.median(dur):.0f} | {min(dur)} | "
+                     f"{max(dur)} | {gap} | {span:.0f} |")
     return "\n".join(lines)
 
 
@@ -733,8 +748,10 @@ def _counter_groups(path: str):
         if "spin_kernel" in name:
             gi += 1
             continue
+        # the zeros check runs once per zeros tensor (its answer is cached),
+        # not per call: left out like the quantize / pack / dequant kernels
         if gi < 0 or gi >= len(PROBE) or "w4a16" not in name or any(
-                t in name for t in ("quantize", "pack", "dequant")):
+                t in name for t in ("quantize", "pack", "dequant", "zeros_check")):
             continue
         for k, v in cs.items():
             out.setdefault(k, {}).setdefault(PROBE[gi][0], {}).setdefault(name, []).append(v)
@@ -840,7 +857,7 @@ def main() -> int:
         print(pmc_summary(args.pmc_summary))
         return 0
     if args.trace_summary:
-        print(trace_summary(args.trace_summary, args.steps))
+        print(trace_summary(args.trace_summary, args.steps, args.trace_last))
         return 0
     if args.decode_table:
         src = decode_table(args.decode_table)
