@@ -830,10 +830,30 @@ def pmc_summary(paths) -> str:
     order = {k[0]: i for i, k in enumerate(PROBE)}
     lines = ["| workload | kernel | " + " | ".join(counters) + " |",
              "|---|---|" + "---|" * len(counters)]
-    for (wkey, name), cs in sorted(rows.items(), key=lambda kv: (order.get(kv[0][0], 99), kv[0][1])):
+    ordered = sorted(rows.items(), key=lambda kv: (order.get(kv[0][0], 99), kv[0][1]))
+    for (wkey, name), cs in ordered:
         short = _kernel_short(name)
         lines.append(f"| {wkey} | `{short}` | " +
                      " | ".join(f"{cs[c]:,.0f}" if c in cs else "" for c in counters) + " |")
+    need = ("SQ_WAVES", "SQ_INSTS_VMEM_RD", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_SALU",
+            "SQ_INSTS_SMEM", "SQ_INSTS_LDS", "SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES",
+            "SQ_VALU_MFMA_BUSY_CYCLES")
+    if all(c in counters for c in need):
+        # per wave; SQ_BUSY_CYCLES counts for each of the 32 shader engines, the
+        # MFMA busy cycles for each of the 1024 SIMDs
+        lines += ["", "| workload | kernel | waves | VMEM_RD / wave | MFMA / wave | other VALU / wave "
+                  "| SALU / wave | SMEM / wave | LDS / wave | WAIT_INST_ANY / WAVE_CYCLES "
+                  "| busy cycles per SE | MFMA busy / busy |", "|---|---|" + "---|" * 10]
+        for (wkey, name), cs in ordered:
+            w = cs["SQ_WAVES"]
+            per = {c: cs[c] / w for c in need}
+            busy = cs["SQ_BUSY_CYCLES"] / 32
+            lines.append(
+                f"| {wkey} | `{_kernel_short(name)}` | {w:,.0f} | {per['SQ_INSTS_VMEM_RD']:.1f} | "
+                f"{per['SQ_INSTS_MFMA']:.1f} | {per['SQ_INSTS_VALU'] - per['SQ_INSTS_MFMA']:.1f} | "
+                f"{per['SQ_INSTS_SALU']:.1f} | {per['SQ_INSTS_SMEM']:.2f} | {per['SQ_INSTS_LDS']:.1f} | "
+                f"{100 * cs['SQ_WAIT_INST_ANY'] / cs['SQ_WAVE_CYCLES']:.0f} % | {busy:,.0f} | "
+                f"{100 * cs['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024 / busy:.0f} % |")
     return "\n".join(lines)
 
 
