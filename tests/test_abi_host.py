@@ -582,7 +582,12 @@ def test_planner_small_batch_wide_weights_stream():
     for M, N, K, cfg, s in ((32, 28672, 4096, 12, 4), (24, 28672, 8192, 12, 4),
                             (17, 28672, 8192, 12, 4), (64, 28672, 8192, 13, 4),
                             (48, 14336, 4096, 13, 4), (64, 4096, 16384, 13, 16),
-                            (32, 22016, 4096, 12, 6), (32, 10240, 8192, 12, 11)):
+                            (32, 22016, 4096, 12, 6), (32, 10240, 8192, 12, 11),
+                            # 64-row tiles whose one-per-CU split would leave < 10
+                            # k-steps take 32-row tiles one per CU
+                            (64, 5120, 5120, 12, 5), (64, 4096, 11008, 13, 15),
+                            # 64-column skinny blocks past two per CU at M > 8
+                            (16, 57344, 8192, 12, 2), (12, 57344, 8192, 12, 2)):
         p = _lib.plan(M, N, K, 128)
         rows = 32 if cfg == 12 else 64
         assert _lib.KERNEL_NAMES[p.kernel] == "mfma" and p.tile_cfg == cfg, (M, N, K)
@@ -590,6 +595,7 @@ def test_planner_small_batch_wide_weights_stream():
         assert p.split_k == s and p.workspace_bytes >= s * M * N * 4, (M, N, K, p.split_k)
         assert p.grid_x == s * ((N + 255) // 256) * ((M + rows - 1) // rows)
     for M, N, K in ((16, 4096, 4096), (16, 4096, 14336), (24, 4096, 4096), (16, 6144, 4096),
+                    (8, 57344, 8192), (16, 28672, 4096),
                     (9, 8192, 8192), (16, 28672, 4160)):      # K % 256 != 0: no streamed kernel
         assert _lib.KERNEL_NAMES[_lib.plan(M, N, K, 64).kernel] == "skinny", (M, N, K)
     # up to N = 8192 (N = 16384 for M <= 16) the skinny kernel's 32-column
@@ -696,8 +702,9 @@ def test_planner_prefill_split_k():
     assert (q.tile_cfg, q.split_k, q.workspace_bytes) == (14, 1, 0)
     assert (_lib.plan(128, 28672, 8192, 128).tile_cfg, _lib.plan(128, 28672, 8192, 128).split_k) == (14, 2)
     assert _lib.plan(512, 14336, 4096, 128).tile_cfg == 14      # C4 M = 512: 224 tiles
-    # ... at least 4 k-steps per slice: K = 4096 caps the splits at 8
-    assert _lib.plan(128, 4096, 4096, 128).split_k == 8
+    # ... K = N = 4096 at M = 128: 64-row tiles, 6 splits of >= 10 k-steps
+    p = _lib.plan(128, 4096, 4096, 128)
+    assert (p.tile_cfg, p.split_k) == (13, 6)
     # G = 32 (a scale / zero load per half-step): cfg 11 split for ~448 workgroups
     p = _lib.plan(256, 8192, 28672, 32)
     assert p.tile_cfg == 11 and p.split_k == 7 and p.grid_x == 448
@@ -713,8 +720,9 @@ def test_planner_prefill_split_k():
     p = _lib.plan(512, 1028, 2048, 64, _lib.KERNEL_MFMA, 2)
     assert (p.tile_cfg, p.split_k) == (14, 2)
     # 64 < M <= 256 on small layers: 64-row tiles (cfg 13) where cfg 14's
-    # slices would hold <= 4 k-steps, split for ~a workgroup per CU ...
-    for M, N, K, split in ((96, 4096, 4096, 8), (192, 4096, 4096, 4), (256, 4096, 4096, 4),
+    # slices would hold <= 4 k-steps, split for ~a workgroup per CU with >= 10
+    # k-steps per split ...
+    for M, N, K, split in ((96, 4096, 4096, 6), (192, 4096, 4096, 4), (256, 4096, 4096, 4),
                            (128, 4096, 2048, 4)):
         p = _lib.plan(M, N, K, 128)
         assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)

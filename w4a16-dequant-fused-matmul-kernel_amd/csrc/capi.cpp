@@ -359,8 +359,12 @@ bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t K, int64_t G, int cu
 // N = 8192: 52.5 vs 43.4), and so does G = 32 with K > 4096 (K = 8192,
 // N = 28672, M = 4 / 8: 39.9 / 41.3 vs 38.9 / 39.2; M = 8, K = N = 14336:
 // 38.4 vs 34.3).
+// Beyond two blocks per CU at M > 8 the streamed 32-row tiles win (M = 16,
+// K = 8192, N = 57344, 896 blocks: 69.6 vs 65.7 split 2; 448 blocks,
+// N = 28672, K = 4096 / 5120: 20.1 / 25.2, the best plan).
 bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  return M <= 16 && N % 4 == 0 && (G % 64 == 0 || K <= 4096) && (N + 63) / 64 > cus / 2;
+  return M <= 16 && N % 4 == 0 && (G % 64 == 0 || K <= 4096) && (N + 63) / 64 > cus / 2 &&
+         (M <= 8 || (N + 63) / 64 <= 2 * (int64_t)cus);
 }
 
 // Skinny blocks with one 16-row group per workgroup (plan tile_m = 16) for
@@ -456,16 +460,20 @@ int stream_split_for(int64_t tiles, int64_t K, int cus) {
   return s < 1 ? 1 : (int)s;
 }
 
-// k-splits for the 64-row streamed tiles when they are few (<= 64 tiles):
-// the split whose workgroups (tiles x splits, after the kernel's rounding of
-// splits to whole 4-step blocks of >= 8 steps) come closest to one per CU
-// from below, where that fills 3/4 of the CUs; 0 where it does not.  Found
-// by the planner audit (bench.py --planner-audit: static plan against every
-// other plan), measured on MI355X (µs) against the ~448 workgroups of
-// stream_split_for: M = 64, K = N = 8192 (32 tiles) 25.4 -> 23.3 at 256
-// workgroups; M = 64, K = 14336, N = 4096 (16 tiles) 26.2 -> 23.7 at 224;
-// M = 64, K = 5120, N = 15360 (60 tiles) 26.7 -> 25.5 at 240.  With more
-// tiles, and for the 32-row tiles, two per CU win (stream_split_two).
+// k-splits for streamed tiles when they are few (<= 64 tiles): the split
+// whose workgroups (tiles x splits, after the kernel's rounding of splits to
+// whole 4-step blocks of >= 8 steps) come closest to one per CU from below,
+// where that fills 3/4 of the CUs with at least 10 64-k steps per split; 0
+// where it does not.
+// Found by the planner audit (bench.py --planner-audit: static plan against
+// every other plan), measured on MI355X (µs) against the ~448 workgroups of
+// stream_split_for, 64-row tiles: M = 64, K = N = 8192 (32 tiles) 25.4 ->
+// 23.3 at 256 workgroups; M = 64, K = 14336, N = 4096 (16 tiles) 26.2 ->
+// 23.7 at 224; M = 64, K = 5120, N = 15360 (60 tiles) 26.7 -> 25.5 at 240.
+// Shorter splits lose: M = 64, K = N = 5120 (20 tiles) 19.7 at 200
+// workgroups of 8 steps against 18.6 for 40 32-row tiles at 200 of 16
+// steps (K = 11008, 16 tiles: 22.0 at 240 of 12 steps, the best plan).
+// With more tiles, and for M <= 32, two per CU win (stream_split_two).
 int stream_split_one_per_cu(int64_t tiles, int64_t K, int cus) {
   if (tiles <= 0 || tiles > 64) return 0;
   const int64_t smax = K / 64 / 8;
@@ -475,7 +483,9 @@ int stream_split_one_per_cu(int64_t tiles, int64_t K, int cus) {
     const int64_t u = tiles * stream_splits((int)K, (int)s);
     if (u <= cus && u > u1) u1 = u, one = (int)s;
   }
-  return one && u1 * 4 >= 3 * (int64_t)cus ? one : 0;
+  if (!one || u1 * 4 < 3 * (int64_t)cus) return 0;
+  const int64_t splits = stream_splits((int)K, one);
+  return (K / 64 + splits - 1) / splits >= 10 ? one : 0;
 }
 
 // k-splits for the 32-row streamed tiles and for the 64-row ones past 64
@@ -502,8 +512,15 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return {2, 1};
     const int rows = M <= 32 ? 32 : 64;
     const int64_t tiles = (N + 255) / 256 * ((M + rows - 1) / rows);
-    const int s1 = rows == 64 ? stream_split_one_per_cu(tiles, K, cus) : 0;
-    const int s = s1 ? s1 : stream_split_two(tiles, K, cus);
+    if (rows == 64) {
+      // 64-row tiles one per CU, else 32-row tiles one per CU, else 64-row
+      // tiles two per CU
+      const int s1 = stream_split_one_per_cu(tiles, K, cus);
+      if (s1) return {13, s1 > 1 ? stream_splits((int)K, s1) : 1};
+      const int s32 = stream_split_one_per_cu(2 * tiles, K, cus);
+      if (s32) return {12, s32 > 1 ? stream_splits((int)K, s32) : 1};
+    }
+    const int s = stream_split_two(tiles, K, cus);
     return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
@@ -564,9 +581,12 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     if (M <= 256 && s > 1) {
       const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
       if (K <= 2048 && 2 * t13 >= cus) return {13, 1};
+      // from K = 4096 at least 10 k-steps per split (M = 128, K = N = 4096,
+      // 32 tiles: 20.0 us at 6 splits of 11 steps against 20.7 at 8 of 8
+      // steps); shorter K keeps 8 (measured at K = 4096 only)
       if (K / s <= 512) {
         int64_t s13 = cus / t13;
-        if (s13 > K / 512) s13 = K / 512;
+        if (s13 > K / (K >= 4096 ? 640 : 512)) s13 = K / (K >= 4096 ? 640 : 512);
         if (s13 < 1) s13 = 1;
         return {13, s13 > 1 ? stream_splits((int)K, (int)s13) : 1};
       }
