@@ -347,6 +347,34 @@ def test_dequant_equals_numpy_fp16_arithmetic():
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+def test_fp16_subtract_is_one_rounding_for_every_zero():
+    """The any-zero kernels compute fp16(q) - z with one hardware RNE subtract.
+    For every finite fp16 zero-point and every code, numpy's fp16 subtraction
+    (the oracle's arithmetic) equals the exact difference (float64 holds it
+    exactly) rounded once to fp16; and the oracle's dequant with such zeros is
+    that rounding followed by one rounding of the product (exact in float64:
+    11-bit x 11-bit significands)."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    z = bits.view(np.float16)
+    z = z[np.isfinite(z)]
+    q = np.arange(16, dtype=np.float16)
+    got = q[:, None] - z[None, :]
+    exact = q.astype(np.float64)[:, None] - z.astype(np.float64)[None, :]
+    with np.errstate(over="ignore"):
+        once = exact.astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), once.view(np.uint16))
+    # the oracle's dequant: zeros spread over 16 columns per code row block
+    rng = np.random.default_rng(11)
+    zs = rng.choice(z, size=4096).astype(np.float16)
+    ss = rng.uniform(1e-3, 0.2, size=4096).astype(np.float16)
+    qcodes = np.tile(np.arange(16, dtype=np.int32)[:, None], (1, 4096))
+    dq = O.dequantize_weight(O.pack_int4(qcodes), ss[None, :], zs[None, :], 16)
+    with np.errstate(over="ignore", invalid="ignore"):
+        a = (qcodes.astype(np.float64) - zs.astype(np.float64)[None, :]).astype(np.float16)
+        ref = (a.astype(np.float64) * ss.astype(np.float64)[None, :]).astype(np.float16)
+    assert np.array_equal(dq.view(np.uint16), ref.view(np.uint16))
+
+
 def test_dequant_constant_group_is_exact():
     """Reference test_quant.py:93-100."""
     W = np.zeros((128, 8), np.float16)
