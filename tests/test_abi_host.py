@@ -702,6 +702,17 @@ def test_planner_prefill_split_k():
     assert (q.tile_cfg, q.split_k, q.workspace_bytes) == (14, 1, 0)
     assert (_lib.plan(128, 28672, 8192, 128).tile_cfg, _lib.plan(128, 28672, 8192, 128).split_k) == (14, 2)
     assert _lib.plan(512, 14336, 4096, 128).tile_cfg == 14      # C4 M = 512: 224 tiles
+    # long rows (K >= 16384) on fewer tiles than CUs: cfg 11 split along K --
+    # from 86 tiles the most of 8 / 4 / 2 splits within three workgroups per
+    # CU, from K = 24576 with more than 64 tiles about two per CU; 64 tiles
+    # and shorter rows below 86 tiles keep cfg 14
+    for M, N, K, cfg, split in ((384, 8192, 28672, 11, 8), (512, 8192, 28672, 11, 4),
+                                (768, 8192, 28672, 11, 4), (768, 8192, 16384, 11, 4),
+                                (768, 10240, 20480, 11, 2), (384, 6144, 28672, 11, 7),
+                                (512, 5120, 28672, 11, 6), (256, 8192, 28672, 14, 4),
+                                (512, 5120, 16384, 14, 3)):
+        p = _lib.plan(M, N, K, 128)
+        assert (p.tile_cfg, p.split_k) == (cfg, split), (M, N, K, p.tile_cfg, p.split_k)
     # ... K = N = 4096 at M = 128: 64-row tiles, 6 splits of >= 10 k-steps
     p = _lib.plan(128, 4096, 4096, 128)
     assert (p.tile_cfg, p.split_k) == (13, 6)

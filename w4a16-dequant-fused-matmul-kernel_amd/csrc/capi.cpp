@@ -591,6 +591,30 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
         return {13, s13 > 1 ? stream_splits((int)K, (int)s13) : 1};
       }
     }
+    // Long rows (K >= 16384) on fewer tiles than CUs: cfg 11 (two workgroups
+    // resident per CU) split along K, whose partials and reduction are small
+    // beside rows that long -- from 86 tiles the most of eight, four or two
+    // splits that makes at most three workgroups per CU, and from K = 24576
+    // with more than 64 tiles split for about two workgroups per CU.  Measured on
+    // MI355X (planner audit, µs, against cfg 14's plan), N = 8192: K = 28672,
+    // M = 384 (96 tiles) 177.1 at eight splits (185.2 at four); M = 512 (128
+    // tiles) 218.8 -> 209.8; M = 768 (192 tiles), K = 28672 / 20480 / 16384
+    // 365.0 / 272.0 / 207.8 -> 330.1 / 241.2 / 199.3; N = 10240, K = 20480,
+    // M = 768 (240 tiles) 285.4 at two splits (300.6 at four); N = 5120,
+    // K = 16384, M = 768 (120 tiles) 124.2, best; K = 28672: 72 tiles (N =
+    // 6144, M = 384) 145.7 -> 138.4 (6 splits), 80 (N = 5120, M = 512) 144.0
+    // (6), best; 64 tiles (N = 8192, M = 256) keep cfg 14 at four splits, a
+    // tie (116.4 against 115.3 at eight) with half the partials, and so do
+    // shorter rows (K = 16384, 80 tiles: 91.8 with three splits, best; K =
+    // 11008, 128 tiles, M = 1024, N = 4096: 92.3, best).
+    if (K >= 16384 && t6 < cus) {
+      if (t6 >= 86) {
+        const int64_t w3 = 3 * (int64_t)cus;
+        return {11, stream_splits((int)K, t6 * 8 <= w3 ? 8 : t6 * 4 <= w3 ? 4 : 2)};
+      }
+      if (K >= 24576 && t6 > 64)
+        return {11, stream_splits((int)K, stream_split_two(t6, K, cus))};
+    }
     return {14, s > 1 ? stream_splits((int)K, (int)s, 2) : 1};
   }
   // M >= 1024 with more tiles than CUs but fewer than two per CU: split K
