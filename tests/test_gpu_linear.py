@@ -63,3 +63,26 @@ def test_forward_leading_dims_and_state_dict(shape):
     fresh = W4A16Linear(1024, 260, group_size=128, device=DEV)
     fresh.load_state_dict(qlin.state_dict())
     assert torch.equal(fresh(x), y)
+
+
+def test_forward_any_input_layout():
+    """forward takes x in any layout the reference accepts (it reshapes and
+    copies to contiguous rows): a row-strided column slice runs in place (the
+    kernels take rows >= K apart), a transposed view and a broadcast row
+    (stride 0) are copied first; all give the contiguous input's bits."""
+    from w4a16 import W4A16Linear
+
+    log("linear input layouts")
+    torch.manual_seed(5)
+    lin = torch.nn.Linear(512, 132, bias=True).to(DEV).half()
+    qlin = W4A16Linear.from_linear(lin, group_size=64)
+    wide = torch.randn(6, 640, dtype=torch.float16, device=DEV)
+    for what, x in (("column slice", wide[:, 64:576]),
+                    ("transposed", wide[:, :512].t().contiguous().t()),
+                    ("broadcast row", wide[:1, :512].expand(6, 512)),
+                    ("3-d slice", wide.view(2, 3, 640)[..., 100:612])):
+        y = qlin(x)
+        assert torch.equal(y, qlin(x.contiguous())), what
+        ref = O.linear_forward(np_(x.reshape(-1, 512)), np_(qlin.qweight), np_(qlin.scales),
+                               np_(qlin.zeros), np_(qlin.bias), 64)
+        assert_gemm_close(y.reshape(-1, 132), ref, what)

@@ -1,14 +1,17 @@
-"""``W4A16Linear`` -- drop-in ``nn.Linear`` replacement on the MI355X kernels.
+"""``W4A16Linear``: an ``nn.Linear`` stand-in whose weight lives as packed uint4.
 
-Same constructor, buffers (names, dtypes, shapes -- so ``state_dict`` files
-interchange with the reference's), ``from_linear``, ``quantize_from_dense`` and
-``forward`` as the reference (w4a16-kernel/src/w4a16/linear.py:19-98).
+Interface of the reference module (w4a16-kernel/src/w4a16/linear.py:19-98):
+the constructor's arguments, the four buffers (names, dtypes and shapes, so a
+``state_dict`` saved by either loads into the other), ``from_linear``,
+``quantize_from_dense``, ``forward`` and the exception types
+(``ValueError`` for sizes the packing cannot hold, ``AssertionError`` for bad
+inputs).
 
-``nn.Linear`` stores weight as [out, in] = [N, K]; the logical weight here is
-[K, N], so ``from_linear`` transposes before quantising (linear.py:66).
-``forward`` flattens leading dims, runs the fused GEMM and adds the bias with the
-reference's arithmetic (fp16 GEMM result, then an fp16 ``+ bias``), the add fused
-into the kernel epilogue instead of a second kernel.
+Layout: ``nn.Linear.weight`` is [out_features, in_features] = [N, K]; this
+module's logical weight is [K, N] (``y = x @ W``), so ``from_linear``
+quantises the transpose.  ``forward`` keeps the reference's arithmetic -- the
+GEMM result rounded to fp16, then an fp16 ``+ bias`` -- with the bias add done
+in the GEMM kernel's epilogue rather than by a second kernel.
 """
 from __future__ import annotations
 
@@ -21,15 +24,29 @@ from .quant import quantize_weight
 __all__ = ["W4A16Linear"]
 
 
-class W4A16Linear(nn.Module):
-    """Linear layer holding its weight as packed uint4 codes, computing in fp16.
+def _check_sizes(in_features: int, group_size: int) -> None:
+    # eight 4-bit codes per int32 word along K, whole quantisation groups
+    if in_features % 8:
+        raise ValueError(f"W4A16Linear: in_features ({in_features}) is not a multiple of 8, "
+                         "the codes packed per int32 word")
+    if in_features % group_size:
+        raise ValueError(f"W4A16Linear: in_features ({in_features}) is not a whole number of "
+                         f"groups of {group_size}")
 
-    K = ``in_features``, N = ``out_features``, G = ``group_size``.  The module
-    owns four buffers and no parameters (it is for inference): the packed codes
-    ``qweight`` (int32, K/8 rows of N words, eight 4-bit codes per word along
-    K), the per-group ``scales`` and ``zeros`` (fp16, K/G rows of N), and an
-    fp16 ``bias`` of N entries, or ``None`` when built with ``bias=False``.
-    Buffers start zeroed; ``from_linear`` or ``quantize_from_dense`` fills them.
+
+class W4A16Linear(nn.Module):
+    """Inference linear layer: fp16 activations, weight as packed uint4 codes.
+
+    With K = ``in_features``, N = ``out_features`` and G = ``group_size`` the
+    module holds buffers only (no parameters):
+
+    * ``qweight`` int32 [K/8, N]: word (i, n) packs the codes of rows 8i..8i+7
+      of column n, row 8i + j in bits [4j, 4j + 4);
+    * ``scales``, ``zeros`` fp16 [K/G, N]: one scale and zero-point per group
+      of G rows and column;
+    * ``bias`` fp16 [N], or ``None`` for ``bias=False``.
+
+    All start zeroed; ``from_linear`` or ``quantize_from_dense`` fills them.
     """
 
     def __init__(
@@ -41,64 +58,68 @@ class W4A16Linear(nn.Module):
         device: torch.device | str | None = None,
     ) -> None:
         super().__init__()
-        if in_features % 8 != 0:
-            raise ValueError(f"in_features={in_features} must be divisible by 8")
-        if in_features % group_size != 0:
-            raise ValueError(f"in_features={in_features} must be divisible by group_size={group_size}")
+        _check_sizes(in_features, group_size)
         self.in_features = in_features
         self.out_features = out_features
         self.group_size = group_size
 
-        K, N = in_features, out_features
-        self.register_buffer("qweight", torch.zeros((K // 8, N), dtype=torch.int32, device=device))
-        self.register_buffer("scales", torch.zeros((K // group_size, N), dtype=torch.float16, device=device))
-        self.register_buffer("zeros", torch.zeros((K // group_size, N), dtype=torch.float16, device=device))
+        def blank(rows: int, dtype: torch.dtype) -> Tensor:
+            return torch.zeros((rows, out_features), dtype=dtype, device=device)
+
+        n_groups = in_features // group_size
+        self.register_buffer("qweight", blank(in_features // 8, torch.int32))
+        self.register_buffer("scales", blank(n_groups, torch.float16))
+        self.register_buffer("zeros", blank(n_groups, torch.float16))
         if bias:
-            self.register_buffer("bias", torch.zeros(N, dtype=torch.float16, device=device))
+            self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16,
+                                                     device=device))
         else:
             self.bias = None
 
     @classmethod
     def from_linear(cls, linear: nn.Linear, group_size: int = 128) -> "W4A16Linear":
-        """Quantise an existing ``nn.Linear`` (linear.py:55-70)."""
-        N, K = linear.weight.shape
-        mod = cls(
-            in_features=K,
-            out_features=N,
-            group_size=group_size,
-            bias=linear.bias is not None,
-            device=linear.weight.device,
-        )
-        W = linear.weight.detach().t().contiguous()  # [N, K] -> [K, N]
-        mod.quantize_from_dense(W)
-        if linear.bias is not None:
-            mod.bias.copy_(linear.bias.detach().to(torch.float16))
-        return mod
+        """A quantised copy of ``linear`` (reference linear.py:55-70), on the
+        same device; its bias, if any, converted to fp16."""
+        out_features, in_features = linear.weight.shape
+        has_bias = linear.bias is not None
+        layer = cls(in_features, out_features, group_size=group_size, bias=has_bias,
+                    device=linear.weight.device)
+        # [out, in] -> the [K, N] layout quantize_weight expects
+        layer.quantize_from_dense(linear.weight.detach().t().contiguous())
+        if has_bias:
+            layer.bias.copy_(linear.bias.detach().to(torch.float16))
+        return layer
 
     def quantize_from_dense(self, W: Tensor) -> None:
-        """Quantise a dense ``W`` of shape [K, N] into the buffers (linear.py:72-80)."""
-        assert W.shape == (self.in_features, self.out_features), (
-            f"expected weight [K,N]={(self.in_features, self.out_features)}, got {tuple(W.shape)}"
-        )
-        qweight, scales, zeros = quantize_weight(W, self.group_size)
-        self.qweight.copy_(qweight.to(self.qweight.device))
-        self.scales.copy_(scales.to(self.scales.device))
-        self.zeros.copy_(zeros.to(self.zeros.device))
+        """Fill the buffers from a dense [K, N] weight (reference linear.py:72-80),
+        with ``quantize_weight``'s group-wise uint4 quantisation."""
+        want = (self.in_features, self.out_features)
+        if tuple(W.shape) != want:
+            raise AssertionError(f"quantize_from_dense: W must be [in_features, out_features] = "
+                                 f"{list(want)}, got {list(W.shape)}")
+        packed = quantize_weight(W, self.group_size)
+        for buf, val in zip((self.qweight, self.scales, self.zeros), packed):
+            buf.copy_(val.to(buf.device))
+        # codes from quantize_weight have integer zero-points: no zeros check
         mark_integer_zeros(self.zeros)
 
     def forward(self, x: Tensor) -> Tensor:
-        """y = (x @ dequant(W)) + bias over the last dim (linear.py:82-92)."""
-        assert x.dtype == torch.float16, f"x must be fp16, got {x.dtype}"
-        assert x.shape[-1] == self.in_features, (
-            f"x last dim {x.shape[-1]} != in_features {self.in_features}"
-        )
-        orig_shape = x.shape
-        x2d = x.reshape(-1, self.in_features).contiguous()
-        y = w4a16_linear(x2d, self.qweight, self.scales, self.zeros, self.bias, self.group_size)
-        return y.reshape(*orig_shape[:-1], self.out_features)
+        """``fp16(x @ dequant(W)) + bias`` over the last dimension of ``x``
+        (reference linear.py:82-92); leading dimensions are kept."""
+        if x.dtype != torch.float16:
+            raise AssertionError(f"W4A16Linear expects fp16 activations, got {x.dtype}")
+        if x.shape[-1] != self.in_features:
+            raise AssertionError(f"W4A16Linear: last dimension of x is {x.shape[-1]}, "
+                                 f"in_features is {self.in_features}")
+        lead = x.shape[:-1]
+        rows = x.reshape(-1, self.in_features)
+        # the kernels take rows at any stride >= K with unit inner stride
+        if rows.stride(-1) != 1 or rows.stride(0) < self.in_features:
+            rows = rows.contiguous()
+        y = w4a16_linear(rows, self.qweight, self.scales, self.zeros, self.bias, self.group_size)
+        return y.view(*lead, self.out_features)
 
     def extra_repr(self) -> str:
-        return (
-            f"in_features={self.in_features}, out_features={self.out_features}, "
-            f"group_size={self.group_size}, bias={self.bias is not None}"
-        )
+        bias = self.bias is not None
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"group_size={self.group_size}, bias={bias}")
