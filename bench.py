@@ -96,12 +96,14 @@ def _args():
     ap.add_argument("--audit-shapes", default=None,
                     help="comma list of KxN (default: AUDIT_SHAPES)")
     ap.add_argument("--audit-ms", default=None, help="comma list of M (default: AUDIT_MS)")
+    ap.add_argument("--audit-g", type=int, default=128, help="group size of the audit (default 128)")
     ap.add_argument("--decode-scan", metavar="OUT_JSON",
-                    help="time every GEMV and skinny plan for M = 1, 2 (G = 128) over the "
-                         "DECODE_KS x DECODE_NS grid, cold weights; JSON for --decode-table")
-    ap.add_argument("--decode-table", metavar="SCAN_JSON",
+                    help="time every GEMV and skinny plan for M = 1, 2 (G = --audit-g) over "
+                         "the DECODE_KS x DECODE_NS grid, cold weights; JSON for --decode-table")
+    ap.add_argument("--decode-table", metavar="SCAN_JSON", nargs="+",
                     help="write csrc/decode_table.inc (the planner's measured M <= 2 table) "
-                         "from a --decode-scan file")
+                         "from --decode-scan files (group-size classes they do not cover keep "
+                         "their current entries)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="markdown table of a rocprofv3 --kernel-trace CSV of bench.py: per "
                          "kernel, the durations of its last --steps dispatches (the timed "
@@ -466,26 +468,48 @@ def decode_scan(out_path: str, ks=None, ns=None, ms=(1, 2), G: int = 128) -> Non
                 json.dump(res, f)
 
 
-def decode_table(scan_path: str) -> str:
-    """C source of the planner's M <= 2 table from a --decode-scan file: per
-    measured (M, K, N) the fastest plan (family, configuration, column block or
-    row group, k-split)."""
-    with open(scan_path) as f:
-        rows = json.load(f)
-    lines = ["// Generated by `python bench.py --decode-table <scan.json>` from",
-             "// `python bench.py --decode-scan <scan.json>` on one MI355X (256 CUs): per",
-             "// (M, K, N) of the grid, G = 128, cold weights, the fastest GEMV / skinny",
-             "// plan.  Fields: M, K, N, kernel (1 GEMV, 4 skinny), tile_cfg, tile_n,",
-             "// tile_m (skinny rows), split_k, µs x 100 of the fastest, of the plan",
-             "// the rules gave.",
+def decode_table(scan_paths) -> str:
+    """C source of the planner's M <= 2 table from --decode-scan files: per
+    group-size class (128: G % 128 == 0, 64: G % 64 == 0, 32: other G % 32 == 0)
+    and measured (M, K, N) the fastest plan (family, configuration, column
+    block or row group, k-split).  Classes the files do not cover keep the
+    entries the current table holds for them."""
+    def gclass(G: int) -> int:
+        return 128 if G % 128 == 0 else 64 if G % 64 == 0 else 32
+
+    rows = []
+    for path in scan_paths:
+        with open(path) as f:
+            rows += json.load(f)
+    scanned = {gclass(r.get("G", 128)) for r in rows}
+    kept = []
+    if os.path.exists(DECODE_TABLE):
+        for ln in open(DECODE_TABLE).read().splitlines():
+            if ln.startswith("{") and int(ln[1:].split(",")[0]) not in scanned:
+                kept.append(ln)
+    lines = ["// Generated by `python bench.py --decode-table <scan.json> ...` from",
+             "// `python bench.py --decode-scan <scan.json> [--audit-g G]` on one MI355X",
+             "// (256 CUs): per group-size class (128: G % 128 == 0, 64: G % 64 == 0,",
+             "// 32: other G % 32 == 0) and (M, K, N) of the grid, cold weights, the",
+             "// fastest GEMV / skinny plan.  Fields: G class, M, K, N, kernel (1 GEMV,",
+             "// 4 skinny), tile_cfg, tile_n, tile_m (skinny rows), split_k, µs x 100 of",
+             "// the fastest, of the plan the planner gave when scanned.",
              "// clang-format off"]
-    for r in sorted(rows, key=lambda r: (r["M"], r["K"], r["N"])):
+    new = []
+    for r in rows:
         us = r["us"]
         best = min(us, key=us.get)
         p = r["plans"][best]
-        lines.append(f"{{{r['M']}, {r['K']}, {r['N']}, {p['kernel']}, {p['tile_cfg']}, "
-                     f"{p['tile_n']}, {p['tile_m']}, {p['split_k']}, {round(100 * us[best])}, "
-                     f"{round(100 * us['static'])}}},")
+        new.append(((gclass(r.get("G", 128)), r["M"], r["K"], r["N"]),
+                    f"{{{gclass(r.get('G', 128))}, {r['M']}, {r['K']}, {r['N']}, {p['kernel']}, "
+                    f"{p['tile_cfg']}, {p['tile_n']}, {p['tile_m']}, {p['split_k']}, "
+                    f"{round(100 * us[best])}, {round(100 * us['static'])}}},"))
+    for ln in kept:
+        f = [int(v) for v in ln.strip("{},").split(",")[:4]]
+        new.append((tuple(f), ln))
+    order = {128: 0, 64: 1, 32: 2}
+    new.sort(key=lambda t: (order[t[0][0]], t[0][1], t[0][2], t[0][3]))
+    lines += [ln for _, ln in new]
     lines.append("// clang-format on")
     return "\n".join(lines) + "\n"
 
@@ -883,7 +907,8 @@ def main() -> int:
         src = decode_table(args.decode_table)
         with open(DECODE_TABLE, "w") as f:
             f.write(src)
-        print(f"wrote {DECODE_TABLE} ({src.count(chr(10)) - 8} entries)")
+        n = sum(1 for ln in src.splitlines() if ln.startswith("{"))
+        print(f"wrote {DECODE_TABLE} ({n} entries)")
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -903,7 +928,7 @@ def main() -> int:
         print(json.dumps(empty_kernels(args.steps, args.warmup)), flush=True)
         return 0
     if args.decode_scan:
-        decode_scan(args.decode_scan)
+        decode_scan(args.decode_scan, G=args.audit_g)
         return 0
     if args.planner_audit:
         shapes = AUDIT_SHAPES
@@ -913,7 +938,7 @@ def main() -> int:
                 (f"{k}x{n}", k, n) for k, n in want if (k, n) not in
                 {(a[1], a[2]) for a in AUDIT_SHAPES}]
         ms = [int(m) for m in args.audit_ms.split(",")] if args.audit_ms else AUDIT_MS
-        print(planner_audit(shapes, ms), flush=True)
+        print(planner_audit(shapes, ms, G=args.audit_g), flush=True)
         return 0
     if args.reference_table:
         print(json.dumps(reference_table(args.reference_json)), flush=True)

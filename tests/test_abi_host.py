@@ -511,63 +511,75 @@ def test_planner_gemv_blocks_and_waves():
 
 
 def _decode_table():
-    """Entries of csrc/decode_table.inc: (M, K, N, kernel, cfg, cols, rows, split)."""
+    """Entries of csrc/decode_table.inc: (G class, M, K, N, kernel, cfg, cols, rows, split)."""
     path = os.path.join(ROOT, "w4a16-dequant-fused-matmul-kernel_amd", "csrc", "decode_table.inc")
     rows = []
     for line in open(path):
-        m = re.match(r"\{(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\},", line)
+        m = re.match(r"\{(\d+)" + r", (\d+)" * 10 + r"\},", line)
         if m:
-            rows.append(tuple(int(v) for v in m.groups()[:8]))
+            rows.append(tuple(int(v) for v in m.groups()[:9]))
     return rows
 
 
 def test_planner_decode_table():
-    """M <= 2 with G % 128 == 0 inside the measured grid's K and N range: the
-    automatic plan is the grid's fastest plan (csrc/decode_table.inc) at every
-    grid point and the nearest grid point's (log2 K, log2 N) between them;
-    other group sizes and shapes outside the range follow the rules."""
+    """M <= 2 inside a group-size class's measured grid (class 128: G % 128 ==
+    0; 64: G % 64 == 0; 32: the other G % 32 == 0): the automatic plan is the
+    grid's fastest plan (csrc/decode_table.inc) at every grid point and the
+    nearest grid point's in (log2 K, log2 N) between them, for any G of the
+    class; shapes outside the grid follow the rules."""
     import math
 
     from w4a16 import _lib
 
     table = _decode_table()
-    assert len(table) >= 300
-    assert {r[0] for r in table} == {1, 2}
-    kmin, kmax = min(r[1] for r in table), max(r[1] for r in table)
-    nmin, nmax = min(r[2] for r in table), max(r[2] for r in table)
+    classes = sorted({r[0] for r in table})
+    assert 128 in classes and set(classes) <= {32, 64, 128}
+    members = {128: (128, 256), 64: (64, 192), 32: (32, 96)}
+    for gc in classes:
+        sub = [r[1:] for r in table if r[0] == gc]
+        assert len(sub) >= 300 and {r[0] for r in sub} == {1, 2}, gc
+        ks, ns = sorted({r[1] for r in sub}), sorted({r[2] for r in sub})
+        assert len(sub) == 2 * len(ks) * len(ns), "a full grid per M"
+        kmin, kmax, nmin, nmax = ks[0], ks[-1], ns[0], ns[-1]
 
-    def expect(M, K, N):
-        best = min((r for r in table if r[0] == M),
-                   key=lambda r: math.log2(K / r[1]) ** 2 + math.log2(N / r[2]) ** 2)
-        return best
+        def expect(M, K, N):
+            return min((r for r in sub if r[0] == M),
+                       key=lambda r: math.log2(K / r[1]) ** 2 + math.log2(N / r[2]) ** 2)
 
-    def check(M, K, N, G=128):
-        p = _lib.plan(M, N, K, G)
-        e = expect(M, K, N)
-        kern, cfg, cols, rows, split = e[3:8]
-        assert p.kernel == kern and p.tile_cfg == cfg, (M, K, N, e, p.as_dict())
-        if kern == _lib.KERNEL_GEMV:
-            assert (p.tile_n, p.split_k) == (cols, split), (M, K, N, e, p.as_dict())
-            assert p.workspace_bytes == (split * M * N * 4 if split > 1 else 0)
-            assert p.grid_x == -(-N // cols) * split
-        else:
-            assert (p.tile_n, p.tile_m, p.split_k) == (cols, rows, 1), (M, K, N, e, p.as_dict())
+        def check(M, K, N, G):
+            p = _lib.plan(M, N, K, G)
+            e = expect(M, K, N)
+            kern, cfg, cols, rows, split = e[3:8]
+            assert p.kernel == kern and p.tile_cfg == cfg, (G, M, K, N, e, p.as_dict())
+            if kern == _lib.KERNEL_GEMV:
+                assert (p.tile_n, p.split_k) == (cols, split), (G, M, K, N, e, p.as_dict())
+                assert p.workspace_bytes == (split * M * N * 4 if split > 1 else 0)
+                assert p.grid_x == -(-N // cols) * split
+            else:
+                assert (p.tile_n, p.tile_m, p.split_k) == (cols, rows, 1), (G, M, K, N, e)
 
-    for r in table:
-        check(r[0], r[1], r[2])
-    rng = np.random.default_rng(5)
-    for _ in range(300):
-        M = int(rng.integers(1, 3))
-        K = int(rng.integers(-(-kmin // 128), kmax // 128 + 1)) * 128
-        N = int(rng.integers(nmin // 4, nmax // 4 + 1)) * 4
-        check(M, K, N)
-    # outside the table's domain the rules decide alike for every group size:
+        for r in sub:
+            if all(r[1] % G == 0 for G in members[gc]):
+                for G in members[gc]:
+                    check(r[0], r[1], r[2], G)
+            else:
+                check(r[0], r[1], r[2], gc)
+        rng = np.random.default_rng(5)
+        for _ in range(300):
+            M = int(rng.integers(1, 3))
+            G = members[gc][int(rng.integers(0, 2))]
+            K = int(rng.integers(-(-kmin // G), kmax // G + 1)) * G
+            N = int(rng.integers(nmin // 4, nmax // 4 + 1)) * 4
+            if kmin <= K <= kmax:
+                check(M, K, N, G)
+    # outside the grid's domain the rules decide alike for every group size:
     # N or K outside the grid
+    sub = [r[1:] for r in table if r[0] == 128]
+    kmin, kmax = min(r[1] for r in sub), max(r[1] for r in sub)
+    nmin, nmax = min(r[2] for r in sub), max(r[2] for r in sub)
     for M, N, K in ((1, nmin // 2, kmax), (2, nmin, 2 * kmax), (1, 2 * nmax, kmin), (2, nmin, kmin // 2)):
         a, b = _lib.plan(M, N, K, 128).as_dict(), _lib.plan(M, N, K, 64).as_dict()
         assert a == b, (M, N, K, a, b)
-    # inside it, a smaller group size follows the rules (here unlike the table)
-    assert _lib.plan(1, 10240, 8192, 64).as_dict() != _lib.plan(1, 10240, 8192, 128).as_dict()
 
 
 def test_planner_small_batch_wide_weights_stream():
@@ -716,9 +728,16 @@ def test_planner_prefill_split_k():
     # ... K = N = 4096 at M = 128: 64-row tiles, 6 splits of >= 10 k-steps
     p = _lib.plan(128, 4096, 4096, 128)
     assert (p.tile_cfg, p.split_k) == (13, 6)
-    # G = 32 (a scale / zero load per half-step): cfg 11 split for ~448 workgroups
+    # G = 32 (a scale / zero load per half-step): the same cfg 14 rules, except
+    # long rows from 60 tiles and 80..128 tiles past K = 4096, which take cfg 11
+    # split for about two workgroups per CU
     p = _lib.plan(256, 8192, 28672, 32)
-    assert p.tile_cfg == 11 and p.split_k == 7 and p.grid_x == 448
+    assert (p.tile_cfg, p.split_k, p.grid_x) == (11, 8, 512)
+    assert (_lib.plan(256, 8192, 28672, 128).tile_cfg, _lib.plan(256, 8192, 28672, 128).split_k) == (14, 4)
+    assert (_lib.plan(256, 28672, 8192, 32).tile_cfg, _lib.plan(256, 28672, 8192, 32).split_k) == (14, 1)
+    p = _lib.plan(512, 5120, 5120, 32)                          # 80 tiles
+    assert (p.tile_cfg, p.split_k) == (11, 5)
+    assert _lib.plan(512, 5120, 5120, 128).tile_cfg == 14
     # splits never take the streamed tiles past two workgroups per CU (512
     # without a device): 296 tiles stay unsplit, 148 64-row tiles split 3 ways
     p = _lib.plan(256, 37888, 3584, 128)

@@ -6,10 +6,12 @@
 // package maps them to the reference's exception types.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <climits>
 #include <cmath>
 #include <mutex>
+#include <vector>
 
 #include "../../include/w4a16.h"
 #include "w4a16_launch.h"
@@ -529,8 +531,12 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // 128 x 256 tiles that fit one per CU: cfg 14 (the cfg 11 kernel with two
   // k-slices per workgroup, one workgroup per CU), split along K for about a
   // workgroup per CU with at least 4 steps per slice, instead of cfg 11 split
-  // for two per CU (whose fp32 partials and reduction cost more).  G % 64 == 0:
-  // with a scale / zero load per half-step the kernel spills and loses.
+  // for two per CU (whose fp32 partials and reduction cost more).  Any G:
+  // with G % 64 != 0 (a scale / zero load per half-step) the kernel spills a
+  // few registers but still wins on most shapes (planner audit, G = 32, µs:
+  // M = 512, K = 4096, N = 12288 68.6 -> 63.5; N = 28672, M = 256 73.2 ->
+  // 64.8; C5 M = 256, K = 8192, N = 28672 134.9 -> 123.5; M = 512, K = 5120,
+  // N = 15360 90.4 -> 80.6), except with 80..128 tiles (below).
   // Measured on MI355X against the plans before it (µs): C4 M = 512 81.2 ->
   // 67.5; M = 384, K = 4096, N = 14336 67.0 -> 60.0; C5 M = 256, K = 8192,
   // N = 28672 137.5 -> 126.3 (G = 64: 135.0 -> 127.6); C5 M = 256, K = 28672,
@@ -549,7 +555,7 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // M = 128, K = 4096, N = 22016).
   const int64_t s14 = t6 > 0 ? (cus / t6 < K / 512 ? cus / t6 : K / 512) : 1;
   const bool fills = s14 > 1 || t6 * 10 >= 7 * (int64_t)cus || K <= 4096;
-  if (c11 && G % 64 == 0 && t6 <= cus && fills) {
+  if (c11 && t6 <= cus && fills) {
     int64_t s = s14;
     if (s < 1) s = 1;
     // 64 < M <= 256 on small layers: the 64-row streamed tiles (cfg 13, one
@@ -612,9 +618,17 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
         const int64_t w3 = 3 * (int64_t)cus;
         return {11, stream_splits((int)K, t6 * 8 <= w3 ? 8 : t6 * 4 <= w3 ? 4 : 2)};
       }
-      if (K >= 24576 && t6 > 64)
+      if (K >= 24576 && (t6 > 64 || (G % 64 != 0 && t6 >= 60)))
         return {11, stream_splits((int)K, stream_split_two(t6, K, cus))};
     }
+    // G % 64 != 0 (a scale / zero load per half-step, where the two-slice
+    // kernel spills a few registers) with 80..128 tiles past K = 4096: cfg 11
+    // split for about two workgroups per CU (measured on MI355X, G = 32, µs:
+    // M = 512, K = N = 5120 (80 tiles) 46.3 -> 43.8; M = 1024, K = 14336,
+    // N = 4096 (128 tiles) 123.8 -> 118.5; K = 13824, N = 5120, M = 512 82.9
+    // -> 81.3)
+    if (G % 64 != 0 && t6 >= 80 && t6 <= 128 && K > 4096)
+      return {11, stream_splits((int)K, stream_split_two(t6, K, cus))};
     return {14, s > 1 ? stream_splits((int)K, (int)s, 2) : 1};
   }
   // M >= 1024 with more tiles than CUs but fewer than two per CU: split K
@@ -648,44 +662,89 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   return {1, 1};
 }
 
-// Measured decode plans (M <= 2, G % 128 == 0, 256 CUs): per (M, K, N) of a
-// grid the fastest GEMV or skinny plan, timed on MI355X with cold weights by
-// bench.py --decode-scan and written into decode_table.inc by bench.py
-// --decode-table.  A shape inside the grid's K and N range takes the plan of
-// the nearest grid point in (log2 K, log2 N).  The rules below cover
-// everything else (other M, smaller groups, other CU counts, shapes outside
-// the grid).  Measured against those rules on the same grid: 71 of 168 shapes
+// Measured decode plans (M <= 2, 256 CUs): per group-size class (G % 128 ==
+// 0, G % 64 == 0, other G % 32 == 0) and (M, K, N) of a grid, the fastest
+// GEMV or skinny plan, timed on MI355X with cold weights by bench.py
+// --decode-scan (--audit-g for the class) and written into decode_table.inc
+// by bench.py --decode-table.  A shape inside its class's grid takes the plan
+// of the nearest grid point in (log2 K, log2 N).  The rules below cover
+// everything else (other M, other CU counts, shapes outside the grid).
+// Measured against those rules on the same grid: 71 of 168 G = 128 shapes
 // had been more than 3 % slower than the grid's best (up to 61 %: M = 2,
 // K = 28672, N = 14336, 66.0 against 41.1 us on 64-column MFMA-dot blocks).
 struct DecodeEntry {
-  int M, K, N, kernel, cfg, cols, rows, split, us100, rule_us100;
+  int G, M, K, N, kernel, cfg, cols, rows, split, us100, rule_us100;
 };
 const DecodeEntry kDecodeTable[] = {
 #include "decode_table.inc"
-    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+
+int decode_gclass(int64_t G) { return G % 128 == 0 ? 128 : G % 64 == 0 ? 64 : 32; }
+
+// One (group class, M) slice of the table as a grid: its distinct K and N
+// (ascending, with their log2) and the entry at each grid point.  Built once;
+// a lookup is then two short nearest-value scans instead of a log2 per entry.
+struct DecodeGrid {
+  int gclass = 0, M = 0;
+  std::vector<int64_t> ks, ns;
+  std::vector<double> lk, ln;
+  std::vector<const DecodeEntry*> at;   // [ik * ns.size() + in]
+};
+
+const std::vector<DecodeGrid>& decode_grids() {
+  static const std::vector<DecodeGrid> grids = [] {
+    std::vector<DecodeGrid> out;
+    for (int gc : {128, 64, 32})
+      for (int m : {1, 2}) {
+        DecodeGrid g;
+        g.gclass = gc;
+        g.M = m;
+        for (const DecodeEntry* e = kDecodeTable; e->M; ++e)
+          if (e->G == gc && e->M == m) {
+            g.ks.push_back(e->K);
+            g.ns.push_back(e->N);
+          }
+        if (g.ks.empty()) continue;
+        for (auto* v : {&g.ks, &g.ns}) {
+          std::sort(v->begin(), v->end());
+          v->erase(std::unique(v->begin(), v->end()), v->end());
+        }
+        for (int64_t k : g.ks) g.lk.push_back(std::log2((double)k));
+        for (int64_t n : g.ns) g.ln.push_back(std::log2((double)n));
+        g.at.assign(g.ks.size() * g.ns.size(), nullptr);
+        for (const DecodeEntry* e = kDecodeTable; e->M; ++e) {
+          if (e->G != gc || e->M != m) continue;
+          const size_t ik = std::lower_bound(g.ks.begin(), g.ks.end(), (int64_t)e->K) - g.ks.begin();
+          const size_t in = std::lower_bound(g.ns.begin(), g.ns.end(), (int64_t)e->N) - g.ns.begin();
+          g.at[ik * g.ns.size() + in] = e;
+        }
+        out.push_back(std::move(g));
+      }
+    return out;
+  }();
+  return grids;
+}
+
+// Index of the value nearest to x (first of equals), by |log2 distance|.
+size_t nearest_log(const std::vector<double>& lv, double x) {
+  size_t best = 0;
+  for (size_t i = 1; i < lv.size(); ++i)
+    if (std::fabs(lv[i] - x) < std::fabs(lv[best] - x)) best = i;
+  return best;
+}
 
 const DecodeEntry* decode_table_entry(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  if (M < 1 || M > 2 || G % 128 != 0 || cus != 256) return nullptr;
-  int64_t kmin = INT64_MAX, kmax = 0, nmin = INT64_MAX, nmax = 0;
-  for (const DecodeEntry* e = kDecodeTable; e->M; ++e) {
-    kmin = e->K < kmin ? e->K : kmin;
-    kmax = e->K > kmax ? e->K : kmax;
-    nmin = e->N < nmin ? e->N : nmin;
-    nmax = e->N > nmax ? e->N : nmax;
+  if (M < 1 || M > 2 || G % 32 != 0 || cus != 256) return nullptr;
+  const int gc = decode_gclass(G);
+  for (const DecodeGrid& g : decode_grids()) {
+    if (g.gclass != gc || g.M != M) continue;
+    if (K < g.ks.front() || K > g.ks.back() || N < g.ns.front() || N > g.ns.back())
+      return nullptr;
+    const size_t ik = nearest_log(g.lk, std::log2((double)K));
+    const size_t in = nearest_log(g.ln, std::log2((double)N));
+    return g.at[ik * g.ns.size() + in];
   }
-  if (K < kmin || K > kmax || N < nmin || N > nmax) return nullptr;
-  const DecodeEntry* best = nullptr;
-  double bd = 1e30;
-  for (const DecodeEntry* e = kDecodeTable; e->M; ++e) {
-    if (e->M != M) continue;
-    const double dk = std::log2((double)K / e->K), dn = std::log2((double)N / e->N);
-    const double d = dk * dk + dn * dn;
-    if (d < bd) {
-      bd = d;
-      best = e;
-    }
-  }
-  return best;
+  return nullptr;
 }
 
 size_t mfma_workspace_bytes(int64_t M, int64_t N, int64_t K, int split) {
