@@ -382,25 +382,35 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
         assert p.tile_m == (16 if rg else 8 if rg8 else g * 16), (M, N)
 
 
+def _rules(M, N, K, G):
+    """The GEMV rules' plan for a decode shape (the measured table decides the
+    automatic plan inside its grid; a forced GEMV plan takes the rules)."""
+    from w4a16 import _lib
+
+    return _lib.plan(M, N, K, G, _lib.KERNEL_GEMV, 0)
+
+
 def test_planner_decode_64_column_band():
     """M <= 2 where 32-column blocks would outnumber the CUs (256 without a
     device) but 64-column ones would not (8192 < N < 16384), K > 2048:
     64-column blocks, unsplit -- the skinny kernel's for K <= 4096 with
     G % 128 == 0, else the GEMV with staged activations and MFMA dot products
-    (cfg 7); K = 2048 takes the skinny kernel's 64-column blocks."""
+    (cfg 7); K = 2048 takes the skinny kernel's 64-column blocks.  (Inside the
+    measured table's grid the table decides; the GEMV rules are checked
+    through forced GEMV plans there.)"""
     from w4a16 import _lib
 
     for M, N, K, G, kern, cfg in ((1, 11008, 4096, 128, "skinny", 3), (2, 14336, 4096, 128, "skinny", 3),
                                   (1, 11008, 4096, 32, "gemv", 7), (1, 10240, 8192, 64, "gemv", 7),
                                   (2, 11008, 8192, 64, "gemv", 7)):
-        p = _lib.plan(M, N, K, G)
+        p = _lib.plan(M, N, K, G) if kern == "skinny" else _rules(M, N, K, G)
         assert (_lib.KERNEL_NAMES[p.kernel], p.tile_cfg, p.tile_n, p.split_k) == (kern, cfg, 64, 1), (M, N, K, G)
     p = _lib.plan(1, 11008, 2048, 64)          # K <= 2048: the skinny kernel's blocks
     assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n) == ("skinny", 64)
     # at the band's edges: N = 8192 (256 32-column blocks) and N = 16384 (256
     # 64-column blocks) keep their plans
-    assert _lib.plan(1, 8192, 8192, 64).tile_n == 32
-    assert (_lib.plan(1, 16384, 4096, 64).tile_n, _lib.plan(1, 16384, 4096, 64).tile_cfg) == (64, 7)
+    assert _rules(1, 8192, 8192, 64).tile_n == 32
+    assert (_rules(1, 16384, 4096, 64).tile_n, _rules(1, 16384, 4096, 64).tile_cfg) == (64, 7)
 
 
 def test_planner_gemv_split_rule():
@@ -418,7 +428,7 @@ def test_planner_gemv_split_rule():
         assert p.tile_n in (16, 32, 64, 128, 256)
         assert p.tile_cfg in (1, 2, 4, 5, 7)
         assert lib.w4a16_gemm_workspace_bytes(1, N, 4096, 128) == 0
-    assert _lib.plan(1, 28672, 4096, 64).tile_n == 128
+    assert _rules(1, 28672, 4096, 64).tile_n == 128
     for M, N, K in ((1, 1024, 14336), (2, 512, 8192), (2, 1024, 28672)):
         p = _lib.plan(M, N, K, 128)
         assert _lib.KERNEL_NAMES[p.kernel] == "gemv" and p.split_k == 4
@@ -433,10 +443,10 @@ def test_planner_gemv_split_rule():
         assert p.workspace_bytes == split * M * N * 4
         assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
     for M, N, K in ((1, 4096, 14336), (1, 8192, 8192), (1, 1024, 28672), (3, 8192, 28672)):
-        p = _lib.plan(M, N, K, 64)                   # shorter rows, too few blocks, M > 2
+        p = _rules(M, N, K, 64)                      # shorter rows, too few blocks, M > 2
         assert p.tile_cfg != 7 or p.split_k == 1, (M, N, K)
-    assert _lib.plan(1, 28672, 14336, 64).split_k == 1   # enough column blocks
-    assert _lib.plan(1, 4096, 14336, 64).split_k == 1    # one block per CU
+    assert _rules(1, 28672, 14336, 64).split_k == 1      # enough column blocks
+    assert _rules(1, 4096, 14336, 64).split_k == 1       # one block per CU
     for split in (2, 3, 7, 600):
         p = _lib.plan(2, 1024, 4096, 128, _lib.KERNEL_GEMV, split)
         rows = -(-512 // p.split_k)
@@ -459,9 +469,9 @@ def test_planner_gemv_blocks_and_waves():
     4), one chunk, no split."""
     from w4a16 import _lib
 
-    p = _lib.plan(1, 4096, 4096, 64)            # C2: 256 blocks of 16 (256 CUs), 8 waves
+    p = _rules(1, 4096, 4096, 64)            # C2: 256 blocks of 16 (256 CUs), 8 waves
     assert (p.tile_n, p.tile_cfg) == (16, 1)
-    p = _lib.plan(2, 4096, 4096, 64)            # ... 16 at M = 2
+    p = _rules(2, 4096, 4096, 64)            # ... 16 at M = 2
     assert (p.tile_n, p.tile_cfg) == (16, 2)
     p = _lib.plan(1, 4096, 2048, 128, _lib.KERNEL_GEMV, 0)   # ... and at K = 2048
     assert (p.tile_n, p.tile_cfg) == (16, 2)
@@ -470,43 +480,43 @@ def test_planner_gemv_blocks_and_waves():
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(2, 6144, 4096, 128, _lib.KERNEL_GEMV, 0)
     assert (p.tile_n, p.tile_cfg) == (32, 2)
-    p = _lib.plan(1, 6144, 14336, 64)            # ... at any K, unsplit, 16 waves
+    p = _rules(1, 6144, 14336, 64)            # ... at any K, unsplit, 16 waves
     assert (_lib.KERNEL_NAMES[p.kernel], p.tile_n, p.tile_cfg, p.split_k) == ("gemv", 32, 2, 1)
-    p = _lib.plan(1, 6144, 28672, 64)            # ... even past the long-row split's K
+    p = _rules(1, 6144, 28672, 64)            # ... even past the long-row split's K
     assert (p.tile_n, p.tile_cfg, p.split_k) == (32, 2, 1)
-    p = _lib.plan(1, 8192, 28672, 64)           # not at N = 8192 (256 blocks of 32)
+    p = _rules(1, 8192, 28672, 64)           # not at N = 8192 (256 blocks of 32)
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
     # 128-column blocks, unsplit, where 64-column ones would take more than one
     # round (N > 16384) and 128-column ones not; N = 16384 keeps one round of 64
     for N, K in ((16896, 4096), (20480, 8192), (20480, 28672), (32768, 4096)):
-        p = _lib.plan(1, N, K, 64)
+        p = _rules(1, N, K, 64)
         assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1), (N, K)
-    assert _lib.plan(1, 16384, 4096, 64).tile_n == 64
-    p = _lib.plan(2, 4096, 10240, 64)           # long rows at M = 2: 8 waves
+    assert _rules(1, 16384, 4096, 64).tile_n == 64
+    p = _rules(2, 4096, 10240, 64)           # long rows at M = 2: 8 waves
     assert p.tile_cfg == 1
-    p = _lib.plan(2, 4096, 14336, 64)           # ... longer: MFMA dots, split K
+    p = _rules(2, 4096, 14336, 64)           # ... longer: MFMA dots, split K
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 4)
-    p = _lib.plan(1, 4096, 14336, 64)           # ... 16 at M = 1, direct
+    p = _rules(1, 4096, 14336, 64)           # ... 16 at M = 1, direct
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 16384, 4096, 64)           # 64-column blocks: 8 waves, staged, MFMA dots
+    p = _rules(1, 16384, 4096, 64)           # 64-column blocks: 8 waves, staged, MFMA dots
     assert (p.tile_n, p.tile_cfg) == (64, 7)
-    p = _lib.plan(1, 28672, 4096, 64)           # 224 blocks of 128: 8 waves, MFMA dots
+    p = _rules(1, 28672, 4096, 64)           # 224 blocks of 128: 8 waves, MFMA dots
     assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
-    p = _lib.plan(2, 28672, 8192, 64)
+    p = _rules(2, 28672, 8192, 64)
     assert (p.tile_n, p.tile_cfg, p.split_k) == (128, 7, 1)
-    p = _lib.plan(1, 65536, 4096, 64)           # 256-column blocks: dot2, staged
+    p = _rules(1, 65536, 4096, 64)           # 256-column blocks: dot2, staged
     assert (p.tile_n, p.tile_cfg) == (256, 4)
     p = _lib.plan(3, 28672, 8192, 128, _lib.KERNEL_GEMV, 0)   # M > 2 keeps 64-column blocks
     assert (p.tile_n, p.tile_cfg) == (64, 1)
-    p = _lib.plan(1, 4096, 8192, 64)            # shorter rows: direct reads
+    p = _rules(1, 4096, 8192, 64)            # shorter rows: direct reads
     assert p.tile_cfg == 2
-    p = _lib.plan(1, 8192, 28672, 64)           # C5 down-proj: MFMA dots, split 2
+    p = _rules(1, 8192, 28672, 64)           # C5 down-proj: MFMA dots, split 2
     assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, 2)
     p = _lib.plan(1, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # unsplit: 16 waves, direct
     assert (p.tile_n, p.tile_cfg) == (32, 2)
     p = _lib.plan(2, 8192, 28672, 128, _lib.KERNEL_GEMV, 1)   # ... 8 waves at M = 2
     assert (p.tile_n, p.tile_cfg) == (32, 1)
-    p = _lib.plan(2, 1024, 8192, 64)            # split 4: 2048 rows per split
+    p = _rules(2, 1024, 8192, 64)            # split 4: 2048 rows per split
     assert p.split_k == 4 and p.tile_cfg == 2
 
 

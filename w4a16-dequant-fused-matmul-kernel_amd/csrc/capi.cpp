@@ -340,8 +340,14 @@ bool skinny_wide(int64_t M, int64_t N, int cus) {
 // gain nothing (M = 17, K = 14336, N = 8192: 26.1 vs 25.7) or lose (16-row
 // groups on the same blocks already do: M = 32, N = 6144, K = 14336: 39.0 vs
 // 25.6; N = 8192, K = 28672: 75.4 vs 44.0).
+// Smaller groups at M <= 16 up to K = 8192 and N = 8192 as well (planner
+// audit, µs: M = 16, K = N = 8192: G = 64 19.2 -> 16.6, G = 32 19.9 ->
+// 18.5; not N = 10240, where the whole-row 32-column blocks lose to 16-row
+// groups on 64-column blocks and to the streamed tiles: G = 32, M = 16
+// 31.0 against 23.5).
 bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  return skinny_wide(M, N, cus) && G % 128 == 0 && (M <= 16 || K <= 8192) &&
+  return skinny_wide(M, N, cus) && (G % 128 == 0 || (K <= 8192 && M <= 16 && N <= 8192)) &&
+         (M <= 16 || K <= 8192) &&
          (N <= 8192 || (N <= 16384 && M <= 16));
 }
 
@@ -364,9 +370,14 @@ bool skinny_wide_beats_stream(int64_t M, int64_t N, int64_t K, int64_t G, int cu
 // Beyond two blocks per CU at M > 8 the streamed 32-row tiles win (M = 16,
 // K = 8192, N = 57344, 896 blocks: 69.6 vs 65.7 split 2; 448 blocks,
 // N = 28672, K = 4096 / 5120: 20.1 / 25.2, the best plan).
+// Smaller groups also up to K = 6144 where the blocks take one round
+// (planner audit, G = 32, µs: M = 4 / 8 / 16, K = 5120, N = 15360: 20.6 /
+// 21.2 / 23.3 on the streamed tiles -> 17.8 / 18.1 / 18.3; not N = 27648:
+// 28.1 / 29.1 / 32.3 against 26.1 / 26.4 / 27.3 streamed).
 bool skinny_quad(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
-  return M <= 16 && N % 4 == 0 && (G % 64 == 0 || K <= 4096) && (N + 63) / 64 > cus / 2 &&
-         (M <= 8 || (N + 63) / 64 <= 2 * (int64_t)cus);
+  const int64_t b64 = (N + 63) / 64;
+  return M <= 16 && N % 4 == 0 && (G % 64 == 0 || K <= 4096 || (K <= 6144 && b64 <= cus)) &&
+         b64 > cus / 2 && (M <= 8 || b64 <= 2 * (int64_t)cus);
 }
 
 // Skinny blocks with one 16-row group per workgroup (plan tile_m = 16) for
