@@ -20,7 +20,8 @@ time per call.  Timing of the K steps:
   host's launch cost (~12 us per Python call) nor a graph launch.  HIP events
   on that stream bracket exactly the K calls; ``ms_per_step`` = event time / K;
 * ``secondary``: TFLOP/s of the prefill MFMA GEMM at C4 M=4096 (2MNK flops),
-  its calls timed as one HIP-graph replay (SECONDARY_GRAPH says why);
+  its calls timed as one HIP-graph replay (SECONDARY_GRAPH says why) after
+  enough untimed calls for the clock to settle under this load;
 * ``cpu_baseline``: the CPU oracle's dequantise-then-matmul path
   (``oracle/w4a16_oracle.reference_w4a16``, a numpy port of the reference's
   reference.py:18-40) on the same C2 inputs, on every host core the process may
@@ -976,21 +977,23 @@ def main() -> int:
     }
     if not args.no_secondary:
         c4 = [c for c in wl.CONFIGS["C4"] if c.M == 4096][0]
-        # steady state: 10 untimed calls (the clock settles under the MFMA
-        # load after the light decode phase), then 50 timed calls (~20 ms)
-        sec = bench_case(c4, max(50, args.steps // 4), max(10, args.warmup // 2),
-                         graph=SECONDARY_GRAPH, cold=False)
+        # steady state: after the light decode phase the chip's clock takes
+        # ~100 calls of this load to settle under its power limit (25-call
+        # chunks measured on MI355X: 493, 444, 426, 418, 416, then 411-417
+        # µs per call), so 150 untimed calls (~60 ms), then 100 timed calls
+        sec_steps, sec_warm = max(100, args.steps // 2), max(150, args.warmup // 2)
+        sec = bench_case(c4, sec_steps, sec_warm, graph=SECONDARY_GRAPH, cold=False)
         line["secondary"] = {
             "metric": "TFLOP/s, C4 prefill M=4096 K=4096 N=14336 G=128",
             "value": round(sec["TFLOP/s"], 2), "unit": "TFLOP/s", "us": round(sec["us"], 2),
             "kernel": sec["kernel"], "tile_cfg": sec["tile_cfg"], "tile": sec["tile"],
-            "timing": f"{sec['steps']} calls in one HIP graph replay, HIP events",
+            "timing": f"{sec['steps']} calls in one HIP graph replay after {sec_warm} untimed "
+                      "calls, HIP events",
             "roofline": {"bound": "mfma", "achieved": round(sec["TFLOP/s"], 2),
                          "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(sec["TFLOP/s"] / FP16_PEAK_TFLOPS, 4),
                          "traffic": _traffic_for("C4_M4096")},
-            "dense_fp16": dense_fp16_case(c4, max(50, args.steps // 4),
-                                          max(10, args.warmup // 2)),
+            "dense_fp16": dense_fp16_case(c4, sec_steps, sec_warm),
         }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(c2)
