@@ -101,10 +101,14 @@ def _args():
     ap.add_argument("--decode-scan", metavar="OUT_JSON",
                     help="time every GEMV and skinny plan for M = 1, 2 (G = --audit-g) over "
                          "the DECODE_KS x DECODE_NS grid, cold weights; JSON for --decode-table")
+    ap.add_argument("--decode-ks", default=None,
+                    help="with --decode-scan: comma list of K (default: DECODE_KS)")
+    ap.add_argument("--decode-ns", default=None,
+                    help="with --decode-scan: comma list of N (default: DECODE_NS)")
     ap.add_argument("--decode-table", metavar="SCAN_JSON", nargs="+",
                     help="write csrc/decode_table.inc (the planner's measured M <= 2 table) "
                          "from --decode-scan files (group-size classes they do not cover keep "
-                         "their current entries)")
+                         "their current entries; a later file's shapes replace an earlier's)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="markdown table of a rocprofv3 --kernel-trace CSV of bench.py: per "
                          "kernel, the durations of its last --steps dispatches (the timed "
@@ -474,7 +478,8 @@ def decode_table(scan_paths) -> str:
     group-size class (128: G % 128 == 0, 64: G % 64 == 0, 32: other G % 32 == 0)
     and measured (M, K, N) the fastest plan (family, configuration, column
     block or row group, k-split).  Classes the files do not cover keep the
-    entries the current table holds for them."""
+    entries the current table holds for them; where files measure the same
+    shape, the later file's measurement is taken."""
     def gclass(G: int) -> int:
         return 128 if G % 128 == 0 else 64 if G % 64 == 0 else 32
 
@@ -496,15 +501,17 @@ def decode_table(scan_paths) -> str:
              "// 4 skinny), tile_cfg, tile_n, tile_m (skinny rows), split_k, µs x 100 of",
              "// the fastest, of the plan the planner gave when scanned.",
              "// clang-format off"]
-    new = []
+    latest = {}
     for r in rows:
+        latest[(gclass(r.get("G", 128)), r["M"], r["K"], r["N"])] = r
+    new = []
+    for key, r in latest.items():
         us = r["us"]
         best = min(us, key=us.get)
         p = r["plans"][best]
-        new.append(((gclass(r.get("G", 128)), r["M"], r["K"], r["N"]),
-                    f"{{{gclass(r.get('G', 128))}, {r['M']}, {r['K']}, {r['N']}, {p['kernel']}, "
-                    f"{p['tile_cfg']}, {p['tile_n']}, {p['tile_m']}, {p['split_k']}, "
-                    f"{round(100 * us[best])}, {round(100 * us['static'])}}},"))
+        new.append((key, f"{{{key[0]}, {r['M']}, {r['K']}, {r['N']}, {p['kernel']}, "
+                         f"{p['tile_cfg']}, {p['tile_n']}, {p['tile_m']}, {p['split_k']}, "
+                         f"{round(100 * us[best])}, {round(100 * us['static'])}}},"))
     for ln in kept:
         f = [int(v) for v in ln.strip("{},").split(",")[:4]]
         new.append((tuple(f), ln))
@@ -929,7 +936,9 @@ def main() -> int:
         print(json.dumps(empty_kernels(args.steps, args.warmup)), flush=True)
         return 0
     if args.decode_scan:
-        decode_scan(args.decode_scan, G=args.audit_g)
+        ints = lambda v: [int(t) for t in v.split(",")] if v else None
+        decode_scan(args.decode_scan, ks=ints(args.decode_ks), ns=ints(args.decode_ns),
+                    G=args.audit_g)
         return 0
     if args.planner_audit:
         shapes = AUDIT_SHAPES

@@ -435,10 +435,11 @@ def test_planner_gemv_split_rule():
         assert p.workspace_bytes == 4 * M * N * 4
         assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes
     # long rows on 32 .. 223 64-column blocks: MFMA dot products, K split to
-    # reach 7/8 of the CUs (power of two, at most 8)
+    # reach 7/8 of the CUs (power of two, at most 8) -- the rules (inside the
+    # measured table's grid the table may pick another measured plan)
     for M, N, K, split in ((1, 8192, 28672, 2), (1, 4096, 28672, 4), (1, 2048, 28672, 8),
                            (2, 2048, 28672, 8), (2, 4096, 14336, 4), (2, 8192, 28672, 2)):
-        p = _lib.plan(M, N, K, 128)
+        p = _rules(M, N, K, 128)
         assert (p.tile_n, p.tile_cfg, p.split_k) == (64, 7, split), (M, N, K)
         assert p.workspace_bytes == split * M * N * 4
         assert lib.w4a16_gemm_workspace_bytes(M, N, K, 128) == p.workspace_bytes

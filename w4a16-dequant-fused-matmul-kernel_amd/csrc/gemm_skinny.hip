@@ -21,13 +21,15 @@
 //   * in v_mfma_f32_16x16x32_f16 lane l holds B[k = 8*(l/16)..+7][n = l%16]: one
 //     packed int32 word.  A wave therefore covers 16 columns x 32 k per MFMA
 //     and n-tile, reading 4 packed rows of its block per load;
-//   * the waves split K into contiguous runs of whole batches of 8 k-steps
-//     (256 k).  Up to K = 4096 there are enough waves (K / 256, at least 4)
-//     for one batch each, and each wave issues all its loads before its first
-//     product; longer K has 4 waves walk their runs with two register batches
-//     used ping-pong, all loads of batch i+1 -- weights, scales, zeros and
-//     activations -- issued before batch i is consumed, unconditionally (past
-//     the range they read zeros), so the compiler's wait counts are exact;
+//   * the waves split K into whole batches of 8 k-steps (256 k).  Up to
+//     K = 4096 there are enough waves (K / 256, at least 4) for one batch
+//     each, and each wave issues all its loads before its first product;
+//     longer K deals the batches to 4 waves in sweeps (batch i of every wave
+//     together is one contiguous run of K), each wave with two register
+//     batches used ping-pong, all loads of batch i+1 -- weights, scales, zeros
+//     and activations -- issued before batch i is consumed, unconditionally
+//     (past the range they read zeros), so the compiler's wait counts are
+//     exact;
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
 //     the buffer range check;
@@ -107,11 +109,19 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(SC, (uint32_t)NG * (uint32_t)N * 2u);
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZR, (uint32_t)NG * (uint32_t)N * 2u);
 
-  // this wave's k-steps [kb, ke): whole 8-step batches, so batch starts are
-  // multiples of 8 k-steps (256 k) and group boundaries fall on fixed slots
+  // This wave's k-steps, in whole 8-step batches.  One batch per wave: a contiguous run of `per` steps.  The two-batch loop
+  // deals the batches to the waves in sweeps instead: batch i of wave w is
+  // steps (i W + w) 8 .. + 8, so batch i of every wave together is one
+  // contiguous run of K, read by the workgroup at once (measured on MI355X
+  // against a contiguous run per wave, cold weights, same run, µs: K = 14336,
+  // N = 4096, M = 16 17.4 -> 17.2, 64-column blocks 26.2 -> 25.3; K = 8192,
+  // N = 8192, M = 16, G = 32 18.7 -> 17.4; K = 13824, N = 5120, M = 8 17.2 ->
+  // 16.8; planned plans -6.5 .. +0.4 %).  Either way batch starts are
+  // multiples of 8 k-steps (256 k), so group boundaries fall on fixed slots.
   const int per = ((KS + kWaves - 1) / kWaves + kBatch - 1) / kBatch * kBatch;
-  const int kb = min(KS, wave * per);
-  const int ke = min(KS, kb + per);
+  const int kb = ONE_BATCH ? min(KS, wave * per) : wave * kBatch;
+  const int ke = ONE_BATCH ? min(KS, kb + per) : KS;
+  const int bstep = ONE_BATCH ? kBatch : kWaves * kBatch;   // steps between a wave's batches
 
   // per-lane offsets at k = 0
   const uint32_t w_off = nv ? ((uint32_t)q * (uint32_t)N + (uint32_t)col) * 4u : kOobOffset;
@@ -256,11 +266,11 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   } else {
     Batch bt[2];
     load_batch(kb, bt[0]);
-    for (int s0 = kb; s0 < ke; s0 += 2 * kBatch) {
-      load_batch(s0 + kBatch, bt[1]);
+    for (int s0 = kb; s0 < ke; s0 += 2 * bstep) {
+      load_batch(s0 + bstep, bt[1]);
       process(bt[0], s0);
-      load_batch(s0 + 2 * kBatch, bt[0]);
-      if (s0 + kBatch < ke) process(bt[1], s0 + kBatch);
+      load_batch(s0 + 2 * bstep, bt[0]);
+      if (s0 + bstep < ke) process(bt[1], s0 + bstep);
     }
   }
 
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 
 // Waves per workgroup: as many as give each wave exactly one batch (K <= 1024:
 // 4, K <= 2048: 8, K <= 4096: 16), so every load is issued before the first
-// product, in one round trip to memory; longer K walks 4 waves' runs in the
+// product, in one round trip to memory; longer K runs 4 waves in the
 // two-batch loop (16 waves' loop registers spill; 8 or 16 waves in the loop
 // measured no faster at K = 8192..28672).  Measured on MI355X, cold weights,
 // against 4 waves in the loop: K = N = 4096 M = 4 / 8 / 16: 6.40 / 6.78 /

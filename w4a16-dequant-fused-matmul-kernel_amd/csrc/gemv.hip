@@ -34,11 +34,13 @@
 // KiB and stays in L2, and no barrier stands before the first dot product):
 // the rows are dealt to the row-lanes in sweeps, so each batch is one
 // contiguous run of rows and a lane's first rows are the first to arrive.
-// gemv_kernel (M > 2, or M <= 2 with X staged in LDS): each row-lane owns a
-// contiguous run of packed rows, cut into batches of BR rows (4 with 8 waves,
-// 2 with 16) aligned to absolute multiples of BR, so a 4-row half (32 k, G %
-// 32 == 0) lies in one group and a batch needs one scale / zero load per
-// half; every load of batch i+1 is issued before batch i is consumed; X is
+// gemv_kernel (M > 2, or M <= 2 with X staged in LDS): a row-lane's rows come
+// in batches of BR rows (4 with 8 waves, 2 with 16) aligned to absolute
+// multiples of BR, so a 4-row half (32 k, G % 32 == 0) lies in one group and a
+// batch needs one scale / zero load per half; for M <= 2 the batches are dealt
+// to the row-lanes in sweeps (batch i of every row-lane together is one
+// contiguous run of rows), for M > 2 each row-lane owns a contiguous run of
+// batches; every load of batch i+1 is issued before batch i is consumed; X is
 // staged once per chunk in LDS, permuted to the dequantiser's pair order.
 #include "w4a16_device.h"
 #include "w4a16_launch.h"
@@ -198,16 +200,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
   constexpr int HW = 4 * CWL;              // columns between a lane's quads
   constexpr int CHUNK = kXsEntries / MT / BR * BR;   // packed rows of X per stage
   static_assert(CHUNK % BR == 0, "chunk must hold whole batches");
-  // M <= 2 on 64-column and wider blocks: every row of a lane's run is
-  // processed without a range check.  The run's end `le` is a multiple of the
-  // batch (K % 32 == 0, splits and chunks in whole batches), so a batch is
-  // wholly inside or wholly past it, and a batch past it loads zero words,
-  // scales and zeros (out-of-range offsets): its weights dequantise to exactly
-  // 0, and its rows read BR zero rows of X (so 0 * x never meets an inf or
-  // NaN of another row; a run of an odd number of batches above one also
-  // processes the batch after its end, whose rows belong to the next
-  // row-lane).  The batch's first row picks its LDS rows, so each row's read
-  // keeps the row offset in the instruction's immediate.  The per-row branch had put every
+  // M <= 2 on 64-column and wider blocks: every row of a batch is processed
+  // without a range check.  The end of the lane's rows `le` (the chunk's end
+  // for M <= 2, below) is a multiple of the batch (K % 32 == 0, splits and
+  // chunks in whole batches), so a batch is wholly inside or wholly past it,
+  // and a batch past it loads zero words, scales and zeros (out-of-range
+  // offsets): its weights dequantise to exactly 0, and its rows read BR zero
+  // rows of X (so 0 * x never meets an inf or NaN of another row; an odd
+  // number of batches above one also processes the batch after the last,
+  // which lies past the chunk's end).  The batch's first row picks its LDS
+  // rows, so each row's read keeps the row offset in the instruction's
+  // immediate.  The per-row branch had put every
   // row's dequant under an exec mask and the next batch's loads between them:
   // measured on MI355X without it, M = 1, K = 8192, N = 28672 on 128-column
   // blocks 27.0 -> 25.6 us, K = 4096 16.0 -> 15.4, M = 2 30.2 -> 29.2, N = 16384
@@ -271,8 +274,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     uint2 s[H][QPL], z[H][QPL];
     uint4 w[BR][QPL];
   };
-  // Rows r0..r0+BR-1 of this lane's run [.., le).  Row u rides in the SGPR
-  // offset; weight rows at or past `le` (only in a run's last batch) read as zero.
+  // Rows r0..r0+BR-1 of this lane's rows, which end at `le`.  Row u rides in
+  // the SGPR offset; weight rows at or past `le` read as zero.
   auto load_batch = [&](int r0, int le, Batch& b) {
 #pragma unroll
     for (int h = 0; h < H; ++h) {
@@ -280,7 +283,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
       const int g = min(group_of((r0 + RH * h) * 8), NG - 1);
 #pragma unroll
       for (int q = 0; q < QPL; ++q) {
-        // a batch past the lane's run (issued only to keep the loads the same
+        // a batch past the lane's rows (issued only to keep the loads the same
         // on every path) reads nothing from memory
         const bool v = n + HW * q < N && r0 < le;
         const uint32_t so =
@@ -371,9 +374,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     const int c1 = min(re, c0 + CHUNK);
     const int nr = c1 - c0;
     // this row-lane's rows in the chunk: BR-row aligned run
+    // M <= 2: batch i of row-lane rl holds rows c0 + (i RL + rl) BR .. + BR,
+    // so each batch index is one contiguous run of RL * BR rows read by the
+    // whole workgroup at once, and the rows of the chunk arrive in the order
+    // the lanes consume them.  Measured on MI355X against contiguous runs of
+    // rows per lane (cold weights, same run, µs): M = 1, K = 8192, N = 16384,
+    // 64-column MFMA-dot blocks 14.9 -> 14.1, 128-column 24.5 -> 22.4; M = 2,
+    // K = 8192, N = 28672, 128-column MFMA-dot 25.5 -> 24.3; M = 1, K = 4096,
+    // N = 16384, 64-column 9.3 -> 8.6; within +-1.5 % on the 128- / 256-column
+    // dot2 blocks.  M > 2 keeps a BR-aligned contiguous run per row-lane.
     const int per = ((nr + RL - 1) / RL + BR - 1) / BR * BR;
-    const int lb = min(c1, c0 + rl * per);
-    const int le = min(c1, lb + per);
+    constexpr bool kSweep = MT <= 2;
+    const int lb = kSweep ? c0 + rl * BR : min(c1, c0 + rl * per);
+    const int le = kSweep ? c1 : min(c1, lb + per);
+    const int bstep = kSweep ? RL * BR : BR;     // rows from one batch to the next
 
     Batch ba, bb;
     {
@@ -419,16 +433,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(
     // keeps the per-lane loop, which measured 6-7 % faster there (M = 3, 4,
     // K = 4096, N = 28672).
     if constexpr (MT <= 2) {
-      const int nbat = per / BR;
+      const int nbat = (nr + RL * BR - 1) / (RL * BR);
       if (nbat == 1) {
         process(ba, lb, le, c0);
       } else {
         for (int i = 0; i < nbat; i += 2) {
-          const int r0 = lb + i * BR;
-          load_batch(r0 + BR, le, bb);
+          const int r0 = lb + i * bstep;
+          load_batch(r0 + bstep, le, bb);
           process(ba, r0, le, c0);
-          load_batch(r0 + 2 * BR, le, ba);
-          process(bb, r0 + BR, le, c0);
+          load_batch(r0 + 2 * bstep, le, ba);
+          process(bb, r0 + bstep, le, c0);
         }
       }
     } else {
