@@ -240,6 +240,30 @@ def trace_summary(path: str, last: int, per_kernel: str | None = None) -> str:
     return "\n".join(lines)
 
 
+def _layer_copies(qw, sc, zr, n: int) -> list:
+    """`n` copies of one quantised layer (the first the tensors themselves where
+    their scales and zeros already lie close together), each copy's scales and
+    zeros the two halves of one allocation.  The streamed prefill kernels read
+    scales and zeros through one buffer resource and need them within 2 GiB
+    of each other (further apart the library runs its register-tiled kernel
+    instead); separate allocations in a process that has allocated and freed
+    many large tensors do not guarantee that, and a timing should measure the
+    planned kernel."""
+    import torch
+    from w4a16.hip_kernel import mark_integer_zeros
+
+    def packed(q):
+        sz = torch.empty((2,) + tuple(sc.shape), dtype=sc.dtype, device=sc.device)
+        sz[0].copy_(sc)
+        sz[1].copy_(zr)
+        mark_integer_zeros(sz[1])
+        return q, sz[0], sz[1]
+
+    near = abs(sc.data_ptr() - zr.data_ptr()) + sc.numel() * 2 < (1 << 30)
+    first = (qw, sc, zr) if near else packed(qw)
+    return [first] + [packed(qw.clone()) for _ in range(n - 1)]
+
+
 def _prepare(case, copies_for_cold: bool):
     import torch
     from w4a16 import quantize_weight
@@ -252,7 +276,7 @@ def _prepare(case, copies_for_cold: bool):
     ncopy = 1
     if copies_for_cold:
         ncopy = max(2, -(-COLD_BYTES // per_copy) + 1)
-    layers = [(qw, s, z)] + [(qw.clone(), s.clone(), z.clone()) for _ in range(ncopy - 1)]
+    layers = _layer_copies(qw, s, z, ncopy)
     y = torch.empty(case.M, case.N, dtype=torch.float16, device="cuda")
     return X, W, Xd, layers, y, ncopy, per_copy
 
@@ -334,7 +358,7 @@ AUDIT_SHAPES = [("7B qkv", 4096, 12288), ("7B o", 4096, 4096), ("7B gate+up", 40
                 ("13B gate+up", 5120, 27648), ("13B down", 13824, 5120),
                 ("70B qkv", 8192, 10240), ("70B o", 8192, 8192), ("70B gate+up", 8192, 57344),
                 ("70B down", 28672, 8192)]
-AUDIT_MS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024]
+AUDIT_MS = [1, 2, 4, 8, 16, 32, 64, 96, 128, 192, 256, 512, 1024]
 
 
 def planner_audit(shapes, ms, G: int = 128, steps: int = 30, reps: int = 3) -> str:
@@ -360,8 +384,7 @@ def planner_audit(shapes, ms, G: int = 128, steps: int = 30, reps: int = 3) -> s
             X = torch.randn(M, K, device="cuda", generator=g).to(torch.float16)
             cold = M < 64
             ncopy = max(2, -(-COLD_BYTES // per) + 1) if cold else 1
-            layers = [(qw, sc, zr)] + [(qw.clone(), sc.clone(), zr.clone())
-                                       for _ in range(ncopy - 1)]
+            layers = _layer_copies(qw, sc, zr, ncopy)
             y = torch.empty(M, N, dtype=torch.float16, device="cuda")
             cands = autotune.candidates(M, N, K, G)
             cands = [cands[0], ("static (again)", cands[0][1])] + cands[1:]
@@ -440,8 +463,7 @@ def decode_scan(out_path: str, ks=None, ns=None, ms=(1, 2), G: int = 128) -> Non
             del W
             per = qw.numel() * 4 + sc.numel() * 4
             ncopy = max(2, -(-COLD_BYTES // per) + 1)
-            layers = [(qw, sc, zr)] + [(qw.clone(), sc.clone(), zr.clone())
-                                       for _ in range(ncopy - 1)]
+            layers = _layer_copies(qw, sc, zr, ncopy)
             for M in ms:
                 X = torch.randn(M, K, device="cuda", generator=g).to(torch.float16)
                 y = torch.empty(M, N, dtype=torch.float16, device="cuda")

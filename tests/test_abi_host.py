@@ -779,9 +779,24 @@ def test_planner_prefill_split_k():
         assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
         assert p.grid_x == split * (N // 256) * 2
     # ... not with longer slices, more or fewer tiles, nor beyond M = 256
-    for M, N, K in ((128, 4096, 14336), (128, 8192, 8192), (384, 4096, 4096), (128, 27648, 5120),
-                    (128, 10240, 8192)):
+    for M, N, K in ((128, 8192, 8192), (384, 4096, 4096), (128, 27648, 5120), (128, 10240, 8192)):
         assert _lib.plan(M, N, K, 128).tile_cfg == 14, (M, N, K)
+    # 64-row tiles split for about two workgroups per CU (>= 10 k-steps each)
+    # where the last 128-row tile is at most half used (128 < M <= 192, at most
+    # 160 64-row tiles) and for few tiles of long rows (M <= 128, K >= 8192, at
+    # most 40 tiles); any G
+    for M, N, K, split in ((192, 5120, 5120, 7), (160, 10240, 8192, 4), (192, 4096, 11008, 9),
+                           (192, 6144, 4096, 6), (96, 4096, 11008, 15), (128, 4096, 14336, 14),
+                           (128, 5120, 13824, 11)):
+        for G in (128, 64, 32):
+            p = _lib.plan(M, N, K, G)
+            assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K, G)
+            assert p.grid_x == split * (N // 256) * ((M + 63) // 64)
+            assert p.workspace_bytes == split * M * N * 4
+    # ... not where the splits would hold fewer than 10 k-steps (K = N = 4096:
+    # the one-per-CU rule above), nor on more tiles
+    assert (_lib.plan(192, 4096, 4096, 128).tile_cfg, _lib.plan(192, 4096, 4096, 128).split_k) == (13, 4)
+    assert _lib.plan(192, 15360, 5120, 128).tile_cfg == 14      # 180 64-row tiles
     # more tiles than CUs: cfg 11
     p = _lib.plan(1024, 14336, 4096, 128)
     assert (p.tile_cfg, p.split_k) == (11, 1)

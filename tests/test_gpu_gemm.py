@@ -389,6 +389,20 @@ def test_streamed_prefill_far_apart_scales_zeros():
     dist = abs(z_far.data_ptr() - s_far.data_ptr())
     log(f"scales/zeros {dist / 2**30:.2f} GiB apart")
     assert dist >= (1 << 31)
+    # the wrapper says once per process that such calls leave the streamed kernels
+    import warnings
+
+    from w4a16 import hip_kernel as hk
+
+    hk._FAR_SZ_WARNED = False
+    with warnings.catch_warnings(record=True) as seen:
+        warnings.simplefilter("always")
+        w4a16_matmul_planned(X, qw, s, z, G, plan_for(M, N, K, G))
+        assert not seen, "adjacent scales / zeros must not warn"
+        w4a16_matmul_planned(X, qw, s_far, z_far, G, plan_for(M, N, K, G))
+        w4a16_matmul_planned(X, qw, s_far, z_far, G, plan_for(M, N, K, G))
+    far = [w for w in seen if issubclass(w.category, RuntimeWarning) and "2 GiB" in str(w.message)]
+    assert len(far) == 1, [str(w.message) for w in seen]
     for cfg, split in ((11, 1), (11, 3), (12, 2), (13, 4), (12, 8), (14, 1), (14, 2)):
         p = plan_for(M, N, K, G, "mfma", split)
         p.tile_cfg = cfg

@@ -536,6 +536,36 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
     const int s = stream_split_two(tiles, K, cus);
     return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
+  // 64-row tiles (cfg 13, one k-slice) split for about two workgroups per CU,
+  // ahead of the 128-row tilings, where those waste rows or have few tiles:
+  //   * 128 < M <= 192 with at most 160 64-row tiles: the last 128-row tile
+  //     is at most half used (M = 192: a quarter of the MFMA work padding);
+  //   * M <= 128, K >= 8192 with at most 40 64-row tiles (down-projections):
+  //     more, shorter workgroups than the two-slice kernel's one per tile;
+  // both only where the splits keep at least 10 k-steps each (K = N = 4096,
+  // M = 192, 48 tiles: 8 splits of 8 steps 25.5 us against 23.3 for the
+  // rule below's 4).
+  // Measured on MI355X against the plans before (µs, G = 128 / 64 / 32, warm
+  // weights, graph replay): M = 192, K = 4096, N = 6144 29.9 / 29.8 / 30.0 ->
+  // 27.5 / 27.9 / 27.1; K = N = 5120 29.0 / 28.4 / 29.3 -> 26.0 / 25.5 / 26.7;
+  // K = 13824, N = 5120 47.0 / 46.4 / 48.9 -> 41.9 / 42.4 / 43.2; K = 8192,
+  // N = 10240 52.2 / 52.3 / 54.4 -> 46.6 / 46.6 / 47.6; K = 4096, N = 12288
+  // 38.7 / 38.8 / 41.9 -> 38.1 / 37.6 / 38.5; M = 96 / 128, K = 11008, N =
+  // 4096 27.8 / 28.9 -> 26.3 / 27.2 (G = 32: 28.7 / 29.7 -> 26.7 / 27.8);
+  // K = 13824, N = 5120 33.0 / 34.4 -> 31.6 / 33.1.  Not taken: more 64-row
+  // tiles (K = 5120, N = 15360, M = 192, 180 tiles: 46.9 on cfg 14 against
+  // 49.3 at best; the gate+up layers), and M = 192 at K = 8192, N = 8192
+  // (96 tiles) stays 3 % slower than cfg 14 (42.2 vs 40.8), K = 28672 a tie.
+  if (M <= 256 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
+    const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
+    const bool half_tile = M > 128 && M <= 192 && t13 <= 160;
+    const bool few = M <= 128 && t13 <= 40 && K >= 8192;
+    if (half_tile || few) {
+      const int s = stream_split_two(t13, K, cus);
+      const int ns = s > 1 ? stream_splits((int)K, s) : 1;
+      if ((K / 64 + ns - 1) / ns >= 10) return {13, ns};
+    }
+  }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
   const bool c7 = mfma_cfg_applicable(7, (int)M, (int)N, (int)K, (int)G);
   const int64_t t6 = ((N + 255) / 256) * ((M + 127) / 128);
