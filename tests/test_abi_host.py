@@ -797,6 +797,14 @@ def test_planner_prefill_split_k():
     # the one-per-CU rule above), nor on more tiles
     assert (_lib.plan(192, 4096, 4096, 128).tile_cfg, _lib.plan(192, 4096, 4096, 128).split_k) == (13, 4)
     assert _lib.plan(192, 15360, 5120, 128).tile_cfg == 14      # 180 64-row tiles
+    p = _lib.plan(192, 5120, 28672, 128)                        # long rows too
+    assert (p.tile_cfg, p.split_k) == (13, 8)
+    # smaller groups: the few-tile case up to 64 tiles, K <= 16384
+    for G in (64, 32):
+        p = _lib.plan(128, 8192, 8192, G)
+        assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, 8), G
+    assert _lib.plan(128, 8192, 8192, 128).tile_cfg == 14
+    assert _lib.plan(128, 8192, 28672, 64).tile_cfg == 14
     # more tiles than CUs: cfg 11
     p = _lib.plan(1024, 14336, 4096, 128)
     assert (p.tile_cfg, p.split_k) == (11, 1)

@@ -554,12 +554,21 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // 4096 27.8 / 28.9 -> 26.3 / 27.2 (G = 32: 28.7 / 29.7 -> 26.7 / 27.8);
   // K = 13824, N = 5120 33.0 / 34.4 -> 31.6 / 33.1.  Not taken: more 64-row
   // tiles (K = 5120, N = 15360, M = 192, 180 tiles: 46.9 on cfg 14 against
-  // 49.3 at best; the gate+up layers), and M = 192 at K = 8192, N = 8192
-  // (96 tiles) stays 3 % slower than cfg 14 (42.2 vs 40.8), K = 28672 a tie.
+  // 49.3 at best; the gate+up layers).  Long rows gain most (planner audit,
+  // M = 192, G = 128: K = 16384 / 28672, N = 5120 +16 / +14 %; K = 20480,
+  // N = 10240 +14 %; K = 28672, N = 6144 +6 %); on 96 tiles (N = 8192) the
+  // plan stays within 1 % of cfg 14 and 3-4 % behind cfg 11 split eight
+  // ways at K = 28672, and 3 % behind cfg 14 at K = 8192 (42.2 vs 40.8).
+  // With G % 128 != 0 (a scale / zero load every k-step or half-step, which
+  // costs the two-slice kernel more) the few-tile case reaches 64 tiles up to
+  // K = 16384 (planner audit, K = N = 8192, M = 96 / 128: G = 64 29.8 / 32.4
+  // -> 28.8 / 31.3, G = 32 31.4 / 34.6 -> 29.9 / 32.3; at G = 128 within 2 %
+  // either way, and K = 28672 on 64 tiles 12 % slower on cfg 13).
   if (M <= 256 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
     const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
     const bool half_tile = M > 128 && M <= 192 && t13 <= 160;
-    const bool few = M <= 128 && t13 <= 40 && K >= 8192;
+    const bool few = M <= 128 && K >= 8192 &&
+                     (t13 <= 40 || (G % 128 != 0 && t13 <= 64 && K <= 16384));
     if (half_tile || few) {
       const int s = stream_split_two(t13, K, cus);
       const int ns = s > 1 ? stream_splits((int)K, s) : 1;
