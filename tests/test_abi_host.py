@@ -593,6 +593,22 @@ def test_planner_decode_table():
         assert a == b, (M, N, K, a, b)
 
 
+def test_planner_small_groups_small_m_long_rows_gemv():
+    """G % 64 != 0, M = 3..4, K >= 11008, 3072 <= N <= 4096: the GEMV on
+    64-column blocks split four ways (measured faster than the skinny kernel
+    there); not with larger groups, at K = 8192, M = 5 or N = 5120."""
+    from w4a16 import _lib
+
+    for M, K in ((3, 11008), (4, 14336), (3, 28672), (4, 20480)):
+        p = _lib.plan(M, 4096, K, 32).as_dict()
+        assert (p["kernel_name"], p["tile_cfg"], p["tile_n"], p["split_k"]) == ("gemv", 1, 64, 4), (M, K)
+        assert p["workspace_bytes"] == 4 * M * 4096 * 4
+    for M, N, K, G in ((3, 4096, 11008, 64), (4, 4096, 14336, 128), (3, 4096, 8192, 32),
+                       (5, 4096, 14336, 32), (3, 5120, 13824, 32)):
+        p = _lib.plan(M, N, K, G).as_dict()
+        assert not (p["kernel_name"] == "gemv" and p["tile_n"] == 64 and p["split_k"] == 4), (M, N, K, G, p)
+
+
 def test_planner_small_batch_wide_weights_stream():
     """4 <= M <= 64 on large enough, wide weights takes the streamed prefill
     kernel with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K

@@ -801,6 +801,19 @@ size_t mfma_workspace_bytes(int64_t M, int64_t N, int64_t K, int split) {
   return occ2_workspace_bytes((int)M, (int)N, (int)K, split);
 }
 
+// G % 64 != 0 (a scale / zero load every 32 k, which the skinny kernel's
+// 4-wave loop pays in every k-step), M = 3..4, long rows on 3072..4096
+// columns: the GEMV on 64-column blocks split four ways (256 workgroups)
+// instead of the skinny kernel.  Measured on MI355X, G = 32, N = 4096, µs,
+// skinny -> GEMV: M = 3, K = 11008 / 14336 / 16384 / 20480 / 28672 15.3 /
+// 17.9 / 20.2 / 24.2 / 32.3 -> 13.4 / 16.3 / 16.6 / 18.8 / 27.0; M = 4 15.5 /
+// 18.4 / 20.4 / 24.6 / 32.3 -> 14.5 / 17.6 / 17.8 / 21.2 / 26.9.  Not at
+// K = 8192 (a tie at M = 3, 3.6 % slower at M = 4), N = 5120 (mixed), M >= 5
+// or with larger groups (the skinny kernel stays fastest).
+bool small_m_long_k_gemv(int64_t M, int64_t N, int64_t K, int64_t G) {
+  return G % 64 != 0 && M >= 3 && M <= 4 && K >= 11008 && N >= 3072 && N <= 4096 && N % 4 == 0;
+}
+
 int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_t split,
               w4a16_plan* p) {
   const int cus = device_cu_count();
@@ -850,6 +863,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
       kernel = W4A16_KERNEL_SIMT;
     else if (skinny_applicable(M, G) && skinny_row_groups(M, N, K, G, cus).cfg >= 0)
       kernel = W4A16_KERNEL_SKINNY;
+    else if (gemv_applicable(M, N, G) && small_m_long_k_gemv(M, N, K, G))
+      kernel = W4A16_KERNEL_GEMV;
     else if (small_m_takes_stream(M, N, K, G))
       kernel = skinny_applicable(M, G) && (skinny_quad(M, N, K, G, cus) ||
                                            skinny_wide_beats_stream(M, N, K, G, cus))
@@ -870,8 +885,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int64_t G, int32_t kernel, int32_
     case W4A16_KERNEL_GEMV: {
       if (!gemv_applicable(M, N, G)) return W4A16_ERR_BAD_PLAN;
       const int mfma_split = split > 0 ? 0 : gemv_mfma_split(M, N, K, cus);
-      const int cols = mfma_split ? 64 : gemv_cols_auto(M, N, K, cus);
+      const bool g32 = split <= 0 && small_m_long_k_gemv(M, N, K, G);
+      const int cols = mfma_split ? 64 : g32 ? 64 : gemv_cols_auto(M, N, K, cus);
       int S = split > 0                                   ? split
+              : g32                                       ? 4
               : mfma_split                                ? mfma_split
               : cols == 64 && gemv_band64(M, N, K, cus)   ? 1
               : cols == 32 && gemv_band32(N, cus)         ? 1
