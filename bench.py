@@ -439,7 +439,7 @@ def planner_audit(shapes, ms, G: int = 128, steps: int = 30, reps: int = 3) -> s
 # covers K in [DECODE_KS[0], DECODE_KS[-1]] and N in [DECODE_NS[0], DECODE_NS[-1]]
 DECODE_KS = [3584, 4096, 5120, 6144, 8192, 11008, 13824, 14336, 16384, 20480, 28672]
 DECODE_NS = [4096, 5120, 6144, 8192, 10240, 11008, 12288, 14336, 15360, 16384, 20480, 22016,
-             24576, 27648, 28672, 32768, 40960, 57344]
+             24576, 27648, 28672, 32768, 40960, 57344, 65536, 98304, 131072, 163840]
 DECODE_TABLE = os.path.join(PKG_DIR, "csrc", "decode_table.inc")
 
 

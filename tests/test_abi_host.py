@@ -609,6 +609,19 @@ def test_planner_small_groups_small_m_long_rows_gemv():
         assert not (p["kernel_name"] == "gemv" and p["tile_n"] == 64 and p["split_k"] == 4), (M, N, K, G, p)
 
 
+def test_planner_lm_head_small_batch_split():
+    """32-row streamed tiles past one round of two per CU (512 without a
+    device): split two ways where that packs the tiles into fewer rounds."""
+    from w4a16 import _lib
+
+    for M, K, N in ((16, 4096, 151936), (32, 3584, 152064)):
+        p = _lib.plan(M, N, K, 128).as_dict()
+        assert (p["tile_cfg"], p["split_k"], p["grid_x"]) == (12, 2, 1188), (M, K, N)
+    p = _lib.plan(16, 128256, 8192, 128).as_dict()             # 501 tiles: one round
+    assert (p["tile_cfg"], p["split_k"]) == (12, 1)
+    assert _lib.plan(64, 151936, 4096, 128).split_k == 1     # 64-row tiles stay unsplit
+
+
 def test_planner_small_batch_wide_weights_stream():
     """4 <= M <= 64 on large enough, wide weights takes the streamed prefill
     kernel with 32-row (M <= 32, cfg 12) or 64-row tiles (cfg 13), split along K

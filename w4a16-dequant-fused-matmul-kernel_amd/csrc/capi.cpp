@@ -533,7 +533,16 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
       const int s32 = stream_split_one_per_cu(2 * tiles, K, cus);
       if (s32) return {12, s32 > 1 ? stream_splits((int)K, s32) : 1};
     }
-    const int s = stream_split_two(tiles, K, cus);
+    int s = stream_split_two(tiles, K, cus);
+    // 32-row tiles beyond one round of two per CU (LM-head widths): split two
+    // ways where that packs them into fewer full rounds (594 tiles, M = 16,
+    // K = 4096 / 3584, N = 151936 / 152064: 99.1 / 87.3 -> 91.9 / 79.4 us;
+    // 501 tiles, N = 128256, unsplit, are within one round; the 64-row tiles
+    // of M = 64 at N = 151936 measured no faster split)
+    const int64_t slots = 2 * (int64_t)cus;
+    if (rows == 32 && tiles > slots && K / 64 / 2 >= 8 &&
+        (2 * tiles + slots - 1) / slots < 2 * ((tiles + slots - 1) / slots))
+      s = 2;
     return {M <= 32 ? 12 : 13, s > 1 ? stream_splits((int)K, s) : 1};
   }
   // 64-row tiles (cfg 13, one k-slice) split for about two workgroups per CU,
