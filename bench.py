@@ -39,6 +39,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -521,19 +522,37 @@ def decode_table(scan_paths) -> str:
              "// 32: other G % 32 == 0) and (M, K, N) of the grid, cold weights, the",
              "// fastest GEMV / skinny plan.  Fields: G class, M, K, N, kernel (1 GEMV,",
              "// 4 skinny), tile_cfg, tile_n, tile_m (skinny rows), split_k, µs x 100 of",
-             "// the fastest, of the plan the planner gave when scanned.",
+             "// the fastest, of the plan the planner gave when scanned (0: the grid",
+             "// point's weights exceed the vector kernels' 2 GiB limit; the entry repeats",
+             "// the nearest fitting K's plan for the fitting shapes around it).",
              "// clang-format off"]
     latest = {}
     for r in rows:
         latest[(gclass(r.get("G", 128)), r["M"], r["K"], r["N"])] = r
-    new = []
-    for key, r in latest.items():
+
+    def fastest(r):
         us = r["us"]
         best = min(us, key=us.get)
-        p = r["plans"][best]
+        return best, r["plans"][best]
+
+    new = []
+    for key, r in latest.items():
+        best, p = fastest(r)
+        us = r["us"]
+        b_us, s_us = round(100 * us[best]), round(100 * us["static"])
+        if p["kernel"] not in (1, 4):
+            # the grid point's operands exceed the vector kernels' 2 GiB
+            # limit (only the SIMT plan ran): repeat the plan of the nearest
+            # K that fits, for the fitting shapes around the point, and mark
+            # the entry with 0 us
+            near = [v for k, v in latest.items() if k[:2] == key[:2] and k[3] == key[3]
+                    and fastest(v)[1]["kernel"] in (1, 4)]
+            if near:
+                p = fastest(min(near, key=lambda v: abs(math.log2(v["K"] / key[2]))))[1]
+                b_us = s_us = 0
         new.append((key, f"{{{key[0]}, {r['M']}, {r['K']}, {r['N']}, {p['kernel']}, "
                          f"{p['tile_cfg']}, {p['tile_n']}, {p['tile_m']}, {p['split_k']}, "
-                         f"{round(100 * us[best])}, {round(100 * us['static'])}}},"))
+                         f"{b_us}, {s_us}}},"))
     for ln in kept:
         f = [int(v) for v in ln.strip("{},").split(",")[:4]]
         new.append((tuple(f), ln))

@@ -559,6 +559,11 @@ def test_planner_decode_table():
 
         def check(M, K, N, G):
             p = _lib.plan(M, N, K, G)
+            if K * N // 2 >= 1 << 31:
+                # weights past the vector kernels' 2 GiB limit: SIMT, whatever
+                # the table holds there (its 0-us entries serve fitting shapes)
+                assert p.kernel == _lib.KERNEL_SIMT, (G, M, K, N, p.as_dict())
+                return
             e = expect(M, K, N)
             kern, cfg, cols, rows, split = e[3:8]
             assert p.kernel == kern and p.tile_cfg == cfg, (G, M, K, N, e, p.as_dict())
