@@ -833,6 +833,19 @@ def test_planner_prefill_split_k():
     assert _lib.plan(192, 15360, 5120, 128).tile_cfg == 14      # 180 64-row tiles
     p = _lib.plan(192, 5120, 28672, 128)                        # long rows too
     assert (p.tile_cfg, p.split_k) == (13, 8)
+    # 256 < M <= 320, K <= 8192: the same where the split fills at least 9/10
+    # of two workgroups per CU, or where the 128-row tiles need a second round
+    # and the 64-row tiles fit one round of two per CU
+    for M, N, K, split in ((320, 12288, 4096, 2), (288, 6144, 4096, 4), (320, 4096, 4096, 6),
+                           (320, 5120, 5120, 5), (288, 8192, 8192, 3), (320, 22016, 4096, 1)):
+        p = _lib.plan(M, N, K, 128)
+        assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
+        assert p.grid_x == split * ((N + 255) // 256) * 5
+    # ... not on 4/5 of the slots or fewer, more than two tiles per CU, long
+    # rows, or M past 320
+    for M, N, K in ((320, 10240, 8192), (320, 15360, 5120), (320, 28672, 4096),
+                    (320, 4096, 11008), (320, 14336, 4096), (384, 12288, 4096)):
+        assert _lib.plan(M, N, K, 128).tile_cfg in (11, 14), (M, N, K)
     # smaller groups: the few-tile case up to 64 tiles, K <= 16384
     for G in (64, 32):
         p = _lib.plan(128, 8192, 8192, G)

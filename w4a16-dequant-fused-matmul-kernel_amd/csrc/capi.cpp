@@ -573,15 +573,31 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // K = 16384 (planner audit, K = N = 8192, M = 96 / 128: G = 64 29.8 / 32.4
   // -> 28.8 / 31.3, G = 32 31.4 / 34.6 -> 29.9 / 32.3; at G = 128 within 2 %
   // either way, and K = 28672 on 64 tiles 12 % slower on cfg 13).
-  if (M <= 256 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
+  // 256 < M <= 320 (the third 128-row tile at most half used), K <= 8192:
+  // the same split where its workgroups fill at least 9/10 of two per CU, or
+  // where the 128-row tiles need a second round on the CUs and the 64-row
+  // ones fit in one round of two per CU.  Planner probe, M = 288 / 320, G =
+  // 128 (µs): K = 4096, N = 12288 57.1 / 57.2 -> 47.4 / 47.5 (2 splits);
+  // N = 6144 35.1 / 35.8 -> 29.9 / 30.9 (4); K = N = 4096 29.8 / 30.8 ->
+  // 27.5 / 28.1 (6); K = N = 5120 36.3 / 37.4 -> 31.1 / 31.9 (5); K = N = 8192
+  // 63.6 / 64.0 -> 59.5 / 60.9 (3); K = 4096, N = 22016 (258 128-row tiles)
+  // 95.5 / 96.3 -> 71.0 / 72.1 (unsplit).  Not taken: 4/5 of the slots or
+  // fewer (K = 8192, N = 10240, 400 workgroups, 12-14 % slower; K = 5120,
+  // N = 15360, 300) and more than two 64-row tiles per CU (the gate+up
+  // layers of 8B / 13B / 70B, 6-11 % slower unsplit); K >= 11008 ties or
+  // loses 1-3 %.
+  if (M <= 320 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
     const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
+    const int64_t t6r = (N + 255) / 256 * ((M + 127) / 128);
     const bool half_tile = M > 128 && M <= 192 && t13 <= 160;
     const bool few = M <= 128 && K >= 8192 &&
                      (t13 <= 40 || (G % 128 != 0 && t13 <= 64 && K <= 16384));
-    if (half_tile || few) {
+    const bool third = M > 256 && K <= 8192 && t13 <= 2 * (int64_t)cus;
+    if (half_tile || few || third) {
       const int s = stream_split_two(t13, K, cus);
       const int ns = s > 1 ? stream_splits((int)K, s) : 1;
-      if ((K / 64 + ns - 1) / ns >= 10) return {13, ns};
+      const bool fills = !third || t13 * ns * 10 >= 9 * 2 * (int64_t)cus || t6r > cus;
+      if (fills && (K / 64 + ns - 1) / ns >= 10) return {13, ns};
     }
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);

@@ -130,7 +130,7 @@ def candidates(M: int, N: int, K: int, G: int) -> list[tuple[str, _lib.Plan]]:
                 add(f"skinny cfg={cfg} rows={rows}", p)
     if N % 4 == 0 and G % 32 == 0:
         if K % 256 == 0:
-            cfgs = (12, 13) if M <= 64 else ((13, 11, 14) if M <= 256 else (11, 14))
+            cfgs = (12, 13) if M <= 64 else ((13, 11, 14) if M <= 512 else (11, 14))
         else:
             cfgs = (7, 6, 1, 2) if K % 128 == 0 else ((7, 1, 2) if K % 64 == 0 else (1, 2))
         for cfg in cfgs:
