@@ -812,8 +812,8 @@ def test_planner_prefill_split_k():
         p = _lib.plan(M, N, K, 128)
         assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
         assert p.grid_x == split * (N // 256) * 2
-    # ... not with longer slices, more or fewer tiles, nor beyond M = 256
-    for M, N, K in ((128, 8192, 8192), (384, 4096, 4096), (128, 27648, 5120), (128, 10240, 8192)):
+    # ... not with longer slices, more or fewer tiles (M > 256: the rule below)
+    for M, N, K in ((128, 8192, 8192), (128, 27648, 5120), (128, 10240, 8192)):
         assert _lib.plan(M, N, K, 128).tile_cfg == 14, (M, N, K)
     # 64-row tiles split for about two workgroups per CU (>= 10 k-steps each)
     # where the last 128-row tile is at most half used (128 < M <= 192, at most
@@ -833,19 +833,26 @@ def test_planner_prefill_split_k():
     assert _lib.plan(192, 15360, 5120, 128).tile_cfg == 14      # 180 64-row tiles
     p = _lib.plan(192, 5120, 28672, 128)                        # long rows too
     assert (p.tile_cfg, p.split_k) == (13, 8)
-    # 256 < M <= 320, K <= 8192: the same where the split fills at least 9/10
-    # of two workgroups per CU, or where the 128-row tiles need a second round
-    # and the 64-row tiles fit one round of two per CU
+    # 256 < M <= 512, K <= 12288: 64-row tiles split for about two workgroups
+    # per CU where the busiest CU's work falls to 5/6 of the 128-row plan's or
+    # less, or stays level on splits of at most 20 k-steps
     for M, N, K, split in ((320, 12288, 4096, 2), (288, 6144, 4096, 4), (320, 4096, 4096, 6),
-                           (320, 5120, 5120, 5), (288, 8192, 8192, 3), (320, 22016, 4096, 1)):
+                           (320, 5120, 5120, 5), (288, 8192, 8192, 3), (320, 22016, 4096, 1),
+                           (320, 11008, 4096, 2), (384, 4096, 4096, 4), (448, 4096, 4096, 4),
+                           (384, 5120, 5120, 4), (320, 4096, 11008, 6)):
         p = _lib.plan(M, N, K, 128)
         assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (M, N, K)
-        assert p.grid_x == split * ((N + 255) // 256) * 5
-    # ... not on 4/5 of the slots or fewer, more than two tiles per CU, long
-    # rows, or M past 320
+        assert p.grid_x == split * ((N + 255) // 256) * ((M + 63) // 64)
+        assert p.grid_x <= 512
+    # ... not on level work with longer splits, past two workgroups per CU,
+    # on long rows, or past M = 512
     for M, N, K in ((320, 10240, 8192), (320, 15360, 5120), (320, 28672, 4096),
-                    (320, 4096, 11008), (320, 14336, 4096), (384, 12288, 4096)):
+                    (384, 22016, 4096), (320, 4096, 13824),
+                    (320, 14336, 4096), (384, 12288, 4096), (640, 4096, 4096)):
         assert _lib.plan(M, N, K, 128).tile_cfg in (11, 14), (M, N, K)
+    # G = 32: against the 128-row cfg 11 split of 80..128 tiles as well
+    p = _lib.plan(320, 8192, 8192, 32)
+    assert (p.tile_cfg, p.split_k) == (13, 3)
     # smaller groups: the few-tile case up to 64 tiles, K <= 16384
     for G in (64, 32):
         p = _lib.plan(128, 8192, 8192, G)

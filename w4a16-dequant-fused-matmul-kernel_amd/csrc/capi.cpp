@@ -520,7 +520,7 @@ int stream_split_two(int64_t tiles, int64_t K, int cus) {
   return two;
 }
 
-MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+MfmaChoice mfma_choice_rules(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   if (M <= 64) {
     if (!mfma_cfg_applicable(12, (int)M, (int)N, (int)K, (int)G)) return {2, 1};
     const int rows = M <= 32 ? 32 : 64;
@@ -573,31 +573,15 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   // K = 16384 (planner audit, K = N = 8192, M = 96 / 128: G = 64 29.8 / 32.4
   // -> 28.8 / 31.3, G = 32 31.4 / 34.6 -> 29.9 / 32.3; at G = 128 within 2 %
   // either way, and K = 28672 on 64 tiles 12 % slower on cfg 13).
-  // 256 < M <= 320 (the third 128-row tile at most half used), K <= 8192:
-  // the same split where its workgroups fill at least 9/10 of two per CU, or
-  // where the 128-row tiles need a second round on the CUs and the 64-row
-  // ones fit in one round of two per CU.  Planner probe, M = 288 / 320, G =
-  // 128 (µs): K = 4096, N = 12288 57.1 / 57.2 -> 47.4 / 47.5 (2 splits);
-  // N = 6144 35.1 / 35.8 -> 29.9 / 30.9 (4); K = N = 4096 29.8 / 30.8 ->
-  // 27.5 / 28.1 (6); K = N = 5120 36.3 / 37.4 -> 31.1 / 31.9 (5); K = N = 8192
-  // 63.6 / 64.0 -> 59.5 / 60.9 (3); K = 4096, N = 22016 (258 128-row tiles)
-  // 95.5 / 96.3 -> 71.0 / 72.1 (unsplit).  Not taken: 4/5 of the slots or
-  // fewer (K = 8192, N = 10240, 400 workgroups, 12-14 % slower; K = 5120,
-  // N = 15360, 300) and more than two 64-row tiles per CU (the gate+up
-  // layers of 8B / 13B / 70B, 6-11 % slower unsplit); K >= 11008 ties or
-  // loses 1-3 %.
-  if (M <= 320 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
+  if (M <= 256 && mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G)) {
     const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
-    const int64_t t6r = (N + 255) / 256 * ((M + 127) / 128);
     const bool half_tile = M > 128 && M <= 192 && t13 <= 160;
     const bool few = M <= 128 && K >= 8192 &&
                      (t13 <= 40 || (G % 128 != 0 && t13 <= 64 && K <= 16384));
-    const bool third = M > 256 && K <= 8192 && t13 <= 2 * (int64_t)cus;
-    if (half_tile || few || third) {
+    if (half_tile || few) {
       const int s = stream_split_two(t13, K, cus);
       const int ns = s > 1 ? stream_splits((int)K, s) : 1;
-      const bool fills = !third || t13 * ns * 10 >= 9 * 2 * (int64_t)cus || t6r > cus;
-      if (fills && (K / 64 + ns - 1) / ns >= 10) return {13, ns};
+      if ((K / 64 + ns - 1) / ns >= 10) return {13, ns};
     }
   }
   const bool c11 = mfma_cfg_applicable(11, (int)M, (int)N, (int)K, (int)G);
@@ -735,6 +719,50 @@ MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
   const int64_t t2 = ((N + 511) / 512) * ((M + 31) / 32);
   if (2 * t6 < cus && t2 > t6) return {2, 1};
   return {1, 1};
+}
+
+// Work of the busiest CU under a streamed plan, in row x k-step units: the
+// workgroups each CU receives (tiles x splits over the CUs, rounded up) x
+// rows per tile x k-steps per split.
+int64_t stream_cu_load(int64_t tiles, int rows, int split, int64_t K, int cus) {
+  const int64_t ks = K / 64;
+  return (tiles * split + cus - 1) / cus * rows * ((ks + split - 1) / split);
+}
+
+// 256 < M <= 512, K <= 12288: the 64-row tiles (cfg 13, one k-slice) split
+// for about two workgroups per CU instead of the 128-row plan where the
+// busiest CU's work falls to 5/6 or less (the last 128-row tile partly
+// padding, or 128-row tiles past one round), or stays level on splits of at
+// most 20 k-steps (where the two-slice kernel's short slices cost more); at
+// most two workgroups per CU, at least 10 k-steps per split.
+// Measured on MI355X (planner audit and probe, G = 128, µs, 128-row plan ->
+// 64-row plan): M = 288 / 320, K = 4096: N = 12288 57.1 / 57.2 -> 47.4 /
+// 47.5 (work 1/2); N = 11008 56.6 / 56.6 -> 45.4 / 46.5 (1/2); N = 22016
+// (258 128-row tiles) 95.5 / 96.3 -> 71.0 / 72.1 (1/2); N = 6144 35.1 / 35.8
+// -> 29.9 / 30.9 (3/4); N = 4096 29.8 / 30.8 -> 27.5 / 28.1 (2/3); K = N =
+// 5120 36.3 / 37.4 -> 31.1 / 31.9 (4/5); K = N = 8192 63.6 / 64.0 -> 59.5 /
+// 60.9 (2/3); K = 11008, N = 4096 48.0 / 49.6 -> 46.0 / 47.9 (5/6; G = 32
+// 49.5 / 51.2 -> 47.0 / 48.2); level work, 16-20 k-steps: M = 384 / 448,
+// K = N = 4096 32.9 / 34.3 -> 30.2 / 31.4; M = 384, K = N = 5120 38.0 ->
+// 34.6.  Kept: level work on longer splits (M = 320, K = 8192, N = 10240,
+// 12-14 % slower; K = 5120, N = 15360), more than two 64-row tiles per CU
+// (the 8B / 13B / 70B gate+up layers, 6-11 % slower), and K >= 13824 (5/6 of
+// the work, 1-3 % slower).
+MfmaChoice mfma_choice(int64_t M, int64_t N, int64_t K, int64_t G, int cus) {
+  const MfmaChoice c = mfma_choice_rules(M, N, K, G, cus);
+  if (M <= 256 || M > 512 || K > 12288 || (c.cfg != 11 && c.cfg != 14) ||
+      !mfma_cfg_applicable(13, (int)M, (int)N, (int)K, (int)G))
+    return c;
+  const int64_t t13 = (N + 255) / 256 * ((M + 63) / 64);
+  const int64_t t6 = (N + 255) / 256 * ((M + 127) / 128);
+  const int s = stream_split_two(t13, K, cus);
+  const int ns = s > 1 ? stream_splits((int)K, s) : 1;
+  const int64_t steps = (K / 64 + ns - 1) / ns;
+  if (t13 * ns > 2 * (int64_t)cus || steps < 10) return c;
+  const int64_t l13 = stream_cu_load(t13, 64, ns, K, cus);
+  const int64_t l6 = stream_cu_load(t6, 128, c.split, K, cus);
+  if (6 * l13 <= 5 * l6 || (l13 <= l6 && steps <= 20)) return {13, ns};
+  return c;
 }
 
 // Measured decode plans (M <= 2, 256 CUs): per group-size class (G % 128 ==
