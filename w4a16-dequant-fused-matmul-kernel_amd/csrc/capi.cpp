@@ -742,9 +742,9 @@ int64_t stream_cu_load(int64_t tiles, int rows, int split, int64_t K, int cus) {
 // -> 29.9 / 30.9 (3/4); N = 4096 29.8 / 30.8 -> 27.5 / 28.1 (2/3); K = N =
 // 5120 36.3 / 37.4 -> 31.1 / 31.9 (4/5); K = N = 8192 63.6 / 64.0 -> 59.5 /
 // 60.9 (2/3); K = 11008, N = 4096 48.0 / 49.6 -> 46.0 / 47.9 (5/6; G = 32
-// 49.5 / 51.2 -> 47.0 / 48.2); level work, 16-20 k-steps: M = 384 / 448,
-// K = N = 4096 32.9 / 34.3 -> 30.2 / 31.4; M = 384, K = N = 5120 38.0 ->
-// 34.6.  Kept: level work on longer splits (M = 320, K = 8192, N = 10240,
+// 49.5 / 51.2 -> 47.0 / 48.2); level work, 16-20 k-steps: M = 384 / 448 /
+// 512, K = N = 4096 32.9 / 34.3 / 34.4 -> 30.2 / 31.4 / 32.6; M = 384,
+// K = N = 5120 38.0 -> 34.6.  Kept: level work on longer splits (M = 320, K = 8192, N = 10240,
 // 12-14 % slower; K = 5120, N = 15360), more than two 64-row tiles per CU
 // (the 8B / 13B / 70B gate+up layers, 6-11 % slower), and K >= 13824 (5/6 of
 // the work, 1-3 % slower).
