@@ -204,6 +204,29 @@ def test_mfma_split_k(M, K, N, G):
     assert plan_for(1, 1024, 4096, 128).split_k == 1
 
 
+@pytest.mark.parametrize("M,K,N,G,split", [
+    (320, 4096, 4096, 128, 6), (300, 5120, 5120, 64, 5), (450, 4096, 4096, 32, 4),
+    (290, 4096, 11008, 128, 2),
+])
+def test_mid_m_64_row_split(M, K, N, G, split):
+    """256 < M <= 512: the automatic path where the planner takes 64-row
+    streamed tiles (cfg 13) split for about two workgroups per CU instead of
+    the 128-row plan (ragged last 64-row tile at M = 300 / 450 / 290), against
+    the oracle, with and without the fused bias."""
+    from w4a16 import w4a16_matmul
+    from w4a16.hip_kernel import plan_for, w4a16_linear
+
+    p = plan_for(M, N, K, G)
+    assert (p.tile_cfg, p.tile_m, p.split_k) == (13, 64, split), (p.tile_cfg, p.split_k)
+    X, qw, s, z = _build_case(M, K, N, G, seed=M + 7 * G)
+    ref = _ref(X, qw, s, z, G)
+    log(f"mid-M auto M={M} K={K} N={N} G={G} cfg=13 split={split}")
+    out = w4a16_matmul(X, qw, s, z, G)
+    assert_gemm_close(out, ref, f"mid-M cfg 13 split={split}")
+    b = (torch.randn(N) * 2).to(torch.float16).to(DEV)
+    assert torch.equal(w4a16_linear(X, qw, s, z, b, G), out + b)
+
+
 @pytest.mark.parametrize("M,K,N,G", [
     (9, 96, 260, 32), (16, 4096, 4096, 128), (17, 160, 7, 32), (32, 11008, 1028, 64),
     (33, 1024, 130, 32), (48, 4096, 516, 128), (64, 4096, 4100, 64), (1, 4096, 1000, 128),
