@@ -878,6 +878,56 @@ def test_planner_prefill_split_k():
                                       128, a, 1 << 30, NULL) == -5
 
 
+def test_planner_invariants_over_shape_grid():
+    """Every automatic plan over a grid of 36 M x 13 N x 9 K x 3 G (decode to
+    prefill, odd and LM-head widths, short and long rows) is well formed: the
+    grid is the tile count times the splits, every split holds at least one
+    k-block of its kernel, a split plan's workspace holds its fp32 partials
+    and the workspace query covers it, an unsplit plan needs none, and each
+    family stays within the M it serves."""
+    import itertools
+    from w4a16 import _lib
+
+    lib = _lib.load()
+    Ms = [1, 2, 3, 4, 5, 8, 13, 16, 17, 24, 32, 33, 48, 64, 65, 80, 96, 128, 129, 160, 192,
+          200, 256, 257, 288, 320, 384, 448, 512, 513, 640, 768, 1024, 1500, 2048, 4096]
+    Ns = [4, 12, 256, 1000, 1028, 4096, 6144, 11008, 14336, 22016, 28672, 57344, 128256]
+    Ks = [256, 512, 2048, 4096, 5120, 8192, 11008, 14336, 28672]
+    seen = set()
+    for M, N, K, G in itertools.product(Ms, Ns, Ks, (32, 64, 128)):
+        p = _lib.plan(M, N, K, G)
+        name = _lib.KERNEL_NAMES[p.kernel]
+        seen.add((name, p.tile_cfg))
+        case = (M, N, K, G, name, p.tile_cfg, p.split_k)
+        assert p.split_k >= 1 and p.grid_x >= 1 and p.grid_y >= 1, case
+        if p.split_k == 1:
+            assert p.workspace_bytes == 0, case
+        else:
+            assert p.workspace_bytes >= p.split_k * M * N * 4, case
+        assert lib.w4a16_gemm_workspace_bytes(M, N, K, G) >= p.workspace_bytes, case
+        if name == "mfma":
+            assert p.grid_x == -(-N // p.tile_n) * -(-M // p.tile_m) * p.split_k, case
+            if p.tile_cfg >= 11:
+                # streamed tiles: whole 4-step (256-k) blocks per split, and
+                # 8-step blocks with the two k-slices of cfg 14
+                assert K % 256 == 0 and p.split_k <= K // 256, case
+                assert p.tile_cfg != 14 or p.split_k <= max(1, K // 512), case
+            if 256 < M <= 512 and p.tile_cfg == 13:
+                assert p.grid_x <= 512, case             # at most two workgroups per CU
+        elif name == "skinny":
+            assert M <= 64 and p.split_k == 1, case
+            assert p.grid_x == -(-N // p.tile_n) * -(-M // p.tile_m), case
+        elif name == "gemv":
+            assert M <= 8 and p.split_k <= K // 8, case
+            assert p.grid_x == -(-N // p.tile_n) * p.split_k, case
+        else:
+            raise AssertionError(f"unexpected kernel for a fitting shape: {case}")
+    # the grid reaches every family and the streamed prefill configurations
+    for want in (("gemv", 1), ("gemv", 7), ("skinny", 0), ("skinny", 2), ("skinny", 3),
+                 ("mfma", 11), ("mfma", 12), ("mfma", 13), ("mfma", 14)):
+        assert want in seen, want
+
+
 def test_planner_forced_kernel_must_fit():
     from w4a16 import _lib
 
