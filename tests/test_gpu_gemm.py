@@ -260,6 +260,37 @@ def test_skinny_path(M, K, N, G):
             assert torch.equal(outb, out + b)
 
 
+@pytest.mark.parametrize("M,K,N,G", [
+    (16, 2080, 1030, 32), (24, 1056, 516, 32), (31, 4064, 772, 32), (40, 4096, 2052, 128),
+    (17, 3104, 260, 32),
+])
+def test_skinny_staged_activations(M, K, N, G):
+    """16-row groups at M >= 16 with 8 or 16 waves (1024 < K <= 4096) stage
+    each wave's activations in LDS by whole-line loads.  Ragged K (a wave's
+    batch partly or wholly past K: K = 2080 / 1056 / 3104 leave one step to
+    the last busy wave, 4064 seven) and a row-strided X whose elements past K
+    hold inf and NaN, which a whole-line load would read and which must count
+    as zero, as the direct loads' out-of-range steps do; every block width,
+    against the oracle."""
+    from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
+
+    X, qw, s, z = _build_case(M, K, N, G, seed=K + M)
+    ref = _ref(X, qw, s, z, G)
+    ldx = K + 64
+    Xp = torch.full((M, ldx), float("nan"), dtype=torch.float16, device=DEV)
+    Xp[:, K:K + 32] = float("inf")
+    Xp[:, :K] = X
+    Xs = Xp[:, :K]
+    assert Xs.stride(0) == ldx
+    for cfg in (0,) + ((2,) if N % 2 == 0 else ()) + ((3,) if N % 4 == 0 else ()):
+        p = plan_for(M, N, K, G, "skinny")
+        p.tile_cfg, p.tile_m = cfg, 16
+        for name, x in (("dense", X), ("strided", Xs)):
+            log(f"skinny staged M={M} K={K} N={N} G={G} cfg={cfg} {name}")
+            out = w4a16_matmul_planned(x, qw, s, z, G, p)
+            assert_gemm_close(out, ref, f"skinny staged cfg={cfg} {name}")
+
+
 @pytest.mark.parametrize("M,K,N,G", [(1, 64, 130, 32), (17, 96, 7, 32), (4, 24, 12, 12), (2, 8, 5, 4)])
 def test_simt_path_any_shape(M, K, N, G):
     """SIMT kernel: odd N, G not a multiple of 8."""

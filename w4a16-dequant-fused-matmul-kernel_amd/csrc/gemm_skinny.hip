@@ -68,14 +68,19 @@ constexpr int kBatch = 8;  // k-steps (32 k each) per batch
 // geo = row groups per column block | rows per group << 8 | group shift << 16;
 // k / G is (umulhi(k, gmagic) + k) >> shift (group_div), no division; the
 // grid size is nblk * mgs (no read of the dispatch packet).
-template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH, bool AZ>
+template <int MT, int GSTEP, int WAVES, int NT, bool ONE_BATCH, bool AZ, bool XS>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     const f16* __restrict__ X, const uint32_t* __restrict__ QW, const uint16_t* __restrict__ SC,
     const uint16_t* __restrict__ ZR, int M, int N, int K, uint32_t gmagic, uint32_t geo, int ldx,
     int ldy, const f16* __restrict__ bias, f16* __restrict__ Y) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four columns per lane");
+  static_assert(!XS || (ONE_BATCH && MT * NT <= 8), "staged activations: one batch per wave");
   constexpr int kWaves = WAVES;
-  __shared__ f32x4 red[kWaves][MT][NT][64];
+  // XS: per wave and m-tile, 512 16-byte slots for the batch's activations
+  // (16 rows x 512 B); once the wave's products are done the same space holds
+  // its partial tiles.  Otherwise only the partial tiles, in red.
+  __shared__ uint4 xs[XS ? kWaves * MT * 512 : 1];
+  __shared__ f32x4 red[XS ? 1 : kWaves][MT][NT][64];
 
   const int mgs = (int)(geo & 0xFFu), rpg = (int)((geo >> 8) & 0xFFu);
   const int gshift = (int)(geo >> 16);
@@ -102,6 +107,13 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   const int NG = (int)group_of((uint32_t)K);
 
   const MagicRegs mg = make_magic();
+  // partial tile (mt, t) of wave w, lane `lane`
+  auto red_at = [&](int w, int mt, int t) -> f32x4& {
+    if constexpr (XS)
+      return reinterpret_cast<f32x4*>(xs)[w * MT * 512 + (mt * NT + t) * 64 + lane];
+    else
+      return red[w][mt][t][lane];
+  };
   // rows of X lie ldx elements apart; the range ends after row M - 1's K
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(X, ((uint32_t)(M - 1) * (uint32_t)ldx + (uint32_t)K) * 2u);
@@ -135,12 +147,51 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
                     : kOobOffset;
   }
 
+  // XS: load j of m-tile mt brings rows 2j and 2j + 1 of the tile (lanes 0-31
+  // and 32-63), 16 B per lane of the batch's 512 B per row, so each load reads
+  // eight whole 128-byte lines (the direct fragment loads read 16 rows x 64 B,
+  // half of 16 lines each: measured on MI355X with same-byte loads, M = 16 /
+  // 24 / 32, K = N = 4096, 6.68 / 7.85 / 7.95 -> 6.11 / 6.31 / 6.66 us).
+  // Lane L writes slot 64 j + L, which holds chunk (L % 32) ^ (row % 16) of
+  // its row, so a fragment read (16 rows, one chunk each) hits 16 distinct
+  // 16-byte bank groups: the row r = 2j + L / 32 chunk (L % 32) ^ r sits at
+  // slot 32 r + ((chunk) ^ r).
+  // Chunks at or past the wave's last k-step (K % 256 != 0, or a wave with
+  // fewer steps) and rows past M or past the row group read zero, as the
+  // direct loads' past steps do (the past steps run branch-free against zero
+  // weights, and a row's bytes past K may hold anything).  Never both offsets
+  // out of range at once: their sum would wrap.
+  const uint32_t xs_h = (uint32_t)(lane >> 5);
+  const uint32_t xs_voff = xs_h * (uint32_t)ldx * 2u;
+  const uint32_t xs_chunk = ((uint32_t)(lane & 31) ^ xs_h) << 4;   // load j: ^ (j << 5)
+  const uint32_t xs_step = ((uint32_t)(lane & 31) ^ xs_h) >> 2;     // load j: ^ (j >> 1)
+  uint4* const xs_wave = XS ? xs + wave * MT * 512 : xs;
+
   struct Batch {
     uint32_t w[kBatch][NT];
     uint32_t sz[kBatch][NT];  // scale bits | zero bits << 16
     uint4 x[kBatch][MT];
   };
   auto load_batch = [&](int s0, Batch& b) {
+    if constexpr (XS) {
+      // the activations first: loads retire in issue order, so the wait for
+      // them before the first LDS read does not wait for the weights
+      const uint32_t lim = (uint32_t)max(0, ke - s0);   // steps of the batch in range
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int r = mt * 16 + 2 * j;
+          const bool rows_in = r < rpg && row0 + r < M;        // wave-uniform
+          const uint32_t xo =
+              uniform(rows_in ? (uint32_t)(row0 + r) * (uint32_t)ldx * 2u + (uint32_t)s0 * 64u : 0u);
+          const uint32_t vo = rows_in && (xs_step ^ (uint32_t)(j >> 1)) < lim
+                                  ? xs_voff + (xs_chunk ^ ((uint32_t)j << 5))
+                                  : kOobOffset;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rx, (lds_void*)(xs_wave + mt * 512 + 64 * j), 16, vo, xo, 0, 0);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int ks = s0 + j;
@@ -191,10 +242,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
           for (int t = 0; t < NT; ++t)   // same group as the batch slot it copies
             b.sz[j][t] = b.sz[j - j % GSTEP][t];
         }
-        const uint32_t xk = uniform(in ? (uint32_t)ks * 64u : kOobOffset);
+        if constexpr (!XS) {
+          const uint32_t xk = uniform(in ? (uint32_t)ks * 64u : kOobOffset);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
+          for (int mt = 0; mt < MT; ++mt) b.x[j][mt] = buf_load16(rx, x_off[mt], xk);
         }
       }
     }
@@ -227,7 +278,11 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
       constexpr bool kXPerm = MT == 1 || NT > MT;
       uint4 xa[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xa[mt] = kXPerm ? perm_pairs(b.x[j][mt]) : b.x[j][mt];
+      for (int mt = 0; mt < MT; ++mt) {
+        // XS: row c, chunk 4 j + q of the staged batch
+        const uint4 xv = XS ? xs_wave[mt * 512 + 32 * c + ((4 * j + q) ^ c)] : b.x[j][mt];
+        xa[mt] = kXPerm ? perm_pairs(xv) : xv;
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const ColQ cq = make_colq<AZ>(b.sz[j][t] & 0xFFFFu, b.sz[j][t] >> 16);
@@ -277,16 +332,16 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) red[wave][mt][t][lane] = acc[mt][t];
+    for (int t = 0; t < NT; ++t) red_at(wave, mt, t) = acc[mt][t];
   __syncthreads();
   // wave w finishes tiles w, w + WAVES, ...: sum the waves in order, round, store
   for (int i = wave; i < MT * NT; i += kWaves) {
     const int mt = i / NT;
     {
       const int t = i % NT;
-      f32x4 v = red[0][mt][t][lane];
+      f32x4 v = red_at(0, mt, t);
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) v += red[w][mt][t][lane];
+      for (int w = 1; w < kWaves; ++w) v += red_at(w, mt, t);
       if (nv) {
         const f16 bv = bias ? bias[col + t] : (f16)0.0f;
 #pragma unroll
@@ -319,10 +374,26 @@ hipError_t launch_ntz(const GemmArgs& a, int rpg, hipStream_t st) {
   // 16 waves hold 128 registers each: 64 rows with a scale / zero load per
   // step would spill there, and take the loop instead
   constexpr int k16 = MT == 4 && GSTEP == 1 ? 0 : 16;
-  auto k = ks <= 4 * kBatch     ? skinny_kernel<MT, GSTEP, 4, NT, true, AZ>
-           : ks <= 8 * kBatch   ? skinny_kernel<MT, GSTEP, 8, NT, true, AZ>
-           : ks <= k16 * kBatch ? skinny_kernel<MT, GSTEP, (k16 ? k16 : 4), NT, true, AZ>
-                                : skinny_kernel<MT, GSTEP, 4, NT, false, AZ>;
+  // Activations staged in LDS by whole-line loads (XS) on one 16-row tile
+  // of 8 or 16 waves (64 / 128 KiB of LDS) whose rows the call fills: M >= 16
+  // and 16-row groups.  Measured on MI355X against the direct fragment loads
+  // (µs, G = 128, cold weights): K = N = 4096, M = 24 / 32 7.81 / 7.93 ->
+  // 6.60 / 6.77; N = 6144, M = 16 / 32 (64-column blocks) 8.05 / 9.64 ->
+  // 7.13 / 8.89; N = 14336 / 28672, M = 16 10.84 / 21.11 -> 10.06 / 19.74;
+  // K = 2048, N = 4096, M = 32 5.28 -> 4.81.  Not taken: M = 4 (1.6-4.4 %
+  // slower: a few rows gain nothing from whole lines and pay the LDS round
+  // trip), M = 8 and 8-row groups (-7 .. +2 %), 4 waves (K <= 1024: M = 16
+  // 8 % slower, M = 32 a tie).
+  const bool xs = MT == 1 && rpg >= 16 && a.M >= 16;
+  using Kernel = decltype(&skinny_kernel<MT, GSTEP, 4, NT, true, AZ, false>);
+  constexpr int w16 = k16 ? k16 : 4;
+  const Kernel k =
+      ks <= 4 * kBatch     ? skinny_kernel<MT, GSTEP, 4, NT, true, AZ, false>
+      : ks <= 8 * kBatch   ? (xs ? skinny_kernel<MT, GSTEP, 8, NT, true, AZ, MT == 1>
+                                 : skinny_kernel<MT, GSTEP, 8, NT, true, AZ, false>)
+      : ks <= k16 * kBatch ? (xs ? skinny_kernel<MT, GSTEP, w16, NT, true, AZ, MT == 1 && w16 == 16>
+                                 : skinny_kernel<MT, GSTEP, w16, NT, true, AZ, false>)
+                           : skinny_kernel<MT, GSTEP, 4, NT, false, AZ, false>;
   const int waves = ks <= 4 * kBatch ? 4 : ks <= 8 * kBatch ? 8 : ks <= k16 * kBatch ? k16 : 4;
   const GroupDiv gd = group_div(a.G);
   const uint32_t geo = (uint32_t)mgs | ((uint32_t)rpg << 8) | ((uint32_t)gd.shift << 16);

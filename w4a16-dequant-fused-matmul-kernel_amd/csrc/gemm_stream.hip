@@ -69,8 +69,6 @@ constexpr int kBN = 16 * kNTiles * kWaves; // 256 columns
 // or 2 (64 / 32 rows: small M, where a 128-row tile would spend most of its
 // matrix-core time on rows past M; the dequant per weight is the same)
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Workgroup barrier for the activation tile: this wave's LDS accesses
 // complete, then s_barrier.  __syncthreads() would also wait for every
 // outstanding LDS-direct load (its fence covers all LDS writes, vmcnt(0)),

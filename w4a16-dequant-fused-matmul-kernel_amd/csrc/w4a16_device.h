@@ -198,6 +198,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 // Byte offset that no buffer range contains: loads from it return zero.
 constexpr uint32_t kOobOffset = 0x80000000u;
 
+// LDS destination of the buffer loads' LDS-direct form (address space 3).
+typedef __attribute__((address_space(3))) void lds_void;
+
 // Wave-uniform value promised to the compiler (keeps buffer SGPR offsets scalar).
 __device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
