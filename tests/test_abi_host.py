@@ -362,16 +362,18 @@ def test_planner_kernel_choice(M, N, K, G, kernel):
     assert p.grid_x >= 1 and p.grid_y >= 1
     if kernel == "skinny":
         # M > 16 with K <= 4096 and few enough blocks: one 16-row group per
-        # workgroup (test_planner_skinny_row_groups); else 32-column blocks
-        # (cfg 2) where 16-column ones outnumber the CUs (256 on MI355X, also
-        # the library's value without a device), M <= 32 and N even; else
-        # 16-column blocks with 4 waves
+        # workgroup (test_planner_skinny_row_groups); 13 <= M <= 16 two 8-row
+        # groups, except M = 16 with 1024 < K <= 4096 (the whole 16-row tile,
+        # its activations staged); else 32-column blocks (cfg 2) where
+        # 16-column ones outnumber the CUs (256 on MI355X, also the library's
+        # value without a device), M <= 32 and N even; else 16-column blocks
         g = (M + 15) // 16
         rg = (M > 16 and K <= 4096 and
               (N % 2 == 0 and (N + 31) // 32 * g <= 256 or
-               N % 4 == 0 and (N + 63) // 64 * g <= (512 if G % 64 == 0 else 256)))
+               N % 4 == 0 and (N + 63) // 64 * g <= (512 if G % 64 == 0 or K > 1024 else 256)))
         rg8 = (13 <= M <= 16 and N % 2 == 0 and (N + 31) // 32 * 2 <= 256 and
-               (K <= 4096 or G % 128 == 0 and K <= 16384))
+               (K <= 4096 or G % 128 == 0 and K <= 16384) and
+               not (M == 16 and 1024 < K <= 4096))
         quad = M <= 16 and N % 4 == 0 and (G % 64 == 0 or K <= 4096) and (N + 63) // 64 > 128
         wide = (N + 15) // 16 > 256 and N % 2 == 0 and M <= 32
         if rg or rg8:
@@ -682,7 +684,8 @@ def test_planner_skinny_row_groups():
     """17 <= M <= 64: skinny blocks with one 16-row group per workgroup
     (tile_m 16, ceil(M / 16) workgroups per column block) where the workgroups
     stay near the CU count: 32-column blocks while they fit one round, else
-    64-column blocks up to two rounds for K <= 4096 (one round at G = 32);
+    64-column blocks up to two rounds for K <= 4096 (one round at G = 32 with
+    K <= 1024);
     with longer K only two row groups on one round, 32-column blocks up to
     K = 16384 (K = 8192 below G = 128) and 64-column ones from M = 24 up to
     K = 8192 with G % 128 == 0."""
@@ -696,19 +699,25 @@ def test_planner_skinny_row_groups():
                             (32, 4096, 16384, 128, 2), (32, 4096, 4096, 64, 2),
                             (32, 4096, 4096, 32, 2), (48, 4096, 4096, 32, 3),
                             (64, 8192, 4096, 64, 3), (32, 4096, 8192, 64, 2),
-                            (24, 4096, 8192, 32, 2)):
+                            (24, 4096, 8192, 32, 2), (48, 6144, 4096, 32, 3),
+                            (64, 6144, 4096, 32, 3), (32, 14336, 4096, 32, 3)):
         p = _lib.plan(M, N, K, G)
         assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K, G)
         cols = 64 if cfg == 3 else 32
         assert (p.tile_cfg, p.tile_m, p.tile_n) == (cfg, 16, cols), (M, N, K, G)
         assert p.grid_x == (N + cols - 1) // cols * ((M + 15) // 16) and p.split_k == 1
     # 13 <= M <= 16: two 8-row groups on 32-column blocks that fit the CUs, up
-    # to K = 4096 at any G and K = 16384 with G % 128 == 0
-    for M, N, K, G in ((16, 4096, 4096, 128), (13, 4096, 14336, 128), (16, 4096, 4096, 64),
-                       (16, 4096, 4096, 32)):
+    # to K = 4096 at any G and K = 16384 with G % 128 == 0 ...
+    for M, N, K, G in ((15, 4096, 4096, 128), (13, 4096, 14336, 128), (16, 4096, 14336, 128),
+                       (16, 4096, 1024, 64), (14, 4096, 4096, 32)):
         p = _lib.plan(M, N, K, G)
         assert _lib.KERNEL_NAMES[p.kernel] == "skinny", (M, N, K, G)
         assert (p.tile_cfg, p.tile_m, p.tile_n, p.grid_x) == (2, 8, 32, N // 32 * 2), (M, N, K, G)
+    # ... except M = 16 with 1024 < K <= 4096: the whole 16-row tile (its
+    # activations staged in LDS), 16-column blocks at N = 4096
+    for G in (128, 64, 32):
+        p = _lib.plan(16, 4096, 4096, G)
+        assert (p.tile_cfg, p.tile_m, p.tile_n, p.grid_x) == (0, 16, 16, 256), G
     # not: wide N, three or more row groups with K > 4096, M = 17 on 64-column
     # blocks with K > 4096, long rows (32-column blocks beyond K = 16384,
     # 64-column ones beyond 8192), smaller groups with longer K or (G = 32)
@@ -717,7 +726,7 @@ def test_planner_skinny_row_groups():
                        (64, 4096, 14336, 128), (17, 8192, 8192, 128), (32, 8192, 28672, 128),
                        (32, 4096, 28672, 128), (24, 4096, 20480, 128), (32, 6144, 14336, 128),
                        (16, 4096, 28672, 128), (32, 4096, 14336, 64), (32, 6144, 8192, 64),
-                       (16, 4096, 14336, 64), (32, 14336, 4096, 32), (48, 6144, 4096, 32),
+                       (16, 4096, 14336, 64), (48, 14336, 4096, 32),
                        (12, 4096, 4096, 128), (16, 6144, 4096, 128)):
         p = _lib.plan(M, N, K, G)
         assert not (_lib.KERNEL_NAMES[p.kernel] == "skinny" and p.tile_m < (M + 15) // 16 * 16), (M, N, K, G)

@@ -441,6 +441,12 @@ SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus
   if (M <= 12 || M > kSkinnyMaxM) return {-1, 0};
   const bool g128 = G % 128 == 0;
   const bool c2 = N % 2 == 0, c3 = N % 4 == 0;
+  // M = 16 with one batch per wave on 8 or 16 waves (1024 < K <= 4096): the
+  // whole 16-row tile, whose activations the kernel stages in LDS by
+  // whole-line loads (measured on MI355X, K = N = 4096: two 8-row groups on
+  // 32-column blocks 6.78 / 7.31 us at G = 128 / 32 against 6.31 / 6.76 on
+  // 16-column blocks of all 16 rows)
+  if (M == 16 && K > 1024 && K <= 4096) return {-1, 0};
   if (M <= 16)
     return c2 && (N + 31) / 32 * 2 <= cus && (K <= 4096 || (g128 && K <= 16384))
                ? SkinnyRows{2, 8}
@@ -450,8 +456,9 @@ SkinnyRows skinny_row_groups(int64_t M, int64_t N, int64_t K, int64_t G, int cus
   if (K <= 4096) {
     if (c2 && wg2 <= cus) return {2, 16};
     // 64-column blocks over as many rounds as keep rounds x K within 8192
-    // (4096 at G = 32): a round's workgroups are short at small K
-    if (c3 && wg3 * K <= (G % 64 == 0 ? 8192 : 4096) * (int64_t)cus) return {3, 16};
+    // (4096 at G = 32 with K <= 1024, where the activations are not staged):
+    // a round's workgroups are short at small K
+    if (c3 && wg3 * K <= (G % 64 == 0 || K > 1024 ? 8192 : 4096) * (int64_t)cus) return {3, 16};
     return {-1, 0};
   }
   if (c2 && wg2 <= cus && K <= (g128 ? 16384 : 8192) && (g == 2 || g128)) return {2, 16};
