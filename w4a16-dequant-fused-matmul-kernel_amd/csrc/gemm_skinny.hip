@@ -32,7 +32,9 @@
 //     exact;
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
-//     the buffer range check;
+//     the buffer range check.  On a 16-row tile with one batch per wave and
+//     M >= 16 (XS) they come instead through the wave's own LDS slots, loaded
+//     as whole rows (whole 128-byte lines) by LDS-direct loads;
 //   * dequant is the packed-fp16 magic-number form; its pairs come out in the
 //     order (w0 w4, w1 w5, w2 w6, w3 w7), and the MFMA's k order is matched by
 //     permuting the activation fragment (one m-tile, or more n-tiles than
