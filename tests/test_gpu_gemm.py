@@ -262,16 +262,17 @@ def test_skinny_path(M, K, N, G):
 
 @pytest.mark.parametrize("M,K,N,G", [
     (16, 2080, 1030, 32), (24, 1056, 516, 32), (31, 4064, 772, 32), (40, 4096, 2052, 128),
-    (17, 3104, 260, 32),
+    (17, 3104, 260, 32), (24, 8224, 516, 32), (32, 11008, 1030, 64), (17, 5120, 260, 128),
 ])
 def test_skinny_staged_activations(M, K, N, G):
-    """16-row groups at M >= 16 with 8 or 16 waves (1024 < K <= 4096) stage
-    each wave's activations in LDS by whole-line loads.  Ragged K (a wave's
-    batch partly or wholly past K: K = 2080 / 1056 / 3104 leave one step to
-    the last busy wave, 4064 seven) and a row-strided X whose elements past K
-    hold inf and NaN, which a whole-line load would read and which must count
-    as zero, as the direct loads' out-of-range steps do; every block width,
-    against the oracle."""
+    """16-row groups at M >= 16 stage each wave's activations in LDS by
+    whole-line loads with one batch per wave on 8 or 16 waves (1024 < K <=
+    4096; longer K, the 4-wave loop's direct loads, alongside).  Ragged K (a
+    wave's batch partly or wholly past K: K = 2080 / 1056 / 3104 leave one
+    step to the last busy wave, 4064 seven, 8224 one in the loop) and a
+    row-strided X whose elements past K hold inf and NaN, which a whole-line
+    load would read and which must count as zero, as the direct loads'
+    out-of-range steps do; every block width, against the oracle."""
     from w4a16.hip_kernel import plan_for, w4a16_matmul_planned
 
     X, qw, s, z = _build_case(M, K, N, G, seed=K + M)

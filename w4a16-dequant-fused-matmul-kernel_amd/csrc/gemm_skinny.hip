@@ -80,7 +80,11 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
   constexpr int kWaves = WAVES;
   // XS: per wave and m-tile, 512 16-byte slots for the batch's activations
   // (16 rows x 512 B); once the wave's products are done the same space holds
-  // its partial tiles.  Otherwise only the partial tiles, in red.
+  // its partial tiles.  Otherwise only the partial tiles, in red.  (Staged in
+  // the 4-wave two-batch loop as well, with a second array for the other
+  // register batch, it measured slower on MI355X: K = 11008 / 14336, N =
+  // 4096, M = 32 17.4 / 21.5 -> 19.0 / 22.5 us, K = N = 5120, M = 24 12.8 ->
+  // 14.0; one wave per SIMD does not hide the LDS round trip.)
   __shared__ uint4 xs[XS ? kWaves * MT * 512 : 1];
   __shared__ f32x4 red[XS ? 1 : kWaves][MT][NT][64];
 
@@ -260,6 +264,16 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
     for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{};
 
   auto process = [&](const Batch& b, int s0) {
+    // XS: the batch's fragments, all read before the first product (one LDS
+    // round trip per batch instead of one per step)
+    uint4 xf[XS ? kBatch : 1][MT];
+    if constexpr (XS) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xf[j][mt] = xs_wave[mt * 512 + 32 * c + ((4 * j + q) ^ c)];
+    }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       // Steps past the range loaded zero activations and zero scales / zeros
@@ -282,7 +296,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         // XS: row c, chunk 4 j + q of the staged batch
-        const uint4 xv = XS ? xs_wave[mt * 512 + 32 * c + ((4 * j + q) ^ c)] : b.x[j][mt];
+        const uint4 xv = XS ? xf[j][mt] : b.x[j][mt];
         xa[mt] = kXPerm ? perm_pairs(xv) : xv;
       }
 #pragma unroll
