@@ -263,9 +263,10 @@ def test_skinny_path(M, K, N, G):
 @pytest.mark.parametrize("M,K,N,G", [
     (16, 2080, 1030, 32), (24, 1056, 516, 32), (31, 4064, 772, 32), (40, 4096, 2052, 128),
     (17, 3104, 260, 32), (24, 8224, 516, 32), (32, 11008, 1030, 64), (17, 5120, 260, 128),
+    (9, 2080, 516, 32), (12, 4096, 1030, 128), (15, 1056, 772, 32),
 ])
 def test_skinny_staged_activations(M, K, N, G):
-    """16-row groups at M >= 16 stage each wave's activations in LDS by
+    """16-row tiles at M >= 9 stage each wave's activations in LDS by
     whole-line loads with one batch per wave on 8 or 16 waves (1024 < K <=
     4096; longer K, the 4-wave loop's direct loads, alongside).  Ragged K (a
     wave's batch partly or wholly past K: K = 2080 / 1056 / 3104 leave one

@@ -33,7 +33,7 @@
 //   * activations (MT x 16 rows) are read directly from global memory: the whole
 //     X is a few hundred KiB and stays in L1/L2; rows past M read as zero through
 //     the buffer range check.  On a 16-row tile with one batch per wave and
-//     M >= 16 (XS) they come instead through the wave's own LDS slots, loaded
+//     M >= 9 (XS) they come instead through the wave's own LDS slots, loaded
 //     as whole rows (whole 128-byte lines) by LDS-direct loads;
 //   * dequant is the packed-fp16 magic-number form; its pairs come out in the
 //     order (w0 w4, w1 w5, w2 w6, w3 w7), and the MFMA's k order is matched by
@@ -391,16 +391,18 @@ hipError_t launch_ntz(const GemmArgs& a, int rpg, hipStream_t st) {
   // step would spill there, and take the loop instead
   constexpr int k16 = MT == 4 && GSTEP == 1 ? 0 : 16;
   // Activations staged in LDS by whole-line loads (XS) on one 16-row tile
-  // of 8 or 16 waves (64 / 128 KiB of LDS) whose rows the call fills: M >= 16
-  // and 16-row groups.  Measured on MI355X against the direct fragment loads
+  // of 8 or 16 waves (64 / 128 KiB of LDS) that holds at least 9 rows: M >= 9
+  // and 16-row groups or the whole tile.  Measured on MI355X against the direct fragment loads
   // (µs, G = 128, cold weights): K = N = 4096, M = 24 / 32 7.81 / 7.93 ->
   // 6.60 / 6.77; N = 6144, M = 16 / 32 (64-column blocks) 8.05 / 9.64 ->
   // 7.13 / 8.89; N = 14336 / 28672, M = 16 10.84 / 21.11 -> 10.06 / 19.74;
-  // K = 2048, N = 4096, M = 32 5.28 -> 4.81.  Not taken: M = 4 (1.6-4.4 %
-  // slower: a few rows gain nothing from whole lines and pay the LDS round
-  // trip), M = 8 and 8-row groups (-7 .. +2 %), 4 waves (K <= 1024: M = 16
-  // 8 % slower, M = 32 a tie).
-  const bool xs = MT == 1 && rpg >= 16 && a.M >= 16;
+  // K = 2048, N = 4096, M = 32 5.28 -> 4.81; M = 9 / 12 / 15 on the whole
+  // 16-row tile, K = 4096, N = 6144: 6.90 / 7.41 / 7.86 -> 6.65 / 6.83 / 7.06
+  // (G = 32: 7.72 / 8.38 / 9.17 -> 7.06 / 7.26 / 7.58).  Not taken: M = 4
+  // (1.6-4.4 % slower: a few rows gain nothing from whole lines and pay the
+  // LDS round trip), M = 8 and 8-row groups (-7 .. +2 %), 4 waves (K <= 1024:
+  // M = 16 8 % slower, M = 32 a tie).
+  const bool xs = MT == 1 && rpg >= 16 && a.M >= 9;
   using Kernel = decltype(&skinny_kernel<MT, GSTEP, 4, NT, true, AZ, false>);
   constexpr int w16 = k16 ? k16 : 4;
   const Kernel k =
